@@ -1,0 +1,254 @@
+/* Deterministic fp32 arithmetic shared, as the same source, by the HIP kernels and
+ * by the CPU build (the C oracle, the host side of the library).
+ *
+ * Every function here is a fixed sequence of IEEE-754 binary32 operations that
+ * are correctly rounded on both targets (add, sub, mul, true division, fused
+ * multiply-add) plus integer work, so a CPU and a gfx950 GPU produce the same
+ * bits.  Callers must compile with floating-point contraction off
+ * (-ffp-contract=off): a fused a*b+c where the source says two operations
+ * would change the rounding.
+ *
+ * The sampler of SeungheonOh/drama3-mlx (src/sampling.c:123-139) uses Apple's
+ * metal::precise::exp, metal::fast::exp and metal::precise::log; their bit
+ * patterns are unpublished, so exp and log are written here from published
+ * methods instead:
+ *   - d3s_expf: Cody & Waite argument reduction a = n*ln2 + r (Cody & Waite,
+ *     "Software Manual for the Elementary Functions", 1980) with a two-part ln2,
+ *     then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2 (truncation
+ *     error < 6e-9 relative), then exact scaling by 2^n.
+ *   - d3s_logf: y = 2^e * m with m in [sqrt(2)/2, sqrt(2)), s = (m-1)/(m+1),
+ *     log(m) = 2*atanh(s) = 2s + 2s^3/3 + ... + 2s^9/9 (|s| <= 0.1716, truncation
+ *     error < 3e-9 relative), log(y) = e*ln2 + log(m) with the two-part ln2.
+ * Both are checked against double-precision libm over dense sweeps by the
+ * tests (error <= 2 ulp), on the CPU and, bit for bit, on the GPU.
+ */
+#ifndef D3S_MATH_H
+#define D3S_MATH_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define D3S_HD __host__ __device__ __forceinline__
+#define D3S_FMAF __builtin_fmaf
+#else
+#include <math.h>
+#include <string.h>
+#define D3S_HD static inline
+#define D3S_FMAF fmaf
+#endif
+
+#ifdef __cplusplus
+#define D3S_INF (__builtin_inff())
+#define D3S_NAN (__builtin_nanf(""))
+#else
+#define D3S_INF (__builtin_inff())
+#define D3S_NAN (__builtin_nanf(""))
+#endif
+
+D3S_HD uint32_t d3s_f2u(float f) {
+#if defined(__HIPCC__)
+  return __builtin_bit_cast(uint32_t, f);
+#else
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+#endif
+}
+
+D3S_HD float d3s_u2f(uint32_t u) {
+#if defined(__HIPCC__)
+  return __builtin_bit_cast(float, u);
+#else
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+#endif
+}
+
+/* bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 bits. */
+D3S_HD float d3s_bf16_to_f32(uint16_t b) { return d3s_u2f((uint32_t)b << 16); }
+
+/* Order-preserving key: a > b (as floats, NaN excluded) iff key(a) > key(b).
+ * -0 and +0 compare equal, so -0 is mapped to the key of +0. */
+D3S_HD uint32_t d3s_ordkey(float f) {
+  uint32_t b = d3s_f2u(f);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+D3S_HD float d3s_from_ordkey(uint32_t k) {
+  return d3s_u2f((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+D3S_HD int d3s_isnan(float f) { return (d3s_f2u(f) & 0x7fffffffu) > 0x7f800000u; }
+
+/* e^a, correctly handling NaN, +-inf, overflow and subnormal results. */
+D3S_HD float d3s_expf(float a) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  if (d3s_isnan(a)) return a;
+  if (a > 0x1.62e430p+6f) return D3S_INF;  /* > 88.7228394: overflows */
+  if (a < -0x1.a0p+6f) return 0.0f;        /* < -104: below half the least subnormal */
+  const float t = a * 0x1.715476p+0f;      /* a * log2(e) */
+  /* round to nearest even: exact for |t| < 2^22 */
+  const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
+  float r = D3S_FMAF(n, -0x1.62e400p-1f, a);  /* a - n*ln2_hi (exact) */
+  r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);       /* - n*ln2_lo */
+  float p = 0x1.a01a02p-13f;                  /* 1/7! */
+  p = D3S_FMAF(p, r, 0x1.6c16c2p-10f);        /* 1/6! */
+  p = D3S_FMAF(p, r, 0x1.111112p-7f);         /* 1/5! */
+  p = D3S_FMAF(p, r, 0x1.555556p-5f);         /* 1/4! */
+  p = D3S_FMAF(p, r, 0x1.555556p-3f);         /* 1/3! */
+  p = D3S_FMAF(p, r, 0x1.0p-1f);              /* 1/2! */
+  p = D3S_FMAF(p, r, 1.0f);
+  p = D3S_FMAF(p, r, 1.0f);
+  int ni = (int)n; /* -150 <= ni <= 128 */
+  /* p * 2^ni with one rounding: the first product is exact, the second rounds
+   * into the subnormal range (or overflows) when it has to. */
+  float s2 = 1.0f;
+  if (ni < -126) {
+    ni += 127;
+    s2 = 0x1.0p-127f;
+  } else if (ni > 127) {
+    ni -= 1;
+    s2 = 2.0f;
+  }
+  const float s1 = d3s_u2f((uint32_t)(ni + 127) << 23);
+  return (p * s1) * s2;
+}
+
+/* natural log, correctly handling NaN, negative, zero, subnormal and +inf. */
+D3S_HD float d3s_logf(float y) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  if (d3s_isnan(y)) return y;
+  if (y < 0.0f) return D3S_NAN;
+  if (y == 0.0f) return -D3S_INF;
+  if (y == D3S_INF) return y;
+  uint32_t b = d3s_f2u(y);
+  int e = 0;
+  if (b < 0x00800000u) { /* subnormal: scale into the normal range */
+    b = d3s_f2u(y * 0x1.0p+23f);
+    e = -23;
+  }
+  e += (int)(b >> 23) - 127;
+  float m = d3s_u2f((b & 0x007fffffu) | 0x3f800000u); /* [1, 2) */
+  if (m > 0x1.6a09e6p+0f) {                           /* > sqrt(2) */
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float f = m - 1.0f; /* exact */
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  /* 2*atanh(s) = 2s + s*z*(2/3 + 2z/5 + ...), and 2s = f - s*f exactly in
+   * real arithmetic, so log(1+f) = f - s*(f - R) with R = z*(2/3 + 2z/5 + ...):
+   * the exact f carries the result and the rounding of s only touches the
+   * small correction term. */
+  float q = 0x1.c71c72p-3f;          /* 2/9 */
+  q = D3S_FMAF(q, z, 0x1.24924ap-2f); /* 2/7 */
+  q = D3S_FMAF(q, z, 0x1.99999ap-2f); /* 2/5 */
+  q = D3S_FMAF(q, z, 0x1.555556p-1f); /* 2/3 */
+  const float R = z * q;
+  const float lm = D3S_FMAF(-s, f - R, f);
+  const float ef = (float)e;
+  float res = D3S_FMAF(ef, 0x1.7f7d1cp-20f, lm); /* + e*ln2_lo */
+  res = D3S_FMAF(ef, 0x1.62e400p-1f, res);       /* + e*ln2_hi */
+  return res;
+}
+
+/* Fixed-point image of a probability-like term e in [0, 1]: floor(e * 2^40).
+ * Sums of these are exact in uint64 (up to 2^23 terms), so a sum does not
+ * depend on the order the terms are added in. */
+#define D3S_FIX_BITS 40
+D3S_HD uint64_t d3s_fix40(float e) {
+  if (!(e > 0.0f)) return 0; /* 0, -0, negative, NaN */
+  if (e >= 1.0f) return (uint64_t)1 << D3S_FIX_BITS;
+  const uint32_t b = d3s_f2u(e);
+  const uint32_t E = b >> 23;
+  const uint64_t m = (uint64_t)((b & 0x007fffffu) | (E ? 0x00800000u : 0u));
+  /* e = m * 2^(max(E,1) - 150), so e * 2^40 = m * 2^(max(E,1) - 110); E <= 126 */
+  const int sh = 110 - (int)(E ? E : 1u);
+  if (sh <= 0) return m << (-sh); /* at most 16: fits in 40 bits */
+  return sh >= 64 ? 0 : (m >> sh);
+}
+
+/* uint64 -> fp32, round to nearest, ties to even (integer steps only). */
+D3S_HD float d3s_u64_to_f32(uint64_t v) {
+  if (v == 0) return 0.0f;
+  int lz = 0;
+  {
+    uint64_t t = v;
+    if (!(t >> 32)) { lz += 32; t <<= 32; }
+    if (!(t >> 48)) { lz += 16; t <<= 16; }
+    if (!(t >> 56)) { lz += 8; t <<= 8; }
+    if (!(t >> 60)) { lz += 4; t <<= 4; }
+    if (!(t >> 62)) { lz += 2; t <<= 2; }
+    if (!(t >> 63)) { lz += 1; }
+  }
+  const int msb = 63 - lz;
+  if (msb < 24) return d3s_u2f(((uint32_t)(127 + msb) << 23) | (((uint32_t)v << (23 - msb)) & 0x7fffffu));
+  const int sh = msb - 23;
+  uint64_t mant = v >> sh;
+  const uint64_t rem = v & ((((uint64_t)1) << sh) - 1);
+  const uint64_t half = ((uint64_t)1) << (sh - 1);
+  int ex = msb;
+  if (rem > half || (rem == half && (mant & 1))) {
+    mant += 1;
+    if (mant >> 24) {
+      mant >>= 1;
+      ex += 1;
+    }
+  }
+  return d3s_u2f(((uint32_t)(127 + ex) << 23) | ((uint32_t)mant & 0x7fffffu));
+}
+
+/* fixed-point sum (scale 2^40) -> fp32, round to nearest */
+D3S_HD float d3s_fixsum_to_f32(uint64_t s) { return d3s_u64_to_f32(s) * 0x1.0p-40f; }
+
+/* ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ---- */
+typedef struct {
+  uint32_t v[4];
+} d3s_u32x4;
+
+D3S_HD void d3s_mulhilo(uint32_t a, uint32_t b, uint32_t *hi, uint32_t *lo) {
+  const uint64_t p = (uint64_t)a * (uint64_t)b;
+  *hi = (uint32_t)(p >> 32);
+  *lo = (uint32_t)p;
+}
+
+D3S_HD d3s_u32x4 d3s_philox4x32_10(d3s_u32x4 c, uint32_t k0, uint32_t k1) {
+  for (int i = 0; i < 10; i++) {
+    uint32_t hi0, lo0, hi1, lo1;
+    d3s_mulhilo(0xD2511F53u, c.v[0], &hi0, &lo0);
+    d3s_mulhilo(0xCD9E8D57u, c.v[2], &hi1, &lo1);
+    d3s_u32x4 n;
+    n.v[0] = hi1 ^ c.v[1] ^ k0;
+    n.v[1] = lo1;
+    n.v[2] = hi0 ^ c.v[3] ^ k1;
+    n.v[3] = lo0;
+    c = n;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+/* The uniform draw number `index` of draw call `stream` under `seed`:
+ * counter (index/4, stream), key seed, word index%4, 24 random bits.
+ * Values are multiples of 2^-24 in [0, 1), exact in fp32. */
+D3S_HD float d3s_uniform(uint64_t seed, uint64_t stream, uint64_t index) {
+  d3s_u32x4 c;
+  const uint64_t q = index >> 2;
+  c.v[0] = (uint32_t)q;
+  c.v[1] = (uint32_t)(q >> 32);
+  c.v[2] = (uint32_t)stream;
+  c.v[3] = (uint32_t)(stream >> 32);
+  const d3s_u32x4 o = d3s_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+  const uint32_t w = o.v[index & 3];
+  return (float)(w >> 8) * 0x1.0p-24f;
+}
+
+#endif /* D3S_MATH_H */

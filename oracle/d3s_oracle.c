@@ -1,0 +1,273 @@
+/* CPU oracle for the drama3-mlx token sampler.  TEST INFRASTRUCTURE ONLY (see
+ * d3s_oracle.h): a plain-C restatement of src/sampling.c used as the parity
+ * checker and as the CPU baseline, never by the product path. */
+#include "d3s_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../drama3-mlx_amd/csrc/d3s_math.h"
+
+#define KERNEL_MAX_K 64 /* src/sampling.c:17: the kernel's order applies up to here */
+#define MIN_TEMPERATURE 1e-5f /* src/sampling.c:16 */
+
+typedef struct {
+  float x;
+  int32_t i;
+} Cand;
+
+/* a ranks before b: larger x first, then the lower index (src/sampling.c:7-8) */
+static inline int beats(float xa, int32_t ia, float xb, int32_t ib) {
+  return xa > xb || (xa == xb && ia < ib);
+}
+
+static int cmp_rank(const void *pa, const void *pb) {
+  const Cand *a = pa, *b = pb;
+  if (beats(a->x, a->i, b->x, b->i)) return -1;
+  if (beats(b->x, b->i, a->x, a->i)) return 1;
+  return 0;
+}
+
+/* min-heap on rank order: the root is the worst kept candidate */
+static void heap_sift_down(Cand *h, int n, int at) {
+  for (;;) {
+    int l = 2 * at + 1, r = l + 1, w = at;
+    if (l < n && beats(h[w].x, h[w].i, h[l].x, h[l].i)) w = l;
+    if (r < n && beats(h[w].x, h[w].i, h[r].x, h[r].i)) w = r;
+    if (w == at) return;
+    Cand t = h[w];
+    h[w] = h[at];
+    h[at] = t;
+    at = w;
+  }
+}
+
+/* top k of x[0..V) in rank order (x desc, index asc), src/sampling.c:27-36 / :90-121 */
+static void top_k_ranked(const float *x, int64_t V, int k, Cand *out, Cand *scratch) {
+  if ((int64_t)k * 8 >= V) {
+    for (int64_t i = 0; i < V; i++) {
+      scratch[i].x = x[i];
+      scratch[i].i = (int32_t)i;
+    }
+    qsort(scratch, (size_t)V, sizeof(Cand), cmp_rank);
+    memcpy(out, scratch, (size_t)k * sizeof(Cand));
+    return;
+  }
+  Cand *h = scratch;
+  int n = 0;
+  for (int64_t i = 0; i < V; i++) {
+    const float xi = x[i];
+    if (n < k) {
+      h[n].x = xi;
+      h[n].i = (int32_t)i;
+      n++;
+      if (n == k)
+        for (int a = k / 2 - 1; a >= 0; a--) heap_sift_down(h, k, a);
+    } else if (xi > h[0].x) { /* an equal x with a larger index never wins */
+      h[0].x = xi;
+      h[0].i = (int32_t)i;
+      heap_sift_down(h, k, 0);
+    }
+  }
+  memcpy(out, h, (size_t)k * sizeof(Cand));
+  qsort(out, (size_t)k, sizeof(Cand), cmp_rank);
+}
+
+static void sample_row(const float *L, int64_t V, int k, const float *u, float T, float top_p,
+                       int32_t *id_out, float *probs, int32_t *cand, float *lse_out,
+                       uint8_t *flags_out, double *gaps, float *x, Cand *top, Cand *scratch,
+                       int *drop, float *score) {
+  uint8_t flags = 0;
+  if (T < MIN_TEMPERATURE) T = MIN_TEMPERATURE; /* src/sampling.c:195 */
+  float m = -D3S_INF;
+  int bad = 0;
+  for (int64_t i = 0; i < V; i++) {
+    const float xi = L[i] / T; /* src/sampling.c:25 / :70 */
+    x[i] = xi;
+    if (d3s_isnan(xi) || xi == D3S_INF) bad = 1;
+    if (xi > m) m = xi;
+  }
+  if (gaps) gaps[0] = gaps[1] = INFINITY;
+  if (bad) {
+    *id_out = -1;
+    if (probs)
+      for (int r = 0; r < k; r++) probs[r] = D3S_NAN;
+    if (cand)
+      for (int r = 0; r < k; r++) cand[r] = -1;
+    if (lse_out) *lse_out = D3S_NAN;
+    if (flags_out) *flags_out = D3S_ORACLE_BAD;
+    return;
+  }
+  if (m == -D3S_INF) {
+    /* every x is -inf: the reference kernel ranks the lowest ids first, every
+     * later quantity is NaN and the argmax keeps its initial choice 0 */
+    *id_out = 0;
+    if (probs)
+      for (int r = 0; r < k; r++) probs[r] = D3S_NAN;
+    if (cand)
+      for (int r = 0; r < k; r++) cand[r] = r;
+    if (lse_out) *lse_out = D3S_NAN;
+    if (flags_out) *flags_out = D3S_ORACLE_ALL_MASKED;
+    return;
+  }
+  /* lse: exact fixed-point sum of the fp32 terms, src/sampling.c:37-38 / :81-89 */
+  uint64_t S = 0;
+  for (int64_t i = 0; i < V; i++) S += d3s_fix40(d3s_expf(x[i] - m));
+  const float lse = m + d3s_logf(d3s_fixsum_to_f32(S));
+
+  top_k_ranked(x, V, k, top, scratch);
+
+  const float v0 = top[0].x;
+  int cut = k;
+  float inv;
+  if (k <= KERNEL_MAX_K) {
+    /* the reference kernel's order, src/sampling.c:123-131 */
+    float cum = 0.0f, sum = 0.0f;
+    for (int r = 0; r < k; r++) {
+      cum = cum + d3s_expf(top[r].x - lse);
+      drop[r] = r > 0 && cum > top_p;
+      if (!drop[r]) sum = sum + d3s_expf(top[r].x - v0);
+    }
+    inv = 1.0f / sum;
+  } else {
+    /* op graph (src/sampling.c:39-44): exact prefix sums, rounded once */
+    uint64_t P = 0, Ssum = 0;
+    for (int r = 0; r < k; r++) {
+      P += d3s_fix40(d3s_expf(top[r].x - lse));
+      drop[r] = r > 0 && d3s_fixsum_to_f32(P) > top_p;
+      if (!drop[r]) Ssum += d3s_fix40(d3s_expf(top[r].x - v0));
+    }
+    inv = 1.0f / d3s_fixsum_to_f32(Ssum);
+  }
+  for (int r = 0; r < k; r++)
+    if (drop[r]) {
+      cut = r;
+      break;
+    }
+  /* exponential race, src/sampling.c:132-139 / :45-48 */
+  float best = -1.0f;
+  int choice = 0;
+  for (int r = 0; r < k; r++) {
+    const float p = drop[r] ? 0.0f : d3s_expf(top[r].x - v0) * inv;
+    const float noise = -d3s_logf(1.0f - u[r]);
+    const float s = p / noise;
+    score[r] = s;
+    if (probs) probs[r] = p;
+    if (cand) cand[r] = top[r].i;
+    if (s > best) {
+      best = s;
+      choice = r;
+    }
+  }
+  *id_out = top[choice].i;
+  if (lse_out) *lse_out = lse;
+
+  /* float64 shadow, for classifying rows where accumulation order could matter */
+  double s64 = 0.0;
+  for (int64_t i = 0; i < V; i++) s64 += exp((double)x[i] - (double)m);
+  const double lse64 = (double)m + log(s64);
+  double c64 = 0.0, min_gap = INFINITY;
+  for (int r = 0; r < k; r++) {
+    c64 += exp((double)top[r].x - lse64);
+    if (r >= 1) {
+      const double g = fabs(c64 - (double)top_p);
+      if (g < min_gap) min_gap = g;
+    }
+  }
+  if (min_gap < 1e-6) flags |= D3S_ORACLE_TOPP_EDGE;
+  double kept64 = 0.0;
+  for (int r = 0; r < cut; r++) kept64 += exp((double)top[r].x - (double)v0);
+  double b1 = -1.0, b2 = -1.0;
+  for (int r = 0; r < k; r++) {
+    const float noise32 = -d3s_logf(1.0f - u[r]);
+    if (!(noise32 > 0.0f)) continue; /* -0 or NaN noise: no race score */
+    const double p64 = r < cut ? exp((double)top[r].x - (double)v0) / kept64 : 0.0;
+    const double s = p64 / -log1p(-(double)u[r]);
+    if (s > b1) {
+      b2 = b1;
+      b1 = s;
+    } else if (s > b2) {
+      b2 = s;
+    }
+  }
+  const double race_gap = (b1 > 0.0 && b2 >= 0.0) ? (b1 - b2) / b1 : INFINITY;
+  if (race_gap < 1e-6) flags |= D3S_ORACLE_RACE_EDGE;
+  if (gaps) {
+    gaps[0] = min_gap;
+    gaps[1] = race_gap;
+  }
+  if (flags_out) *flags_out = flags;
+}
+
+int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
+                      int64_t row_stride, const float *u, int k, const float *temperature,
+                      const float *top_p, float temperature_scalar, float top_p_scalar,
+                      const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
+                      float *lse, uint8_t *flags, double *gaps, int n_threads) {
+  if (n_rows < 0 || vocab < 1 || row_stride < vocab || k < 1 || k > vocab || !ids ||
+      (n_rows > 0 && (!logits || !u)) || (dtype != D3S_ORACLE_DTYPE_F32 && dtype != D3S_ORACLE_DTYPE_BF16))
+    return -1;
+  if (n_threads < 1) n_threads = 1;
+  int failed = 0;
+#pragma omp parallel num_threads(n_threads)
+  {
+    float *L = malloc((size_t)vocab * sizeof(float));
+    float *x = malloc((size_t)vocab * sizeof(float));
+    Cand *top = malloc((size_t)k * sizeof(Cand));
+    Cand *scratch = malloc((size_t)vocab * sizeof(Cand));
+    int *drop = malloc((size_t)k * sizeof(int));
+    float *score = malloc((size_t)k * sizeof(float));
+    if (!L || !x || !top || !scratch || !drop || !score) {
+#pragma omp atomic write
+      failed = 1;
+    } else {
+#pragma omp for schedule(dynamic, 4)
+      for (int64_t row = 0; row < n_rows; row++) {
+        if (dtype == D3S_ORACLE_DTYPE_F32) {
+          memcpy(L, (const float *)logits + row * row_stride, (size_t)vocab * sizeof(float));
+        } else {
+          const uint16_t *b = (const uint16_t *)logits + row * row_stride;
+          for (int64_t i = 0; i < vocab; i++) L[i] = d3s_bf16_to_f32(b[i]);
+        }
+        if (banned && banned[row] >= 0 && banned[row] < vocab) L[banned[row]] = -D3S_INF;
+        sample_row(L, vocab, k, u + row * (int64_t)k, temperature ? temperature[row] : temperature_scalar,
+                   top_p ? top_p[row] : top_p_scalar, ids + row, probs ? probs + row * (int64_t)k : NULL,
+                   cand ? cand + row * (int64_t)k : NULL, lse ? lse + row : NULL,
+                   flags ? flags + row : NULL, gaps ? gaps + 2 * row : NULL, x, top, scratch, drop, score);
+      }
+    }
+    free(L);
+    free(x);
+    free(top);
+    free(scratch);
+    free(drop);
+    free(score);
+  }
+  return failed ? -1 : 0;
+}
+
+void d3s_oracle_expf(const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_expf(in[i]);
+}
+
+void d3s_oracle_logf(const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_logf(in[i]);
+}
+
+void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40(in[i]);
+}
+
+float d3s_oracle_u64_to_f32(uint64_t v) { return d3s_u64_to_f32(v); }
+
+void d3s_oracle_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  d3s_u32x4 c = {{ctr[0], ctr[1], ctr[2], ctr[3]}};
+  d3s_u32x4 o = d3s_philox4x32_10(c, key[0], key[1]);
+  memcpy(out, o.v, sizeof(o.v));
+}
+
+void d3s_oracle_uniform(uint64_t seed, uint64_t stream0, int64_t rows, int64_t k, float *u) {
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t j = 0; j < k; j++) u[r * k + j] = d3s_uniform(seed, stream0 + (uint64_t)r, (uint64_t)j);
+}

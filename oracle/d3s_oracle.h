@@ -1,0 +1,78 @@
+/* CPU oracle for the token sampler of SeungheonOh/drama3-mlx (src/sampling.c).
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * or as the timed CPU baseline.  The product (the HIP library under
+ * drama3-mlx_amd/) never links, loads or falls back to it.
+ *
+ * Semantics restated (per row; k = number of uniform columns = min(top_k, V)):
+ *   T <- max(T, 1e-5)                                  src/sampling.c:16,195
+ *   x_i = f32(logit_i) / T                             src/sampling.c:25,70
+ *   m = max x; lse = m + log(sum_i exp(x_i - m))       src/sampling.c:37-38,67-89
+ *   rank by (x desc, index asc), keep the first k      src/sampling.c:27-36,90-121
+ *   c_r = cumulative of exp(v_r - lse) in rank order   src/sampling.c:39,126-127
+ *   drop_r = r > 0 and c_r > top_p                     src/sampling.c:40-42,128
+ *   p_r = kept ? exp(v_r - v_0) / sum_kept : 0         src/sampling.c:43-44,129-134
+ *   noise_r = -log(1 - u_r); score_r = p_r / noise_r   src/sampling.c:45-47,135-136
+ *   choice = first r with the greatest score (> -1)    src/sampling.c:132-138
+ *   id = index of rank `choice`                         src/sampling.c:48,139
+ *
+ * Floating-point order (the parts the reference leaves to its hardware):
+ *   - exp and log are d3s_expf / d3s_logf (drama3-mlx_amd/csrc/d3s_math.h);
+ *   - the row sum inside lse is the exact fixed-point sum (2^-40 units) of the
+ *     fp32 terms exp(x_i - m), rounded once to fp32: order independent;
+ *   - k <= 64: c_r and sum_kept are sequential fp32 sums in rank order and
+ *     p_r = e_r * (1/sum_kept), the operation order of the reference kernel
+ *     (src/sampling.c:123-139);
+ *   - k > 64 (the reference's op graph, src/sampling.c:22-49, whose MLX scan
+ *     and softmax order is unpublished): c_r and sum_kept are exact fixed-point
+ *     prefix sums rounded to fp32, p_r = e_r * (1/sum_kept).
+ * Rows whose logits (after the optional banned index) give a NaN or +inf x are
+ * refused: id -1 (the reference's caller refuses them, src/generate.c:92,130).
+ * A row whose x are all -inf returns index 0, as the reference kernel does.
+ */
+#ifndef D3S_ORACLE_H
+#define D3S_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D3S_ORACLE_DTYPE_F32 0
+#define D3S_ORACLE_DTYPE_BF16 1
+
+/* flags per row */
+#define D3S_ORACLE_BAD 1          /* non-finite x: refused, id -1 */
+#define D3S_ORACLE_TOPP_EDGE 2    /* some r in [1,k) has |c64_r - top_p| < 1e-6 */
+#define D3S_ORACLE_RACE_EDGE 4    /* top two race scores within 1e-6 relative */
+#define D3S_ORACLE_ALL_MASKED 8   /* every x is -inf */
+
+/* logits: [n_rows, row_stride] of fp32 or bf16 (uint16 bits); u: [n_rows, k].
+ * temperature / top_p: per-row arrays, or NULL to use the scalars.
+ * banned: per-row index set to -inf before sampling (<0 or >= vocab: none), or NULL.
+ * Outputs (each may be NULL except ids): ids [n_rows]; probs, cand [n_rows, k]
+ * (post-filter probability and index by rank); lse [n_rows]; flags [n_rows];
+ * gaps [n_rows, 2] = (min_r |c64_r - top_p|, relative gap of the top two scores).
+ * Returns 0, or -1 for bad arguments. */
+int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
+                      int64_t row_stride, const float *u, int k, const float *temperature,
+                      const float *top_p, float temperature_scalar, float top_p_scalar,
+                      const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
+                      float *lse, uint8_t *flags, double *gaps, int n_threads);
+
+/* elementwise d3s_expf / d3s_logf / true division, for the math tests */
+void d3s_oracle_expf(const float *in, float *out, int64_t n);
+void d3s_oracle_logf(const float *in, float *out, int64_t n);
+void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n);
+float d3s_oracle_u64_to_f32(uint64_t v);
+void d3s_oracle_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* u[r, j] = d3s_uniform(seed, stream0 + r, j) for r < rows, j < k */
+void d3s_oracle_uniform(uint64_t seed, uint64_t stream0, int64_t rows, int64_t k, float *u);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

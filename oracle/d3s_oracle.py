@@ -1,0 +1,137 @@
+"""ctypes binding of the CPU oracle (oracle/libd3s_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
+product path (drama3-mlx_amd/) never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libd3s_oracle.so")
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+BAD = 1
+TOPP_EDGE = 2
+RACE_EDGE = 4
+ALL_MASKED = 8
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+        L.d3s_oracle_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp,
+                                        vp, vp, vp, vp, vp, i32]
+        L.d3s_oracle_sample.restype = i32
+        for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40"):
+            getattr(L, name).argtypes = [vp, vp, i64]
+            getattr(L, name).restype = None
+        L.d3s_oracle_u64_to_f32.argtypes = [ctypes.c_uint64]
+        L.d3s_oracle_u64_to_f32.restype = f32
+        L.d3s_oracle_philox.argtypes = [vp, vp, vp]
+        L.d3s_oracle_philox.restype = None
+        L.d3s_oracle_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, i64, i64, vp]
+        L.d3s_oracle_uniform.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=None, vocab=None):
+    """Oracle sampling.  logits: float32 [N, >=V] or uint16 (bf16 bits) [N, >=V];
+    u: float32 [N, k]; temperature / top_p: scalars or float32 [N] arrays.
+    Returns dict(ids, probs, cand, lse, flags, gaps)."""
+    logits = np.ascontiguousarray(logits)
+    if logits.dtype == np.float32:
+        dtype = DTYPE_F32
+    elif logits.dtype == np.uint16:
+        dtype = DTYPE_BF16
+    else:
+        raise TypeError("logits must be float32 or uint16 (bf16 bits)")
+    N = logits.shape[0]
+    stride = logits.shape[1] if row_stride is None else row_stride
+    V = stride if vocab is None else vocab
+    u = np.ascontiguousarray(u, np.float32)
+    k = u.shape[1]
+    t_arr = t_s = None
+    if np.ndim(temperature):
+        t_arr = np.ascontiguousarray(temperature, np.float32)
+        t_s = 0.0
+    else:
+        t_s = float(temperature)
+    p_arr = p_s = None
+    if np.ndim(top_p):
+        p_arr = np.ascontiguousarray(top_p, np.float32)
+        p_s = 0.0
+    else:
+        p_s = float(top_p)
+    ban = None if banned is None else np.ascontiguousarray(banned, np.int32)
+    ids = np.empty(N, np.int32)
+    probs = np.empty((N, k), np.float32)
+    cand = np.empty((N, k), np.int32)
+    lse = np.empty(N, np.float32)
+    flags = np.empty(N, np.uint8)
+    gaps = np.empty((N, 2), np.float64)
+    rc = lib().d3s_oracle_sample(_p(logits), dtype, N, V, stride, _p(u), k, _p(t_arr), _p(p_arr), t_s,
+                                 p_s, _p(ban), _p(ids), _p(probs), _p(cand), _p(lse), _p(flags),
+                                 _p(gaps), n_threads)
+    if rc != 0:
+        raise ValueError("oracle rejected the arguments")
+    return dict(ids=ids, probs=probs, cand=cand, lse=lse, flags=flags, gaps=gaps)
+
+
+def expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().d3s_oracle_expf(_p(x), _p(out), x.size)
+    return out
+
+
+def logf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().d3s_oracle_logf(_p(x), _p(out), x.size)
+    return out
+
+
+def fix40(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint64)
+    lib().d3s_oracle_fix40(_p(x), _p(out), x.size)
+    return out
+
+
+def u64_to_f32(v):
+    return lib().d3s_oracle_u64_to_f32(int(v))
+
+
+def philox(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().d3s_oracle_philox(_p(c), _p(k), _p(out))
+    return out
+
+
+def uniform(seed, stream0, rows, k):
+    """u[r, j] = uniform draw j of stream (stream0 + r) under seed."""
+    u = np.empty((rows, k), np.float32)
+    lib().d3s_oracle_uniform(seed, stream0, rows, k, _p(u))
+    return u
