@@ -1,0 +1,94 @@
+/* C-ABI of the MI355X token sampler (include/d3s_sampler.h): argument checks
+ * and routing between the fused and the streaming kernel.
+ *
+ * Routing mirrors sample_with_noise (src/sampling.c:194-203): the one-kernel
+ * path when k <= 64 and the row fits it, unless D3_NO_FUSED_SAMPLER is set in
+ * the environment (read once per process) or D3S_FLAG_GENERIC is passed.  The
+ * reference also requires k < V for its kernel; here both kernels compute the
+ * same definition, so k == V <= 64 stays on the fused kernel. */
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/d3s_sampler.h"
+#include "d3s_internal.h"
+
+namespace {
+
+bool env_no_fused() {
+  static const bool v = [] {
+    const char *e = getenv("D3_NO_FUSED_SAMPLER");
+    return e != nullptr && *e != '\0';
+  }();
+  return v;
+}
+
+int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+               const float *u, int k, const float *temperature, const float *top_p,
+               float temperature_scalar, float top_p_scalar, const int32_t *banned,
+               int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+               void *stream) {
+  if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;
+  if (n_rows < 0 || n_rows > 0x7fffffff || vocab < 1 || vocab > (1 << 26) ||
+      row_stride < vocab || k < 1 || k > vocab)
+    return D3S_ERR_ARG;
+  if (k > d3s::generic_max_k()) return D3S_ERR_UNSUPPORTED;
+  if (n_rows == 0) return D3S_OK;
+  if (!logits || !u || !ids) return D3S_ERR_ARG;
+  /* rows are addressed in whole elements */
+  if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
+  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT)) != 0u)
+    return D3S_ERR_ARG;
+  d3s::SampleArgs a;
+  a.logits = logits;
+  a.row_stride = row_stride;
+  a.vocab = (int)vocab;
+  a.k = k;
+  a.n_rows = (int)n_rows;
+  a.u = u;
+  a.temperature = temperature;
+  a.top_p = top_p;
+  a.temperature_scalar = temperature_scalar;
+  a.top_p_scalar = top_p_scalar;
+  a.banned = banned;
+  a.ids = ids;
+  a.probs = probs;
+  a.cand = cand;
+  a.counters = counters;
+  a.flags = flags;
+  const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  const bool generic = (flags & D3S_FLAG_GENERIC) || env_no_fused();
+  if (!generic && d3s::launch_fused(a, dt, s)) return launched();
+  if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
+  return launched();
+}
+
+int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream) {
+  if (n < 0 || (n > 0 && !u)) return D3S_ERR_ARG;
+  d3s::launch_uniform(u, n, seed, draw, (hipStream_t)stream);
+  return n > 0 ? launched() : D3S_OK;
+}
+
+int d3s_max_k(void) { return d3s::generic_max_k(); }
+
+int d3s_fused_max_vocab(int dtype) {
+  if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;
+  return d3s::fused_max_vocab(dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16);
+}
+
+int d3s_math_selftest(const float *in, float *out_exp, float *out_log, float *out_div,
+                      uint64_t *out_fix, int64_t n, float divisor, void *stream) {
+  if (n < 0 || (n > 0 && (!in || !out_exp || !out_log || !out_div || !out_fix))) return D3S_ERR_ARG;
+  d3s::launch_math_selftest(in, out_exp, out_log, out_div, out_fix, n, divisor, (hipStream_t)stream);
+  return n > 0 ? launched() : D3S_OK;
+}
+
+const char *d3s_version(void) { return "d3sampler 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+/* Internal launch interface between the C-ABI layer (d3s_api.hip) and the
+ * kernels (d3s_kernels.hip).  Not installed; the public ABI is include/. */
+#ifndef D3S_INTERNAL_H
+#define D3S_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace d3s {
+
+/* every row-independent input of one sampling launch; pointers are device
+ * pointers (or host memory the device can read) */
+struct SampleArgs {
+  const void *logits;       /* [n_rows, row_stride] fp32 or bf16 */
+  int64_t row_stride;       /* in elements */
+  int vocab;                /* V */
+  int k;                    /* uniform columns per row, 1 <= k <= V */
+  int n_rows;
+  const float *u;           /* [n_rows, k] */
+  const float *temperature; /* [n_rows] or null -> temperature_scalar */
+  const float *top_p;       /* [n_rows] or null -> top_p_scalar */
+  float temperature_scalar;
+  float top_p_scalar;
+  const int32_t *banned;    /* [n_rows] index forced to -inf, or null */
+  int32_t *ids;             /* [n_rows] */
+  float *probs;             /* [n_rows, k] or null */
+  int32_t *cand;            /* [n_rows, k] or null */
+  uint32_t *counters;       /* [D3S_NUM_COUNTERS] or null */
+  unsigned flags;
+};
+
+/* counters[] slots (atomic increments per row) */
+enum {
+  CNT_REFUSED = 0,      /* non-finite x: id -1 */
+  CNT_ALL_MASKED = 1,   /* every x -inf */
+  CNT_EXACT_SELECT = 2, /* fused kernel fell back to the radix select */
+  CNT_EXACT_LSE = 3,    /* fused kernel recomputed the exact lse */
+  CNT_NUM = 4
+};
+
+/* flags (same values as the public D3S_FLAG_*) */
+enum : unsigned {
+  FLAG_GENERIC = 1u,
+  FLAG_EXACT_LSE = 2u,
+  FLAG_EXACT_SELECT = 4u,
+};
+
+enum Dtype { DT_F32 = 0, DT_BF16 = 1 };
+
+/* Launch the fused one-workgroup-per-row kernel (k <= 64, V within the
+ * register-resident limit).  Returns false if no instantiation fits. */
+bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);
+/* Largest V the fused kernel accepts for this dtype. */
+int fused_max_vocab(Dtype dt);
+/* Launch the streaming generic kernel (any V, k <= generic_max_k()). */
+bool launch_generic(const SampleArgs &a, Dtype dt, hipStream_t s);
+int generic_max_k();
+/* u[i] = d3s_uniform(seed, stream_id, i), i < n */
+void launch_uniform(float *u, int64_t n, uint64_t seed, uint64_t stream_id, hipStream_t s);
+/* elementwise d3s_expf / d3s_logf / x / divisor / d3s_fix40 for the math self-test */
+void launch_math_selftest(const float *in, float *out_exp, float *out_log, float *out_div,
+                          uint64_t *out_fix, int64_t n, float divisor, hipStream_t s);
+
+}  // namespace d3s
+
+#endif

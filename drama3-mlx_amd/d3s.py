@@ -1,0 +1,160 @@
+"""ctypes binding of libd3sampler.so, the MI355X token sampler.
+
+The host-side counterpart of the reference's ctypes layer for this path
+(tests/d3.py:211-217 binds d3_sample of src/testapi.c:155-166).  It loads the
+in-tree library and fails loudly when it is missing: there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libd3sampler.so")
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+FLAG_GENERIC = 1
+FLAG_EXACT_LSE = 2
+FLAG_EXACT_SELECT = 4
+COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
+NUM_COUNTERS = 4
+OK = 0
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C drama3-mlx_amd` "
+                               "(or __graft_entry__.build()); there is no fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32, f32, u32 = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float,
+                                  ctypes.c_uint)
+        L.d3s_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
+                                 vp, u32, vp]
+        L.d3s_sample.restype = i32
+        L.d3s_uniform_fill.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
+        L.d3s_uniform_fill.restype = i32
+        L.d3s_max_k.argtypes = []
+        L.d3s_max_k.restype = i32
+        L.d3s_fused_max_vocab.argtypes = [i32]
+        L.d3s_fused_max_vocab.restype = i32
+        L.d3s_math_selftest.argtypes = [vp, vp, vp, vp, vp, i64, f32, vp]
+        L.d3s_math_selftest.restype = i32
+        L.d3s_version.argtypes = []
+        L.d3s_version.restype = ctypes.c_char_p
+        L.d3_sample.argtypes = [vp, i32, i32, f32, i32, f32, ctypes.c_ulonglong, vp]
+        L.d3_sample.restype = None
+        L.d3_sample_with_noise.argtypes = [vp, vp, i32, i32, i32, f32, f32, vp]
+        L.d3_sample_with_noise.restype = None
+        _lib = L
+    return _lib
+
+
+def sample_raw(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, banned, ids,
+               probs=None, cand=None, counters=None, flags=0, stream=None):
+    """d3s_sample on device pointers (ints).  temperature / top_p: a float
+    (scalar) or a device pointer wrapped as ("ptr", address)."""
+    t_ptr, t_s = (temperature[1], 0.0) if isinstance(temperature, tuple) else (None, float(temperature))
+    p_ptr, p_s = (top_p[1], 0.0) if isinstance(top_p, tuple) else (None, float(top_p))
+    return lib().d3s_sample(logits, dtype, n_rows, vocab, row_stride, u, k, t_ptr, p_ptr, t_s, p_s,
+                            banned, ids, probs, cand, counters, flags, stream)
+
+
+def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True, row_stride=None,
+           vocab=None, stream=None):
+    """Host arrays in, host arrays out (copies through device memory).
+    logits: float32 or uint16 (bf16 bits) [N, row_stride]; u: float32 [N, k];
+    temperature / top_p: scalars or float32 [N].  Returns dict(ids, probs, cand,
+    counters, rc)."""
+    import hiprt
+    logits = np.ascontiguousarray(logits)
+    dtype = DTYPE_F32 if logits.dtype == np.float32 else DTYPE_BF16
+    if logits.dtype not in (np.float32, np.uint16):
+        raise TypeError("logits must be float32 or uint16 (bf16 bits)")
+    N = logits.shape[0]
+    stride = logits.shape[1] if row_stride is None else row_stride
+    V = stride if vocab is None else vocab
+    u = np.ascontiguousarray(u, np.float32)
+    k = u.shape[1]
+    bufs = dict(logits=hiprt.to_device(logits), u=hiprt.to_device(u),
+                ids=hiprt.DeviceBuffer(4 * N), counters=hiprt.DeviceBuffer(4 * NUM_COUNTERS).zero())
+    if want_probs:
+        bufs["probs"] = hiprt.DeviceBuffer(4 * N * k)
+        bufs["cand"] = hiprt.DeviceBuffer(4 * N * k)
+    T = float(temperature) if not np.ndim(temperature) else None
+    if np.ndim(temperature):
+        bufs["Tbuf"] = hiprt.to_device(np.asarray(temperature, np.float32))
+        T = ("ptr", bufs["Tbuf"].ptr)
+    P = float(top_p) if not np.ndim(top_p) else None
+    if np.ndim(top_p):
+        bufs["Pbuf"] = hiprt.to_device(np.asarray(top_p, np.float32))
+        P = ("ptr", bufs["Pbuf"].ptr)
+    ban = None
+    if banned is not None:
+        bufs["ban"] = hiprt.to_device(np.asarray(banned, np.int32))
+        ban = bufs["ban"].ptr
+    rc = sample_raw(bufs["logits"].ptr, dtype, N, V, stride, bufs["u"].ptr, k, T, P, ban,
+                    bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
+                    bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
+                    stream.ptr if stream else None)
+    out = dict(rc=rc)
+    if rc != OK:
+        return out
+    hiprt.synchronize()
+    out["ids"] = bufs["ids"].download((N,), np.int32)
+    out["counters"] = bufs["counters"].download((NUM_COUNTERS,), np.uint32)
+    if want_probs:
+        out["probs"] = bufs["probs"].download((N, k), np.float32)
+        out["cand"] = bufs["cand"].download((N, k), np.int32)
+    for b in bufs.values():
+        if isinstance(b, hiprt.DeviceBuffer):
+            b.free()
+    return out
+
+
+def uniform_fill(n, seed, draw):
+    import hiprt
+    buf = hiprt.DeviceBuffer(4 * n)
+    rc = lib().d3s_uniform_fill(buf.ptr, n, seed, draw, None)
+    if rc != OK:
+        raise RuntimeError(f"d3s_uniform_fill: {rc}")
+    hiprt.synchronize()
+    return buf.download((n,), np.float32)
+
+
+def math_selftest(x, divisor):
+    import hiprt
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.size
+    bi = hiprt.to_device(x)
+    be, bl, bd, bf = (hiprt.DeviceBuffer(4 * n), hiprt.DeviceBuffer(4 * n), hiprt.DeviceBuffer(4 * n),
+                      hiprt.DeviceBuffer(8 * n))
+    rc = lib().d3s_math_selftest(bi.ptr, be.ptr, bl.ptr, bd.ptr, bf.ptr, n, divisor, None)
+    if rc != OK:
+        raise RuntimeError(f"d3s_math_selftest: {rc}")
+    hiprt.synchronize()
+    return (be.download((n,), np.float32), bl.download((n,), np.float32),
+            bd.download((n,), np.float32), bf.download((n,), np.uint64))
+
+
+def d3_sample(logits, temperature, top_k, top_p, seed):
+    """The reference's test export (src/testapi.c:155-166): host fp32 logits,
+    a seed, host ids."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    out = np.zeros(len(logits), np.int32)
+    lib().d3_sample(logits.ctypes.data, logits.shape[0], logits.shape[1], temperature, top_k, top_p,
+                    seed, out.ctypes.data)
+    return out
+
+
+def d3_sample_with_noise(logits, u, temperature, top_p):
+    logits = np.ascontiguousarray(logits, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.zeros(len(logits), np.int32)
+    lib().d3_sample_with_noise(logits.ctypes.data, u.ctypes.data, logits.shape[0], logits.shape[1],
+                               u.shape[1], temperature, top_p, out.ctypes.data)
+    return out

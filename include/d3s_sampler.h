@@ -1,0 +1,93 @@
+/* MI355X token sampler: raw C-ABI core (libd3sampler.so).
+ *
+ * Replaces the device work behind the sampler of SeungheonOh/drama3-mlx:
+ *   - sample_kernel_call / drama3_sample (src/sampling.c:53-177): fused k <= 64;
+ *   - the compiled op graph sample_fn (src/sampling.c:22-51): any k, any V;
+ *   - the routing of sample_with_noise (src/sampling.c:194-203);
+ *   - m_uniform on the GPU stream inside sample_top_k_top_p (src/sampling.c:208,
+ *     src/mlxu.c:771-774), as d3s_uniform_fill.
+ * Plain pointers and sizes only; every pointer argument is device memory (or
+ * memory the device can read); `stream` is a hipStream_t (NULL: the null stream).
+ * Calls enqueue work and return; nothing here allocates device memory.
+ */
+#ifndef D3S_SAMPLER_H
+#define D3S_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D3S_DTYPE_F32 0  /* fp32 logits */
+#define D3S_DTYPE_BF16 1 /* bf16 logits (uint16 bit patterns) */
+
+/* status codes */
+#define D3S_OK 0
+#define D3S_ERR_ARG -1         /* shape, pointer or parameter out of range */
+#define D3S_ERR_UNSUPPORTED -2 /* k beyond d3s_max_k() */
+#define D3S_ERR_LAUNCH -3      /* the HIP launch failed */
+#define D3S_ERR_DTYPE -4       /* unknown logits dtype */
+
+/* flags for d3s_sample */
+#define D3S_FLAG_GENERIC 1u     /* always the streaming kernel (the reference's
+                                   D3_NO_FUSED_SAMPLER switch, src/sampling.c:197) */
+#define D3S_FLAG_EXACT_LSE 2u   /* fused kernel: always the exact log-sum-exp */
+#define D3S_FLAG_EXACT_SELECT 4u /* fused kernel: always the radix select */
+
+/* counters[] slots, when a counters array is given (atomic per-row increments) */
+#define D3S_COUNTER_REFUSED 0      /* rows with a NaN / +inf x: id -1 */
+#define D3S_COUNTER_ALL_MASKED 1   /* rows whose x are all -inf: id 0 */
+#define D3S_COUNTER_EXACT_SELECT 2 /* fused rows that took the radix select */
+#define D3S_COUNTER_EXACT_LSE 3    /* fused rows that computed the exact log-sum-exp */
+#define D3S_NUM_COUNTERS 4
+
+/* One sampled index per row of logits [n_rows, vocab] (row r at
+ * logits + r * row_stride elements), with the uniform draws u [n_rows, k]
+ * (k = min(top_k, vocab), as the reference derives it, src/sampling.c:186,207).
+ *
+ * Per row (src/sampling.c:1-3,:22-49,:53-140): T = max(temperature, 1e-5);
+ * x = logit / T; ranks by (x desc, index asc); c_r = sum_{j<=r} exp(x_j - lse);
+ * ranks r > 0 with c_r > top_p are dropped; p_r = softmax over the kept ranks;
+ * ids[row] = index of argmax_r p_r / -log(1 - u_r) (first maximum).
+ *
+ * temperature, top_p: per-row device arrays [n_rows], or NULL to use the
+ * scalars.  banned: per-row index set to -inf first (any value outside
+ * [0, vocab) = none), or NULL.  probs, cand: optional [n_rows, k] outputs, the
+ * post-filter probability and the index of each rank.  counters: optional
+ * [D3S_NUM_COUNTERS] uint32 device array that the call increments.
+ * A row with a NaN or +inf x is refused: ids = -1, cand = -1, probs = NaN.
+ * A row whose x are all -inf gets ids = 0 (the reference kernel's answer).
+ * The result is identical for every flag combination.
+ * Replaces: sample_with_noise (src/sampling.c:194-203, declared src/model.h:175-176). */
+int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+               const float *u, int k, const float *temperature, const float *top_p,
+               float temperature_scalar, float top_p_scalar, const int32_t *banned,
+               int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+               void *stream);
+
+/* u[i] = the i-th uniform of draw `draw` under `seed` (Philox4x32-10, counter
+ * (i/4, draw), key seed, 24-bit values in [0, 1)), for i < n.
+ * Replaces: m_uniform (src/mlxu.c:771-774) as used by sample_top_k_top_p
+ * (src/sampling.c:208); the MLX generator itself is not reproduced. */
+int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream);
+
+/* The largest k d3s_sample accepts, and the largest vocab the fused kernel
+ * takes for a dtype (wider rows use the streaming kernel). */
+int d3s_max_k(void);
+int d3s_fused_max_vocab(int dtype);
+
+/* Diagnostic, no counterpart in the reference: the device versions of the
+ * shared fp32 functions (exp, log, division by `divisor`, 2^-40 fixed-point
+ * image), elementwise over in[0..n), for bit-exact comparison with the CPU. */
+int d3s_math_selftest(const float *in, float *out_exp, float *out_log, float *out_div,
+                      uint64_t *out_fix, int64_t n, float divisor, void *stream);
+
+/* "d3sampler <version> gfx950" */
+const char *d3s_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

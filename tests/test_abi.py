@@ -1,0 +1,76 @@
+"""The C-ABI library: it loads, exports every function include/*.h declares,
+and rejects bad arguments before touching the device (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
+
+
+def declared_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"#.*", "", text)
+    names = set()
+    for m in re.finditer(r"([A-Za-z_][A-Za-z0-9_]*)\s*\(([^()]*)\)\s*;", text):
+        name = m.group(1)
+        if name not in {"if", "while", "for", "return", "sizeof"}:
+            names.add(name)
+    return names
+
+
+def exported_symbols(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import d3s
+    return d3s.lib()
+
+
+def test_headers_declare_the_reference_names():
+    names = set().union(*(declared_functions(h) for h in HEADERS))
+    for ref_name in ("sample_top_k_top_p", "sample_noise", "sample_with_noise", "m_seed",
+                     "d3_sample", "d3s_sample"):
+        assert ref_name in names
+
+
+def test_library_exports_every_declared_function(lib):
+    import d3s
+    exported = exported_symbols(d3s.LIB_PATH)
+    for h in HEADERS:
+        missing = declared_functions(h) - exported
+        assert not missing, (os.path.basename(h), missing)
+
+
+def test_host_queries(lib):
+    assert lib.d3s_version().startswith(b"d3sampler")
+    assert lib.d3s_max_k() == 16384
+    assert lib.d3s_fused_max_vocab(0) >= 4097 and lib.d3s_fused_max_vocab(1) >= 4096
+    assert lib.d3s_fused_max_vocab(7) == -4
+
+
+def test_argument_validation_without_device(lib):
+    import d3s
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation
+    base = dict(logits=p.value, dtype=0, n_rows=4, vocab=100, row_stride=100, u=p.value, k=10,
+                temperature=1.0, top_p=0.9, banned=None, ids=p.value)
+    assert d3s.sample_raw(**{**base, "dtype": 5}) == -4
+    assert d3s.sample_raw(**{**base, "k": 0}) == -1
+    assert d3s.sample_raw(**{**base, "k": 101}) == -1
+    assert d3s.sample_raw(**{**base, "row_stride": 99}) == -1
+    assert d3s.sample_raw(**{**base, "vocab": 0, "row_stride": 0}) == -1
+    assert d3s.sample_raw(**{**base, "n_rows": -1}) == -1
+    assert d3s.sample_raw(**{**base, "ids": None}) == -1
+    assert d3s.sample_raw(**{**base, "flags": 64}) == -1
+    big = dict(base, vocab=20000, row_stride=20000, k=16385)
+    assert d3s.sample_raw(**big) == -2
+    assert d3s.sample_raw(**{**base, "n_rows": 0}) == 0  # nothing to do, nothing launched

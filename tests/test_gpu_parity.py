@@ -1,0 +1,237 @@
+"""GPU parity: the HIP sampler through the C-ABI against the CPU oracle on the
+same logits and the same uniforms.
+
+Ids and candidate lists must be identical on every row and probabilities
+bit-identical (the north-star bar is ids equal except boundary rows and
+probabilities within 1e-5 relative; both kernels compute the oracle's exact
+definition, so the test asks for equality and reports the boundary rows, i.e.
+rows where an fp32 implementation with another summation order could differ)."""
+import sys
+
+import numpy as np
+import pytest
+
+import d3s_workloads as W
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5  # the north-star tolerance for post-filter probabilities
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import d3s
+    import hiprt
+    d3s.lib()
+    if hiprt.device_count() < 1:
+        pytest.skip("no GPU")
+    return d3s
+
+
+def banner(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def compare(oracle, gpu, logits, u, T, top_p, banned=None, flags=0, label="", row_stride=None,
+            vocab=None):
+    banner(f"{label} shape={logits.shape} k={u.shape[1]} flags={flags}")
+    exp = oracle.sample(logits, u, T, top_p, banned=banned, n_threads=8, row_stride=row_stride,
+                        vocab=vocab)
+    got = gpu.sample(logits, u, T, top_p, banned=banned, flags=flags, row_stride=row_stride,
+                     vocab=vocab)
+    assert got["rc"] == 0, got["rc"]
+    bad = np.nonzero(got["ids"] != exp["ids"])[0]
+    edge = int(np.sum((exp["flags"] & (oracle.TOPP_EDGE | oracle.RACE_EDGE)) != 0))
+    banner(f"  rows={len(exp['ids'])} mismatched={len(bad)} boundary={edge} "
+           f"counters={got['counters'].tolist()}")
+    assert len(bad) == 0, (bad[:10], got["ids"][bad[:10]], exp["ids"][bad[:10]])
+    assert np.array_equal(got["cand"], exp["cand"])
+    both_nan = np.isnan(got["probs"]) & np.isnan(exp["probs"])
+    assert np.array_equal(got["probs"][~both_nan], exp["probs"][~both_nan])
+    np.testing.assert_allclose(got["probs"][~both_nan], exp["probs"][~both_nan], rtol=RTOL)
+    return got, exp
+
+
+def test_device_math_is_bit_exact(gpu, oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([np.linspace(-110, 95, 400_001, dtype=np.float32),
+                        (rng.standard_normal(200_000) * 30).astype(np.float32),
+                        np.exp(rng.uniform(-100, 88, 200_000)).astype(np.float32),
+                        rng.random(100_000).astype(np.float32),
+                        np.array([0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 1.0], np.float32)])
+    for divisor in (0.7, 1.0, 1e-5, 3.3, 0.123456):
+        e, l, d, f = gpu.math_selftest(x, divisor)
+        assert np.array_equal(e.view(np.uint32), oracle.expf(x).view(np.uint32))
+        assert np.array_equal(l.view(np.uint32), oracle.logf(x).view(np.uint32))
+        ref = x / np.float32(divisor)
+        assert np.array_equal(np.isnan(d), np.isnan(ref))
+        assert np.array_equal(d[~np.isnan(d)].view(np.uint32), ref[~np.isnan(ref)].view(np.uint32))
+        assert np.array_equal(f, oracle.fix40(x))
+
+
+def test_uniform_fill_matches_host(gpu, oracle):
+    u = gpu.uniform_fill(100_003, 42, 7)
+    assert np.array_equal(u, oracle.uniform(42, 7, 1, 100_003)[0])
+
+
+@pytest.mark.parametrize("name,rows", [("C1", 2000), ("C2", 9), ("C3", 256), ("C4", 64),
+                                       ("C5", 4096)])
+def test_parity_on_configs(gpu, oracle, name, rows):
+    w = W.make(name, rows=rows, seed=42, uniforms=False)
+    u = oracle.uniform(42, 0, rows, w["k"])
+    compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], w["banned"], label=name)
+
+
+def test_single_row_launches(gpu, oracle):
+    """C1 as the CLI runs it: one row per call (the few-row instantiation)."""
+    w = W.make("C1", rows=24, seed=3, uniforms=False)
+    u = oracle.uniform(42, 100, 24, 30)
+    exp = oracle.sample(w["logits"], u, 0.7, 0.7)
+    for r in range(24):
+        got = gpu.sample(w["logits"][r:r + 1], u[r:r + 1], 0.7, 0.7)
+        assert got["ids"][0] == exp["ids"][r]
+        assert np.array_equal(got["probs"][0], exp["probs"][r])
+
+
+@pytest.mark.parametrize("flags", [1, 2, 4, 6])
+@pytest.mark.parametrize("name", ["C2", "C3"])
+def test_every_path_gives_the_same_bits(gpu, oracle, name, flags):
+    w = W.make(name, rows=64 if name == "C3" else 9, seed=5, uniforms=False)
+    u = oracle.uniform(5, 0, w["logits"].shape[0], w["k"])
+    compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], flags=flags,
+            label=f"{name} flags")
+
+
+@pytest.mark.parametrize("V,k", [(4097, 30), (1024, 30), (4097, 5)])
+def test_ties_fused_equals_generic(gpu, oracle, V, k):
+    """tests/test_decode.py:73-86 restated: integer-valued logits tie across the
+    k-th place; every path keeps the same (lowest-id) candidates."""
+    rng = np.random.default_rng(1)
+    logits = np.round(rng.standard_normal((8, V)) * 2).astype(np.float32)
+    for seed in range(0, 40, 8):
+        u = oracle.uniform(seed, 0, 8, k)
+        a, _ = compare(oracle, gpu, logits, u, 1.0, 2.0, label=f"ties seed {seed}")
+        b, _ = compare(oracle, gpu, logits, u, 1.0, 2.0, flags=gpu.FLAG_GENERIC, label="ties generic")
+        assert np.array_equal(a["ids"], b["ids"])
+
+
+def test_ambiguous_top_p_takes_the_exact_lse(gpu, oracle):
+    """top_p placed on a row's own cumulative value: the fast sum of exp cannot
+    decide the cut, the kernel recomputes the exact lse and still matches."""
+    w = W.make("C3", rows=64, seed=9, uniforms=False)
+    u = oracle.uniform(9, 0, 64, 30)
+    x = w["logits"]
+    T = np.float32(0.9)
+    top_p = np.empty(64, np.float32)
+    for r in range(64):
+        o = oracle.sample(x[r:r + 1], u[r:r + 1], T, 2.0)
+        lse = o["lse"][0]
+        xs = np.sort(x[r] / T)[::-1][:30]
+        c = np.float32(0)
+        cs = []
+        for v in xs:
+            c = np.float32(c + oracle.expf(np.array([v - lse], np.float32))[0])
+            cs.append(c)
+        j = 1 + r % 5
+        top_p[r] = np.nextafter(cs[j], np.float32(0 if r % 2 else 2))
+    got, _ = compare(oracle, gpu, x, u, T, top_p, label="ambiguous top_p")
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] >= 60
+
+
+def test_edge_rows(gpu, oracle):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((12, 300)) * 2).astype(np.float32)
+    x[0, 5] = np.nan
+    x[1, 7] = np.inf
+    x[2, :] = -np.inf
+    x[3, ::2] = -np.inf
+    x[4, :] = 3.0
+    x[5, :] = np.round(x[5])
+    x[6, 10] = 1e30
+    x[7, :] = 0.0
+    x[7, 3] = -0.0
+    u = rng.random((12, 20)).astype(np.float32)
+    u[8, :] = 0.0
+    u[9, 0] = 0.0
+    got, _ = compare(oracle, gpu, x, u, 0.8, 0.9, label="edge rows")
+    assert got["ids"][0] == -1 and got["ids"][1] == -1 and got["ids"][2] == 0
+    assert got["counters"][gpu.COUNTER_REFUSED] == 2 and got["counters"][gpu.COUNTER_ALL_MASKED] == 1
+    compare(oracle, gpu, x, u, 0.8, 0.9, flags=gpu.FLAG_GENERIC, label="edge rows generic")
+
+
+@pytest.mark.parametrize("T,top_p", [(0.0, 0.7), (np.inf, 0.9), (np.nan, 0.9), (1e-5, 0.5),
+                                     (1e4, 0.8), (0.7, np.nan), (0.7, -1.0), (0.7, 1.0)])
+def test_parameter_edges(gpu, oracle, T, top_p):
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((16, 500)) * 3).astype(np.float32)
+    u = rng.random((16, 30)).astype(np.float32)
+    compare(oracle, gpu, x, u, T, top_p, label=f"T={T} top_p={top_p}")
+
+
+@pytest.mark.parametrize("V,k", [(1, 1), (2, 1), (2, 2), (63, 63), (64, 64), (65, 64), (65, 65),
+                                 (100, 80), (5117, 30), (5118, 30), (8189, 64), (8190, 64),
+                                 (16381, 30), (16382, 30), (40000, 64), (40000, 300)])
+def test_shapes(gpu, oracle, V, k):
+    rng = np.random.default_rng([V, k])
+    N = 70  # >= 64 rows: the 256-thread instantiations (fewer rows use 1024 threads)
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    u = oracle.uniform(1, 0, N, k)
+    compare(oracle, gpu, x, u, 0.7, 0.8, label=f"V={V}")
+    xb = W.f32_to_bf16_bits(x)
+    compare(oracle, gpu, xb, u, 0.7, 0.8, label=f"V={V} bf16")
+
+
+def test_strided_and_unaligned_rows(gpu, oracle):
+    rng = np.random.default_rng(13)
+    for stride, V in [(4099, 4097), (4097, 4000), (301, 300), (8195, 8190)]:
+        x = (rng.standard_normal((40, stride)) * 2).astype(np.float32)
+        u = oracle.uniform(2, 0, 40, 30)
+        compare(oracle, gpu, x, u, 0.7, 0.7, row_stride=stride, vocab=V, label=f"stride {stride}")
+        xb = W.f32_to_bf16_bits(x)
+        compare(oracle, gpu, xb, u, 0.7, 0.7, row_stride=stride, vocab=V, label=f"stride {stride} bf16")
+
+
+def test_banned_rows(gpu, oracle):
+    w = W.make("C5", rows=64, seed=4, uniforms=False)
+    u = oracle.uniform(4, 0, 64, 4097)
+    compare(oracle, gpu, w["logits"], u, 1.0, 0.95, banned=w["banned"], label="C5 banned")
+    w3 = W.make("C3", rows=64, seed=4, uniforms=False)
+    u3 = oracle.uniform(4, 0, 64, 30)
+    ban = np.where(np.arange(64) % 3 == 0, np.argmax(w3["logits"], axis=1), -1).astype(np.int32)
+    compare(oracle, gpu, w3["logits"], u3, 0.7, 0.7, banned=ban, label="C3 banned argmax")
+
+
+def test_shim_entry_points(gpu, oracle):
+    """d3_sample (src/testapi.c:155-166): m_seed, device draws, sample."""
+    w = W.make("C3", rows=32, seed=6, uniforms=False)
+    x = w["logits"]
+    ids = gpu.d3_sample(x, 0.7, 30, 0.7, 1234)
+    u = oracle.uniform(1234, 0, 1, 32 * 30).reshape(32, 30)  # draw 0, flat index r*k+j
+    assert np.array_equal(ids, oracle.sample(x, u, 0.7, 0.7)["ids"])
+    ids2 = gpu.d3_sample_with_noise(x, u, 0.7, 0.7)
+    assert np.array_equal(ids, ids2)
+    # top_k above V clamps to V (src/sampling.c:207)
+    small = x[:, :20].copy()
+    ids3 = gpu.d3_sample(small, 1.0, 50, 0.9, 7)
+    u3 = oracle.uniform(7, 0, 1, 32 * 20).reshape(32, 20)
+    assert np.array_equal(ids3, oracle.sample(small, u3, 1.0, 0.9)["ids"])
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p",
+                         [(0.7, 30, 0.7), (1.0, 30, 0.9), (1.0, 5, 1.0), (0.3, 30, 0.95)])
+def test_distribution(gpu, temperature, top_k, top_p):
+    """tests/test_decode.py:89-114 restated on the GPU: 4000 draws against the
+    float64 closed form, within 4 sigma + 1e-3."""
+    import closed_form as CF
+    rng = np.random.default_rng(0)
+    logits = (rng.standard_normal((1, 4097)) * 3).astype(np.float32)
+    n = 4000
+    u = W.uniform_rows(0, 0, n, top_k)
+    ours = gpu.sample(np.repeat(logits, n, axis=0), u, temperature, top_p, want_probs=False)["ids"]
+    cf = CF.row(logits[0], u[0], temperature, top_p, top_k)
+    expected = dict(zip(cf["cand"][:cf["kept"]], cf["probs"][:cf["kept"]]))
+    for token, prob in expected.items():
+        freq = np.mean(ours == token)
+        assert abs(freq - prob) < 4 * np.sqrt(prob * (1 - prob) / n) + 1e-3, (token, freq, prob)
+    assert set(np.unique(ours)) <= set(expected)
