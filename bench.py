@@ -112,6 +112,26 @@ def time_kernel(batches, params, n):
     return float(d.mean()), float(np.median(d))
 
 
+def launch_floor(n):
+    """Events around a near-empty launch (the uniform fill of 64 values): the
+    part of any event-timed launch that is dispatch, not work."""
+    import d3s
+    import hiprt
+    buf = hiprt.DeviceBuffer(256)
+    s = hiprt.Stream()
+    a, b = hiprt.Event(), hiprt.Event()
+    d = []
+    for i in range(n + 20):
+        a.record(s)
+        assert d3s.lib().d3s_uniform_fill(buf.ptr, 64, 1, i, s.ptr) == 0
+        b.record(s)
+        b.synchronize()
+        if i >= 20:
+            d.append(a.elapsed_ms(b) * 1e3)
+    s.destroy()
+    return float(np.median(d))
+
+
 def single_row_latency(n):
     """C1: one [1, 4097] fp32 row per call.  GPU time (events around the
     launch) and host time (call to completion) per row, p50 / p90."""
@@ -204,6 +224,8 @@ def main():
     bytes_per_launch = ROWS * BYTES_PER_ROW
     achieved = bytes_per_launch / (kmean * 1e-6) / 1e9
     log(f"kernel: mean {kmean:.2f} us, median {kmed:.2f} us -> {achieved:.0f} GB/s")
+    floor_us = launch_floor(500)
+    log(f"empty-launch floor (events): {floor_us:.2f} us")
     lat = single_row_latency(args.single_rows)
     log(f"C1 single row: p50 {lat['p50_us']:.2f} us (GPU), host p50 {lat['host_p50_us']:.2f} us")
     traffic = None
@@ -240,6 +262,7 @@ def main():
         "cpu_baseline": cpu,
         "single_stream_rows_per_s": single_stream,
         "p50_us_single_row": lat["p50_us"],
+        "event_floor_us": floor_us,
         "single_row": lat,
     }
     print(json.dumps(out), flush=True)

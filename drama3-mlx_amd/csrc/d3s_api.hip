@@ -42,7 +42,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   if (!logits || !u || !ids) return D3S_ERR_ARG;
   /* rows are addressed in whole elements */
   if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
-  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT)) != 0u)
+  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_SELECT)) != 0u)
     return D3S_ERR_ARG;
   d3s::SampleArgs a;
   a.logits = logits;

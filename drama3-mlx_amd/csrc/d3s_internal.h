@@ -34,14 +34,12 @@ enum {
   CNT_REFUSED = 0,      /* non-finite x: id -1 */
   CNT_ALL_MASKED = 1,   /* every x -inf */
   CNT_EXACT_SELECT = 2, /* fused kernel fell back to the radix select */
-  CNT_EXACT_LSE = 3,    /* fused kernel recomputed the exact lse */
-  CNT_NUM = 4
+  CNT_NUM = 3
 };
 
 /* flags (same values as the public D3S_FLAG_*) */
 enum : unsigned {
   FLAG_GENERIC = 1u,
-  FLAG_EXACT_LSE = 2u,
   FLAG_EXACT_SELECT = 4u,
 };
 

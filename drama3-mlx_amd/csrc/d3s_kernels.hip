@@ -6,21 +6,20 @@
  * :43-44,:129-134; exponential race over caller uniforms :45-48,:132-139).
  *
  * Two kernels, one workgroup per row:
- *  - k_fused (k <= 64, row held in registers): one pass over the row computes
- *    the row max, then a second pass over the registers accumulates a fast
- *    sum of exp (hardware exp2) and a 256-bin histogram of the distance to the
- *    max; the bin holding the k-th value bounds a small candidate set that is
- *    ranked exactly.  Rows the histogram cannot settle (too many candidates,
- *    or a candidate tie across the cut) take an exact 8-bit radix select over
- *    order-preserving keys.  The fast sum of exp decides the top-p cut unless
- *    some c_r lies within the fast sum's error bound of top_p; such rows
- *    recompute the exact, order-independent log-sum-exp.  Every row therefore
- *    gets the same bits as the exact definition.
+ *  - k_fused (k <= 64, row held in registers, 1024 threads): pass 1 divides
+ *    the row by T exactly (FMA division) and takes its max; pass 2 sums
+ *    exp(x - m) exactly in 2^-40 fixed point (order independent) and builds a
+ *    256-bin histogram of the distance below the max; the bin holding the k-th
+ *    value bounds a small candidate set, each candidate finds its own rank and
+ *    files its rank-independent terms, and wave 0 runs the reference kernel's
+ *    sequential cumulative, the cut and the race.  Rows the histogram cannot
+ *    settle take an exact 8-bit radix select over order-preserving keys.
  *  - k_generic (any V, k <= 16384): streams the row from global memory for
  *    every pass; exact log-sum-exp, radix select, LDS bitonic sort of the k
  *    selected, exact-sum top-p for k > 64.  Rows wider than the fused kernel
  *    takes, k > 64 (the reference's op-graph cases), and the
  *    D3S_FLAG_GENERIC switch use it.
+ * Both compute the same definition bit for bit (the oracle's).
  */
 #include <mutex>
 
@@ -37,50 +36,88 @@ constexpr int KF = 64;                      /* fused kernel's largest k */
 constexpr int NB = 256;                     /* histogram bins */
 constexpr float BINS_PER_NAT = 8.0f;        /* 256 bins over 32 units of x below the max */
 constexpr int GCAP = 256;                   /* candidate capacity of the fused kernel */
-constexpr float LOG2E = 1.44269504088896341f;
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
 
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
+/* ---- wave64 primitives on DPP (gfx9 row_shr / row_bcast lane movement) ----
+ * A Kogge-Stone scan within each row of 16 lanes (row_shr 1, 2, 4, 8), then
+ * row_bcast:15 / row_bcast:31 carry row totals forward: lane i ends with the
+ * combination of lanes 0..i, lane 63 with the whole wave.  Lanes without a
+ * source keep the identity passed as `old`. */
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
+constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
 
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
-  return v;
+template <int CTRL, int ROWM>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWM, 0xf, false);
 }
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const uint32_t t = __shfl_up(v, (unsigned)o);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
-
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const uint64_t t = __shfl_up(v, (unsigned)o);
-    if (lane >= o) v += t;
-  }
-  return v;
+template <int CTRL, int ROWM>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWM, 0xf, false));
 }
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+
+/* inclusive prefix sum over the wave */
+__device__ __forceinline__ uint32_t wave_scan_add_u32(uint32_t v) {
+  v += dpp_u<DPP_SHR1, 0xf>(0u, v);
+  v += dpp_u<DPP_SHR2, 0xf>(0u, v);
+  v += dpp_u<DPP_SHR4, 0xf>(0u, v);
+  v += dpp_u<DPP_SHR8, 0xf>(0u, v);
+  v += dpp_u<DPP_BCAST15, 0xa>(0u, v);
+  v += dpp_u<DPP_BCAST31, 0xc>(0u, v);
+  return v;
+}
+
+/* wave-uniform results (lane 63's scan value, read into a scalar) */
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return readlane_u(wave_scan_add_u32(v), 63); }
+
+__device__ __forceinline__ float wave_max_f(float v) {
+  const float ninf = -__builtin_inff();
+  v = fmaxf(v, dpp_f<DPP_SHR1, 0xf>(ninf, v));
+  v = fmaxf(v, dpp_f<DPP_SHR2, 0xf>(ninf, v));
+  v = fmaxf(v, dpp_f<DPP_SHR4, 0xf>(ninf, v));
+  v = fmaxf(v, dpp_f<DPP_SHR8, 0xf>(ninf, v));
+  v = fmaxf(v, dpp_f<DPP_BCAST15, 0xa>(ninf, v));
+  v = fmaxf(v, dpp_f<DPP_BCAST31, 0xc>(ninf, v));
+  return readlane_f(v, 63);
+}
+
+/* sum of per-lane values below 2^45 (fixed-point partial sums): two 32-bit
+ * scans of the high and low parts, recombined */
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  const uint32_t lo = wave_sum_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t hi = wave_sum_u32((uint32_t)(v >> 24));
+  return ((uint64_t)hi << 24) + lo;
+}
+
+/* The best (score, rank) over the wave: the greatest score, ties to the
+ * smaller rank (the reference's first maximum).  Wave-uniform result. */
+__device__ __forceinline__ void wave_argmax(float &s, int &r) {
+#define D3S_ARGMAX_STEP(CTRL, ROWM)                                        \
+  {                                                                        \
+    const float os = dpp_f<CTRL, ROWM>(-2.0f, s);                          \
+    const int orr = (int)dpp_u<CTRL, ROWM>(0x7fffffffu, (uint32_t)r);      \
+    if (os > s || (os == s && orr < r)) {                                  \
+      s = os;                                                              \
+      r = orr;                                                             \
+    }                                                                      \
+  }
+  D3S_ARGMAX_STEP(DPP_SHR1, 0xf)
+  D3S_ARGMAX_STEP(DPP_SHR2, 0xf)
+  D3S_ARGMAX_STEP(DPP_SHR4, 0xf)
+  D3S_ARGMAX_STEP(DPP_SHR8, 0xf)
+  D3S_ARGMAX_STEP(DPP_BCAST15, 0xa)
+  D3S_ARGMAX_STEP(DPP_BCAST31, 0xc)
+#undef D3S_ARGMAX_STEP
+  s = readlane_f(s, 63);
+  r = (int)readlane_u((uint32_t)r, 63);
 }
 
 __device__ __forceinline__ uint64_t composite_key(float x, int idx) {
@@ -105,6 +142,11 @@ __device__ __forceinline__ RowP row_params(const SampleArgs &a, int row) {
   return p;
 }
 
+/* x = logit / T, correctly rounded (y = RN(1/T)); T = +inf takes the division */
+__device__ __forceinline__ float scale_logit(float L, float T, float y, bool t_finite) {
+  return t_finite ? d3s_div_rn(L, T, y) : L / T;
+}
+
 /* bit 0: NaN or +inf (refused), bit 1: -inf present */
 __device__ __forceinline__ uint32_t classify(float v) {
   const uint32_t b = d3s_f2u(v);
@@ -125,23 +167,77 @@ __device__ void write_special(const SampleArgs &a, int row, bool masked) {
   }
 }
 
+/* Wave-aggregated append: the lanes with `pred` get consecutive slots from
+ * *counter with one atomic per wave.  Called by every lane of the wave. */
+__device__ __forceinline__ int wave_append(bool pred, int *counter) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0ull) return -1;
+  int base = 0;
+  if (lane_id() == 0) base = atomicAdd(counter, (int)__popcll(m));
+  base = __builtin_amdgcn_readfirstlane(base);
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  return pred ? base + below : -1;
+}
+
+/* Make a wave's LDS writes visible to its own later LDS reads (other lanes). */
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 /* Lane r (< k) gets e_0 + e_1 + ... + e_r added left to right in fp32: the
- * reference kernel's sequential cumulative (src/sampling.c:126-127). */
-__device__ __forceinline__ float wave_seq_cumsum(float e, int k) {
+ * reference kernel's sequential cumulative (src/sampling.c:126-127).  The
+ * terms go through LDS (`buf`, 64 floats private to the wave, 16-byte
+ * aligned) and every lane runs the same chain of additions on broadcast
+ * reads of four terms at a time: no cross-lane round trip per step. */
+__device__ __forceinline__ float wave_seq_cumsum(float e, int k, float *buf) {
   const int lane = lane_id();
+  buf[lane] = lane < k ? e : 0.0f;
+  wave_lds_sync();
+  const float4 *b4 = (const float4 *)buf;
   float c = 0.0f, mine = 0.0f;
-  for (int r = 0; r < k; r++) {
-    c = c + readlane_f(e, r);
-    if (lane == r) mine = c;
+  for (int r4 = 0; r4 < (k + 3) / 4; r4++) {
+    const float4 q = b4[r4];
+    const int r = 4 * r4;
+    c = c + q.x;
+    mine = lane == r ? c : mine;
+    c = c + q.y;
+    mine = lane == r + 1 ? c : mine;
+    c = c + q.z;
+    mine = lane == r + 2 ? c : mine;
+    c = c + q.w;
+    mine = lane == r + 3 ? c : mine;
   }
+  wave_lds_sync();
   return mine;
 }
 
-/* One wave; lane r < k holds rank r's x and index, and c_r.  The exclusive
- * top-p cut, the kept sum, the probabilities and the race, in the reference
- * kernel's order (src/sampling.c:128-139); writes ids/probs/cand. */
+/* the fp32 sum e_0 + ... + e_{n-1}, left to right, in every lane (n <= 64) */
+__device__ __forceinline__ float wave_seq_sum(float e, int n, float *buf) {
+  const int lane = lane_id();
+  buf[lane] = lane < n ? e : 0.0f;
+  wave_lds_sync();
+  const float4 *b4 = (const float4 *)buf;
+  float s = 0.0f;
+  for (int r4 = 0; r4 < n / 4; r4++) {
+    const float4 q = b4[r4];
+    s = s + q.x;
+    s = s + q.y;
+    s = s + q.z;
+    s = s + q.w;
+  }
+  for (int r = n & ~3; r < n; r++) s = s + buf[r];
+  wave_lds_sync();
+  return s;
+}
+
+/* One wave; lane r < k holds rank r's x (v), index, c_r and noise -log(1 - u_r).  The
+ * exclusive top-p cut, the kept sum, the probabilities and the race, in the
+ * reference kernel's order (src/sampling.c:128-139); writes ids/probs/cand. */
 __device__ void wave_tail_finish(const SampleArgs &a, int row, float v, int idx, float c,
-                                 float top_p) {
+                                 float noise, float top_p, float *buf) {
   const int lane = lane_id();
   const int k = a.k;
   const bool act = lane < k;
@@ -150,27 +246,17 @@ __device__ void wave_tail_finish(const SampleArgs &a, int row, float v, int idx,
   const int cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
   const float v0 = readlane_f(v, 0);
   const float ep = act ? d3s_expf(v - v0) : 0.0f;
-  float s = 0.0f;
-  for (int r = 0; r < cut; r++) s = s + readlane_f(ep, r);
+  const float s = wave_seq_sum(ep, cut, buf);
   const float inv = 1.0f / s;
   const float p = (act && lane < cut) ? ep * inv : 0.0f;
   float sc = -1.0f;
   if (act) {
-    const float noise = -d3s_logf(1.0f - a.u[(size_t)row * k + lane]);
     const float score = p / noise;
     sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
   }
   int best = lane;
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) {
-    const float os = __shfl_xor(sc, o);
-    const int ob = __shfl_xor(best, o);
-    if (os > sc || (os == sc && ob < best)) {
-      sc = os;
-      best = ob;
-    }
-  }
-  const int id = __shfl(idx, best);
+  wave_argmax(sc, best);
+  const int id = (int)readlane_u((uint32_t)idx, best);
   if (lane == 0) a.ids[row] = id;
   if (act) {
     if (a.probs) a.probs[(size_t)row * k + lane] = p;
@@ -178,10 +264,10 @@ __device__ void wave_tail_finish(const SampleArgs &a, int row, float v, int idx,
   }
 }
 
-/* Wave 0 scans a 256-bin histogram for the bin holding the `need`-th element,
+/* A wave scans a 256-bin histogram for the bin holding the `need`-th element,
  * counting from bin 0 upward (ASC) or from bin 255 downward (!ASC).  The
- * result (the bin, the count before it, its count) is the same in every lane;
- * ok is false when the histogram holds fewer than `need`. */
+ * result (the bin, the count before it, its count) is wave-uniform; ok is
+ * false when the histogram holds fewer than `need`. */
 struct BinSel {
   bool ok;
   uint32_t bin, above, count;
@@ -194,8 +280,8 @@ __device__ BinSel wave_find_bin(const uint32_t *hist, uint32_t need) {
 #pragma unroll
   for (int q = 0; q < 4; q++) h[q] = hist[ASC ? 4 * lane + q : NB - 1 - 4 * lane - q];
   const uint32_t ls = h[0] + h[1] + h[2] + h[3];
-  const uint32_t incl = wave_incl_scan_u32(ls);
-  const uint32_t total = __shfl(incl, WAVE - 1);
+  const uint32_t incl = wave_scan_add_u32(ls);
+  const uint32_t total = readlane_u(incl, 63);
   BinSel r;
   r.ok = total >= need;
   r.bin = r.above = r.count = 0u;
@@ -215,15 +301,44 @@ __device__ BinSel wave_find_bin(const uint32_t *hist, uint32_t need) {
       cum += h[q];
     }
   }
-  r.bin = __shfl(bin, L0);
-  r.above = __shfl(above, L0);
-  r.count = __shfl(cnt, L0);
+  r.bin = readlane_u(bin, L0);
+  r.above = readlane_u(above, L0);
+  r.count = readlane_u(cnt, L0);
   return r;
 }
 
 /* ------------------------------------------------------------------------ */
 /* fused kernel                                                              */
 /* ------------------------------------------------------------------------ */
+
+/* Wave 0: the exclusive top-p cut over c_r, the kept sum of ep_r (= exp(x_r - x_0)),
+ * the probabilities and the race (src/sampling.c:128-139); lane r < k holds
+ * rank r's index, c_r, ep_r and noise -log(1 - u_r).  Writes ids/probs/cand. */
+__device__ void wave_race(const SampleArgs &a, int row, int idx, float c, float ep, float noise,
+                          float top_p, float *buf) {
+  const int lane = lane_id();
+  const int k = a.k;
+  const bool act = lane < k;
+  const bool drop = act && lane > 0 && c > top_p;
+  const uint64_t dm = __ballot(drop);
+  const int cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
+  const float s = wave_seq_sum(ep, cut, buf);
+  const float inv = 1.0f / s;
+  const float p = (act && lane < cut) ? ep * inv : 0.0f;
+  float sc = -1.0f;
+  if (act) {
+    const float score = p / noise;
+    sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
+  }
+  int best = lane;
+  wave_argmax(sc, best);
+  const int id = (int)readlane_u((uint32_t)idx, best);
+  if (lane == 0) a.ids[row] = id;
+  if (act) {
+    if (a.probs) a.probs[(size_t)row * k + lane] = p;
+    if (a.cand) a.cand[(size_t)row * k + lane] = idx;
+  }
+}
 
 template <int BLOCK, int CPT, bool BF16>
 __global__ __launch_bounds__(BLOCK) void k_fused(SampleArgs a) {
@@ -233,78 +348,105 @@ __global__ __launch_bounds__(BLOCK) void k_fused(SampleArgs a) {
   constexpr int NW = BLOCK / WAVE;
   static_assert(BLOCK >= GCAP, "one thread per candidate");
 
-  __shared__ uint32_t hist[NB];
-  __shared__ float sh_max[NW], sh_sum[NW], sh_out[NW];
-  __shared__ uint32_t sh_flag[NW], sh_scan[NW];
-  __shared__ uint64_t sh_q[NW];
-  __shared__ uint64_t gK[GCAP];
-  __shared__ float gX[GCAP];
-  __shared__ int gI[GCAP];
-  __shared__ float sv[KF];
+  /* bins, then one overflow bin per lane: skipped elements still add (no branch) */
+  __shared__ uint32_t hist[NB + WAVE];
+  __shared__ float sh_max[NW];
+  __shared__ uint32_t sh_flag[NW], sh_scan[NW], sh_lo[NW], sh_hi[NW];
+  /* candidates, zero past them, then one write-off slot per lane */
+  __shared__ __align__(16) uint64_t gK[GCAP + 2 + WAVE];
+  /* by rank: index, exp(x - lse), exp(x - x_0) */
   __shared__ int si[KF];
-  __shared__ uint32_t sel[4];
-  __shared__ int n_gather, need_exact_sh, ambiguous_sh;
+  __shared__ float se[KF], sp[KF];
+  __shared__ __align__(16) float wbuf[WAVE];
+  __shared__ int n_gather;
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), wid = tid / WAVE;
   const int V = a.vocab, k = a.k;
   const RowP rp = row_params(a, row);
   const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
+  float uval = 0.0f; /* this row's uniforms, fetched early: the race reads them last */
+  if (wid == 0 && lane < k) uval = a.u[(size_t)row * k + lane];
 
-  /* ---- the row, in 16-byte chunks from the aligned address below its start */
+  /* ---- the row, in 16-byte chunks from the aligned address at or below its
+   * start (a chunk never crosses a page, so the bytes outside the row that it
+   * covers are readable; they are masked out below) */
   const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
-  const uintptr_t a0 = (uintptr_t)rowp & ~(uintptr_t)15;
-  const int off = (int)(((uintptr_t)rowp - a0) / ES);
+  const int off = (int)(((uintptr_t)rowp & 15u) / ES);
+  const uint4 *src = (const uint4 *)(rowp - off * ES);
   const int nchunks = (off + V + EPC - 1) / EPC;
-  float L[NV];
+  float x[NV];
 #pragma unroll
   for (int j = 0; j < CPT; j++) {
     const int c = j * BLOCK + tid;
     uint4 q = make_uint4(0u, 0u, 0u, 0u);
-    if (c < nchunks) q = *(const uint4 *)(a0 + (size_t)c * 16);
+    if (c < nchunks) q = src[c];
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int e = 0; e < EPC; e++) {
       if (BF16)
-        L[j * EPC + e] = d3s_u2f((e & 1) ? (w[e / 2] & 0xffff0000u) : (w[e / 2] << 16));
+        x[j * EPC + e] = d3s_u2f((e & 1) ? (w[e / 2] & 0xffff0000u) : (w[e / 2] << 16));
       else
-        L[j * EPC + e] = d3s_u2f(w[e]);
+        x[j * EPC + e] = d3s_u2f(w[e]);
     }
   }
-  auto pos = [&](int j, int e) { return (j * BLOCK + tid) * EPC + e - off; };
-  auto valid = [&](int j, int e) { return (unsigned)pos(j, e) < (unsigned)V; };
-  if (rp.banned >= 0 && rp.banned < V) {
-#pragma unroll
-    for (int j = 0; j < CPT; j++)
-#pragma unroll
-      for (int e = 0; e < EPC; e++)
-        if (pos(j, e) == rp.banned) L[j * EPC + e] = -__builtin_inff();
-  }
+  /* element i of this thread: chunk row i/EPC, lane-in-chunk i%EPC; index order
+   * is (chunk row, thread, lane-in-chunk) */
+  auto pos = [&](int i) { return ((i / EPC) * BLOCK + tid) * EPC + (i % EPC) - off; };
+  auto valid = [&](int i) { return (unsigned)pos(i) < (unsigned)V; };
+  /* does any lane of this wave hold a chunk of row j (wave-uniform) */
+  auto wave_has_row = [&](int j) {
+    return __builtin_amdgcn_readfirstlane(j * BLOCK + wid * WAVE) < nchunks;
+  };
 
-  /* ---- row max and input classification */
-  float lmax = -__builtin_inff();
-  uint32_t fl = 0;
+  /* ---- pass 1: x = logit / T exactly, classification, row max.  A wave whose
+   * logits all lie where the FMA division is exact takes it without branches;
+   * otherwise each element picks its own way (d3s_div_rn). */
+  bool in_range = true;
 #pragma unroll
-  for (int j = 0; j < CPT; j++)
-#pragma unroll
-    for (int e = 0; e < EPC; e++)
-      if (valid(j, e)) {
-        const float v = L[j * EPC + e];
-        const uint32_t c = classify(v);
-        fl |= c;
-        if (!(c & 1u)) lmax = fmaxf(lmax, v);
-      }
-  for (int i = tid; i < NB; i += BLOCK) hist[i] = 0u;
-  if (tid == 0) {
-    n_gather = 0;
-    need_exact_sh = 0;
-    ambiguous_sh = 0;
+  for (int i = 0; i < NV; i++) {
+    const uint32_t ea = (d3s_f2u(x[i]) >> 23) & 0xffu;
+    const bool ok = ea - 67u <= 160u && pos(i) != rp.banned; /* 2^-60 <= |L| < 2^101 */
+    in_range = in_range && (ok || !valid(i));
   }
-  lmax = wave_max_f(lmax);
-  fl = (__ballot(fl & 1u) ? 1u : 0u) | (__ballot(fl & 2u) ? 2u : 0u);
+  float xm = -__builtin_inff();
+  uint32_t fl = 0u;
+  if (t_finite && __all(in_range)) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const float q = x[i] * y;
+      const float r = __builtin_fmaf(-q, T, x[i]);
+      const float xi = __builtin_fmaf(r, y, q);
+      x[i] = xi;
+      const bool vld = valid(i);
+      fl |= vld ? classify(xi) : 0u;
+      xm = vld ? fmaxf(xm, xi) : xm;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      if (valid(i)) {
+        const float L = pos(i) == rp.banned ? -__builtin_inff() : x[i];
+        const float xi = scale_logit(L, T, y, t_finite);
+        x[i] = xi;
+        const uint32_t c = classify(xi);
+        fl |= c;
+        if (!(c & 1u)) xm = fmaxf(xm, xi);
+      }
+  }
+  for (int i = tid; i < NB + WAVE; i += BLOCK) hist[i] = 0u;
+  for (int i = tid; i < GCAP + 2; i += BLOCK) gK[i] = 0ull;
+  if (tid == 0) n_gather = 0;
+  /* the race's noise -log(1 - u) only needs u: wave 0 computes it while the
+   * other waves finish the first pass */
+  const float noise = wid == 0 ? -d3s_logf(1.0f - uval) : 0.0f;
+  xm = wave_max_f(xm);
+  const uint32_t wf = (__ballot(fl & 1u) ? 1u : 0u) | (__ballot(fl & 2u) ? 2u : 0u);
   if (lane == 0) {
-    sh_max[wid] = lmax;
-    sh_flag[wid] = fl;
+    sh_max[wid] = xm;
+    sh_flag[wid] = wf;
   }
   __syncthreads();
   float M = sh_max[0];
@@ -314,9 +456,7 @@ __global__ __launch_bounds__(BLOCK) void k_fused(SampleArgs a) {
     M = fmaxf(M, sh_max[w]);
     F |= sh_flag[w];
   }
-  const float xmax = M / T; /* = max x: correctly rounded division is monotone */
-  if ((F & 1u) || d3s_isnan(xmax) || xmax == __builtin_inff() ||
-      (T == __builtin_inff() && (F & 2u))) {
+  if (F & 1u) { /* a NaN or +inf x */
     write_special(a, row, false);
     return;
   }
@@ -325,153 +465,121 @@ __global__ __launch_bounds__(BLOCK) void k_fused(SampleArgs a) {
     return;
   }
 
-  /* ---- fast sum of exp and the distance histogram, one pass over registers */
-  const float c2 = LOG2E / T;
-  const float hs = BINS_PER_NAT / T;
-  float s = 0.0f;
+  /* ---- pass 2: the exact row sum of exp(x - m) in 2^-40 fixed point (order
+   * independent, src/sampling.c:81-89) and a histogram of the distance below
+   * the max, 8 bins per unit of x over 32 units */
+  uint64_t acc = 0;
+  const int overflow_bin = NB + lane;
 #pragma unroll
   for (int j = 0; j < CPT; j++)
+    if (wave_has_row(j)) {
 #pragma unroll
-    for (int e = 0; e < EPC; e++)
-      if (valid(j, e)) {
-        const float d = M - L[j * EPC + e];
-        s = s + __builtin_amdgcn_exp2f(-d * c2);
-        const float b = d * hs;
-        if (b < (float)NB) atomicAdd(&hist[(int)b], 1u);
+      for (int e = 0; e < EPC; e++) {
+        const int i = j * EPC + e;
+        const bool vld = valid(i);
+        const float z = x[i] - M;
+        const uint64_t f = d3s_fix40_exp(z);
+        acc += vld ? f : 0ull;
+        const float b = -z * BINS_PER_NAT;
+        atomicAdd(&hist[(vld && b < (float)NB) ? (int)b : overflow_bin], 1u);
       }
-  s = wave_sum_f(s);
-  if (lane == 0) sh_sum[wid] = s;
-  __syncthreads();
-  float S_f = 0.0f;
-#pragma unroll
-  for (int w = 0; w < NW; w++) S_f = S_f + sh_sum[w];
-  if (wid == 0) {
-    const BinSel b = wave_find_bin<true>(hist, (uint32_t)k);
+    }
+  {
+    const uint64_t w = wave_sum_u64(acc);
     if (lane == 0) {
-      sel[0] = b.bin;
-      sel[1] = b.above;
-      sel[2] = b.count;
-      if (!b.ok) need_exact_sh = 1;
+      sh_lo[wid] = (uint32_t)w;
+      sh_hi[wid] = (uint32_t)(w >> 32);
     }
   }
   __syncthreads();
-  bool need_exact = need_exact_sh || (a.flags & FLAG_EXACT_SELECT);
-  if (!need_exact && sel[1] + sel[2] > (uint32_t)GCAP) need_exact = true;
+  uint64_t S = 0;
+#pragma unroll
+  for (int w = 0; w < NW; w++) S += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
+  const float lse = M + d3s_logf(d3s_fixsum_to_f32(S)); /* src/sampling.c:89 */
+  /* every wave finds the k-th element's bin: same answer, no extra barrier */
+  const BinSel bs = wave_find_bin<true>(hist, (uint32_t)k);
+  const bool need_exact = !bs.ok || bs.above + bs.count > (uint32_t)GCAP || (a.flags & FLAG_EXACT_SELECT);
 
-  /* ---- candidates: every element in a bin up to the k-th element's bin */
+  int G;
   if (!need_exact) {
-    const int bstar = (int)sel[0];
-    float lout = -__builtin_inff();
+    /* candidates: every element in a bin up to the k-th element's.  The bin is
+     * a non-increasing function of x, so an element left out has a smaller x
+     * than every candidate and ranks below all of them. */
+    const float blim = (float)(bs.bin + 1u); /* b < bin + 1  <=>  (int)b <= bin */
+    uint32_t mine = 0u;
+#pragma unroll
+    for (int i = 0; i < NV; i++) mine += (valid(i) && -(x[i] - M) * BINS_PER_NAT < blim) ? 1u : 0u;
+    /* slots: one atomic per wave, then each lane's exclusive prefix */
+    const uint32_t incl = wave_scan_add_u32(mine);
+    const uint32_t wtot = readlane_u(incl, 63);
+    int base = 0;
+    if (wtot != 0u) {
+      if (lane == 0) base = atomicAdd(&n_gather, (int)wtot);
+      base = __builtin_amdgcn_readfirstlane(base);
+    }
+    uint32_t slot = (uint32_t)base + incl - mine;
+    const uint32_t write_off = GCAP + 2 + lane;
 #pragma unroll
     for (int j = 0; j < CPT; j++)
+      if (wave_has_row(j)) {
 #pragma unroll
-      for (int e = 0; e < EPC; e++)
-        if (valid(j, e)) {
-          const float v = L[j * EPC + e];
-          const float b = (M - v) * hs;
-          if (b < (float)NB && (int)b <= bstar) {
-            const int slot = atomicAdd(&n_gather, 1);
-            if (slot < GCAP) {
-              gX[slot] = v; /* the logit for now; x below */
-              gI[slot] = pos(j, e);
-            }
-          } else {
-            lout = fmaxf(lout, v);
-          }
+        for (int e = 0; e < EPC; e++) {
+          const int i = j * EPC + e;
+          const bool cnd = valid(i) && -(x[i] - M) * BINS_PER_NAT < blim;
+          gK[(cnd && slot < (uint32_t)GCAP) ? slot : write_off] = composite_key(x[i], pos(i));
+          slot += cnd ? 1u : 0u;
         }
-    lout = wave_max_f(lout);
-    if (lane == 0) sh_out[wid] = lout;
-    __syncthreads();
-    const int G = min(n_gather, GCAP);
-    float Lo = sh_out[0];
-#pragma unroll
-    for (int w = 1; w < NW; w++) Lo = fmaxf(Lo, sh_out[w]);
-    if (tid < G) {
-      const float x = gX[tid] / T;
-      gX[tid] = x;
-      gK[tid] = composite_key(x, gI[tid]);
-    }
-    __syncthreads();
-    if (tid < G) {
-      const uint64_t my = gK[tid];
-      int rank = 0;
-      for (int j = 0; j < G; j++) rank += gK[j] > my;
-      if (rank < k) {
-        sv[rank] = gX[tid];
-        si[rank] = gI[tid];
       }
-    }
     __syncthreads();
-    /* an element left out must rank below the k-th: it has a smaller logit, so
-     * its x is <= x_k; equality (a tie made by the division) is settled exactly */
-    if (Lo / T == sv[k - 1]) need_exact = true;
-  }
-
-  /* ---- exact radix select over order-preserving keys of x */
-  if (need_exact) {
+    G = min(n_gather, GCAP); /* = above + count >= k */
+  } else {
+    /* ---- exact radix select of the k-th (x desc, index asc) rank over
+     * order-preserving keys of x, 8 bits per pass */
     if (tid == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_SELECT], 1u);
-#pragma unroll
-    for (int i = 0; i < NV; i++) L[i] = L[i] / T; /* L now holds x */
     uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)k, done = 0u;
-    for (int pass = 0; pass < 4 && !done; pass++) {
-      const int shift = 24 - 8 * pass;
-      __syncthreads();
-      for (int i = tid; i < NB; i += BLOCK) hist[i] = 0u;
-      __syncthreads();
 #pragma unroll
-      for (int j = 0; j < CPT; j++)
+    for (int pass = 0; pass < 4; pass++) {
+      if (!done) {
+        const int shift = 24 - 8 * pass;
+        __syncthreads(); /* every wave has read the previous histogram */
+        for (int i = tid; i < NB; i += BLOCK) hist[i] = 0u;
+        __syncthreads();
 #pragma unroll
-        for (int e = 0; e < EPC; e++)
-          if (valid(j, e)) {
-            const uint32_t key = d3s_ordkey(L[j * EPC + e]);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-          }
-      __syncthreads();
-      if (wid == 0) {
-        const BinSel b = wave_find_bin<false>(hist, need); /* always holds >= need */
-        if (lane == 0) {
-          sel[0] = prefix | (b.bin << shift);
-          sel[1] = pmask | (0xffu << shift);
-          sel[2] = need - b.above;
-          sel[3] = (b.count == need - b.above) ? 1u : 0u;
+        for (int i = 0; i < NV; i++) {
+          const uint32_t key = d3s_ordkey(x[i]);
+          if (valid(i) && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
         }
+        __syncthreads();
+        const BinSel b = wave_find_bin<false>(hist, need); /* holds >= need */
+        prefix |= b.bin << shift;
+        pmask |= 0xffu << shift;
+        done = b.count == need - b.above;
+        need -= b.above;
       }
-      __syncthreads();
-      prefix = sel[0];
-      pmask = sel[1];
-      need = sel[2];
-      done = sel[3];
     }
-    /* gather: everything above the group, then the group (all of it when it
-     * holds exactly `need`, else its lowest-index `need`: exact ties) */
-    if (tid == 0) n_gather = 0;
-    __syncthreads();
+    /* everything above the group, then the group: all of it when it holds
+     * exactly `need`, else (exact ties) its lowest-index `need` */
 #pragma unroll
-    for (int j = 0; j < CPT; j++)
-#pragma unroll
-      for (int e = 0; e < EPC; e++)
-        if (valid(j, e)) {
-          const uint32_t key = d3s_ordkey(L[j * EPC + e]) & pmask;
-          if (key > prefix || (done && key == prefix)) {
-            const int slot = atomicAdd(&n_gather, 1);
-            if (slot < GCAP) {
-              gX[slot] = L[j * EPC + e];
-              gI[slot] = pos(j, e);
-            }
-          }
-        }
+    for (int i = 0; i < NV; i++) {
+      const uint32_t key = d3s_ordkey(x[i]) & pmask;
+      const int slot = wave_append(valid(i) && (key > prefix || (done && key == prefix)), &n_gather);
+      if (slot >= 0 && slot < GCAP) gK[slot] = composite_key(x[i], pos(i));
+    }
     if (!done) {
-      /* index order is (j, tid, e): one block scan per chunk row j */
       uint32_t base = 0u;
+#pragma unroll
       for (int j = 0; j < CPT; j++) {
         uint32_t cnt = 0u;
 #pragma unroll
-        for (int e = 0; e < EPC; e++)
-          if (valid(j, e) && d3s_ordkey(L[j * EPC + e]) == prefix) cnt++;
-        const uint32_t incl = wave_incl_scan_u32(cnt);
+        for (int e = 0; e < EPC; e++) {
+          const int i = j * EPC + e;
+          cnt += (valid(i) && d3s_ordkey(x[i]) == prefix) ? 1u : 0u;
+        }
+        const uint32_t incl = wave_scan_add_u32(cnt);
         if (lane == WAVE - 1) sh_scan[wid] = incl;
         __syncthreads();
         uint32_t wbase = 0u, tot = 0u;
+#pragma unroll
         for (int w = 0; w < NW; w++) {
           const uint32_t t = sh_scan[w];
           if (w < wid) wbase += t;
@@ -479,90 +587,52 @@ __global__ __launch_bounds__(BLOCK) void k_fused(SampleArgs a) {
         }
         uint32_t ord = base + wbase + incl - cnt;
 #pragma unroll
-        for (int e = 0; e < EPC; e++)
-          if (valid(j, e) && d3s_ordkey(L[j * EPC + e]) == prefix) {
-            if (ord < need) {
-              const int slot = atomicAdd(&n_gather, 1);
-              if (slot < GCAP) {
-                gX[slot] = L[j * EPC + e];
-                gI[slot] = pos(j, e);
-              }
-            }
-            ord++;
-          }
+        for (int e = 0; e < EPC; e++) {
+          const int i = j * EPC + e;
+          const bool tie = valid(i) && d3s_ordkey(x[i]) == prefix;
+          const int slot = wave_append(tie && ord < need, &n_gather);
+          if (slot >= 0 && slot < GCAP) gK[slot] = composite_key(x[i], pos(i));
+          ord += tie ? 1u : 0u;
+        }
         base += tot;
         __syncthreads();
-        if (base >= need) break;
       }
     }
     __syncthreads();
-    const int G = min(n_gather, GCAP); /* == k */
-    if (tid < G) gK[tid] = composite_key(gX[tid], gI[tid]);
-    __syncthreads();
-    if (tid < G) {
-      const uint64_t my = gK[tid];
-      int rank = 0;
-      for (int j = 0; j < G; j++) rank += gK[j] > my;
-      if (rank < k) {
-        sv[rank] = gX[tid];
-        si[rank] = gI[tid];
-      }
-    }
-    __syncthreads();
+    G = min(n_gather, GCAP); /* == k */
   }
 
-  /* ---- log-sum-exp and the top-p cut */
-  const bool have_x = need_exact;
-  auto exact_lse = [&]() -> float {
-    /* exact fixed-point sum of exp(x_i - m): independent of the order */
-    uint64_t acc = 0;
-#pragma unroll
-    for (int j = 0; j < CPT; j++)
-#pragma unroll
-      for (int e = 0; e < EPC; e++)
-        if (valid(j, e)) {
-          const float x = have_x ? L[j * EPC + e] : L[j * EPC + e] / T;
-          acc += d3s_fix40(d3s_expf(x - xmax));
-        }
-    acc = wave_sum_u64(acc);
-    if (lane == 0) sh_q[wid] = acc;
-    __syncthreads();
-    uint64_t S = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) S += sh_q[w];
-    if (tid == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-    return xmax + d3s_logf(d3s_fixsum_to_f32(S));
-  };
-
-  const float v = (wid == 0 && lane < k) ? sv[lane] : 0.0f;
-  const int idx = (wid == 0 && lane < k) ? si[lane] : 0;
-  const float top_p = rp.top_p;
-  if (need_exact || (a.flags & FLAG_EXACT_LSE)) {
-    const float lse = exact_lse();
-    if (wid == 0) {
-      const float c = wave_seq_cumsum(lane < k ? d3s_expf(v - lse) : 0.0f, k);
-      wave_tail_finish(a, row, v, idx, c, top_p);
+  /* ---- each candidate finds its rank (keys above its own, broadcast reads of
+   * two keys at a time) and, if it is among the top k, files its index and
+   * its rank-independent terms exp(x - lse) (src/sampling.c:127) and
+   * exp(x - x_0) (x_0 = m; src/sampling.c:129,134) at its rank */
+  if (tid < G) {
+    const uint64_t my = gK[tid];
+    const ulonglong2 *k2 = (const ulonglong2 *)gK;
+    int rank = 0;
+#pragma unroll 4
+    for (int j2 = 0; j2 < (G + 1) / 2; j2++) {
+      const ulonglong2 q = k2[j2];
+      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
     }
-    return;
+    if (rank < k) {
+      const float xr = key_x(my);
+      si[rank] = key_idx(my);
+      se[rank] = d3s_expf(xr - lse);
+      sp[rank] = d3s_expf(xr - M);
+    }
   }
-  float c = 0.0f;
-  if (wid == 0) {
-    const float lse_f = xmax + d3s_logf(S_f);
-    c = wave_seq_cumsum(lane < k ? d3s_expf(v - lse_f) : 0.0f, k);
-    /* |lse_f - lse| is below 4*2^-23*(|m|+64) + 1e-5 (input rounding of x,
-     * hardware exp2, fp32 summation); a c_r moves by at most that plus 1.2e-5
-     * of exp / addition rounding.  Twice that bound is the margin. */
-    const float eps = 8.0f * 0x1.0p-23f * (fabsf(xmax) + 64.0f) + 5e-5f;
-    const bool amb = lane >= 1 && lane < k && fabsf(c - top_p) <= eps;
-    const bool any_amb = __ballot(amb) != 0ull;
-    if (lane == 0 && any_amb) ambiguous_sh = 1;
-  }
-  __syncthreads();
-  if (ambiguous_sh) {
-    const float lse = exact_lse();
-    if (wid == 0) c = wave_seq_cumsum(lane < k ? d3s_expf(v - lse) : 0.0f, k);
-  }
-  if (wid == 0) wave_tail_finish(a, row, v, idx, c, top_p);
+  if (G > WAVE)
+    __syncthreads();
+  if (wid != 0) return;
+  wave_lds_sync();
+  const bool act = lane < k;
+  const int idx = act ? si[lane] : 0;
+  const float e = act ? se[lane] : 0.0f;
+  const float ep = act ? sp[lane] : 0.0f;
+  /* ---- the reference kernel's sequential cumulative (src/sampling.c:126-128) */
+  const float c = wave_seq_cumsum(e, k, wbuf);
+  wave_race(a, row, idx, c, ep, noise, rp.top_p, wbuf);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -582,20 +652,15 @@ __device__ __forceinline__ float load_logit(const void *rowp, int i, int banned)
   return i == banned ? -__builtin_inff() : v;
 }
 
-/* exclusive block scan in thread order; `tot` receives the block total */
-template <typename U>
-__device__ __forceinline__ U block_excl_scan(U v, U *sh, U &tot) {
+/* exclusive block scan of per-thread counts in thread order; `tot` = total */
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t *sh, uint32_t &tot) {
   const int lane = lane_id(), wid = threadIdx.x / WAVE;
-  U incl;
-  if constexpr (sizeof(U) == 8)
-    incl = wave_incl_scan_u64(v);
-  else
-    incl = wave_incl_scan_u32(v);
+  const uint32_t incl = wave_scan_add_u32(v);
   if (lane == WAVE - 1) sh[wid] = incl;
   __syncthreads();
-  U wbase = 0, t = 0;
+  uint32_t wbase = 0u, t = 0u;
   for (int w = 0; w < GNW; w++) {
-    const U x = sh[w];
+    const uint32_t x = sh[w];
     if (w < wid) wbase += x;
     t += x;
   }
@@ -604,40 +669,70 @@ __device__ __forceinline__ U block_excl_scan(U v, U *sh, U &tot) {
   return wbase + incl - v;
 }
 
+/* the same for per-thread fixed-point sums below 2^45 (split in 24-bit parts) */
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint32_t *sh_lo, uint32_t *sh_hi) {
+  const int lane = lane_id(), wid = threadIdx.x / WAVE;
+  const uint32_t lo = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t hi = wave_scan_add_u32((uint32_t)(v >> 24));
+  if (lane == WAVE - 1) {
+    sh_lo[wid] = lo;
+    sh_hi[wid] = hi;
+  }
+  __syncthreads();
+  uint64_t wbase = 0;
+  for (int w = 0; w < wid; w++) wbase += ((uint64_t)sh_hi[w] << 24) + sh_lo[w];
+  __syncthreads();
+  return wbase + ((uint64_t)hi << 24) + lo - v;
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+  const int big = 0x7fffffff;
+  v = min(v, (int)dpp_u<DPP_SHR1, 0xf>((uint32_t)big, (uint32_t)v));
+  v = min(v, (int)dpp_u<DPP_SHR2, 0xf>((uint32_t)big, (uint32_t)v));
+  v = min(v, (int)dpp_u<DPP_SHR4, 0xf>((uint32_t)big, (uint32_t)v));
+  v = min(v, (int)dpp_u<DPP_SHR8, 0xf>((uint32_t)big, (uint32_t)v));
+  v = min(v, (int)dpp_u<DPP_BCAST15, 0xa>((uint32_t)big, (uint32_t)v));
+  v = min(v, (int)dpp_u<DPP_BCAST31, 0xc>((uint32_t)big, (uint32_t)v));
+  return (int)readlane_u((uint32_t)v, 63);
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
   extern __shared__ uint64_t glist[]; /* [kpow] composite keys, sorted in place */
   __shared__ uint32_t hist[NB];
   __shared__ float sh_max[GNW];
-  __shared__ uint32_t sh_flag[GNW], sh_u32[GNW];
-  __shared__ uint64_t sh_q[GNW];
-  __shared__ uint32_t sel[4];
+  __shared__ uint32_t sh_flag[GNW], sh_u32[GNW], sh_lo[GNW], sh_hi[GNW];
   __shared__ int n_gather;
   __shared__ float sh_best[GNW];
   __shared__ int sh_bestr[GNW];
+  __shared__ __align__(16) float wbuf[WAVE];
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), wid = tid / WAVE;
   const int V = a.vocab, k = a.k;
   const RowP rp = row_params(a, row);
   const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
   const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  auto xat = [&](int i) { return scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite); };
 
   /* ---- pass 1: max and classification */
-  float lmax = -__builtin_inff();
+  float xm = -__builtin_inff();
   uint32_t fl = 0;
   for (int i = tid; i < V; i += GBLOCK) {
-    const float v = load_logit<BF16>(rowp, i, rp.banned);
-    const uint32_t c = classify(v);
+    const float xi = xat(i);
+    const uint32_t c = classify(xi);
     fl |= c;
-    if (!(c & 1u)) lmax = fmaxf(lmax, v);
+    if (!(c & 1u)) xm = fmaxf(xm, xi);
   }
-  lmax = wave_max_f(lmax);
-  fl = (__ballot(fl & 1u) ? 1u : 0u) | (__ballot(fl & 2u) ? 2u : 0u);
+  xm = wave_max_f(xm);
+  const uint32_t wf = (__ballot(fl & 1u) ? 1u : 0u) | (__ballot(fl & 2u) ? 2u : 0u);
   if (lane == 0) {
-    sh_max[wid] = lmax;
-    sh_flag[wid] = fl;
+    sh_max[wid] = xm;
+    sh_flag[wid] = wf;
   }
+  if (tid == 0) n_gather = 0;
   __syncthreads();
   float M = sh_max[0];
   uint32_t F = sh_flag[0];
@@ -645,9 +740,7 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
     M = fmaxf(M, sh_max[w]);
     F |= sh_flag[w];
   }
-  const float xmax = M / T;
-  if ((F & 1u) || d3s_isnan(xmax) || xmax == __builtin_inff() ||
-      (T == __builtin_inff() && (F & 2u))) {
+  if (F & 1u) {
     write_special(a, row, false);
     return;
   }
@@ -658,16 +751,20 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
 
   /* ---- pass 2: exact log-sum-exp */
   uint64_t acc = 0;
-  for (int i = tid; i < V; i += GBLOCK)
-    acc += d3s_fix40(d3s_expf(load_logit<BF16>(rowp, i, rp.banned) / T - xmax));
-  acc = wave_sum_u64(acc);
-  if (lane == 0) sh_q[wid] = acc;
+  for (int i = tid; i < V; i += GBLOCK) acc += d3s_fix40(d3s_expf(xat(i) - M));
+  {
+    const uint64_t w = wave_sum_u64(acc);
+    if (lane == 0) {
+      sh_lo[wid] = (uint32_t)w;
+      sh_hi[wid] = (uint32_t)(w >> 32);
+    }
+  }
   __syncthreads();
   uint64_t S = 0;
-  for (int w = 0; w < GNW; w++) S += sh_q[w];
-  const float lse = xmax + d3s_logf(d3s_fixsum_to_f32(S));
+  for (int w = 0; w < GNW; w++) S += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
+  const float lse = M + d3s_logf(d3s_fixsum_to_f32(S));
 
-  /* ---- radix select of the k-th composite rank over keys of x */
+  /* ---- radix select of the k-th rank over order-preserving keys of x */
   uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)k, done = 0u;
   for (int pass = 0; pass < 4 && !done; pass++) {
     const int shift = 24 - 8 * pass;
@@ -675,33 +772,22 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
     for (int i = tid; i < NB; i += GBLOCK) hist[i] = 0u;
     __syncthreads();
     for (int i = tid; i < V; i += GBLOCK) {
-      const uint32_t key = d3s_ordkey(load_logit<BF16>(rowp, i, rp.banned) / T);
+      const uint32_t key = d3s_ordkey(xat(i));
       if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
-    if (wid == 0) {
-      const BinSel b = wave_find_bin<false>(hist, need);
-      if (lane == 0) {
-        sel[0] = prefix | (b.bin << shift);
-        sel[1] = pmask | (0xffu << shift);
-        sel[2] = need - b.above;
-        sel[3] = (b.count == need - b.above) ? 1u : 0u;
-      }
-    }
-    __syncthreads();
-    prefix = sel[0];
-    pmask = sel[1];
-    need = sel[2];
-    done = sel[3];
+    const BinSel b = wave_find_bin<false>(hist, need);
+    prefix |= b.bin << shift;
+    pmask |= 0xffu << shift;
+    done = b.count == need - b.above;
+    need -= b.above;
   }
-  if (tid == 0) n_gather = 0;
-  __syncthreads();
   for (int i = tid; i < V; i += GBLOCK) {
-    const float x = load_logit<BF16>(rowp, i, rp.banned) / T;
-    const uint32_t key = d3s_ordkey(x) & pmask;
+    const float xi = xat(i);
+    const uint32_t key = d3s_ordkey(xi) & pmask;
     if (key > prefix || (done && key == prefix)) {
       const int slot = atomicAdd(&n_gather, 1);
-      if (slot < kpow) glist[slot] = composite_key(x, i);
+      if (slot < kpow) glist[slot] = composite_key(xi, i);
     }
   }
   if (!done) {
@@ -709,17 +795,17 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
     uint32_t base = 0u;
     for (int t0 = 0; t0 < V && base < need; t0 += GBLOCK) {
       const int i = t0 + tid;
-      float x = 0.0f;
+      float xi = 0.0f;
       uint32_t tie = 0u;
       if (i < V) {
-        x = load_logit<BF16>(rowp, i, rp.banned) / T;
-        tie = d3s_ordkey(x) == prefix;
+        xi = xat(i);
+        tie = d3s_ordkey(xi) == prefix;
       }
       uint32_t tot;
-      const uint32_t ord = base + block_excl_scan<uint32_t>(tie, sh_u32, tot);
+      const uint32_t ord = base + block_excl_scan_u32(tie, sh_u32, tot);
       if (tie && ord < need) {
         const int slot = atomicAdd(&n_gather, 1);
-        if (slot < kpow) glist[slot] = composite_key(x, i);
+        if (slot < kpow) glist[slot] = composite_key(xi, i);
       }
       base += tot;
     }
@@ -750,8 +836,9 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
       const uint64_t key = lane < k ? glist[lane] : 0ull;
       const float v = key_x(key);
       const int idx = key_idx(key);
-      const float c = wave_seq_cumsum(lane < k ? d3s_expf(v - lse) : 0.0f, k);
-      wave_tail_finish(a, row, v, idx, c, top_p);
+      const float uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
+      const float c = wave_seq_cumsum(lane < k ? d3s_expf(v - lse) : 0.0f, k, wbuf);
+      wave_tail_finish(a, row, v, idx, c, -d3s_logf(1.0f - uval), top_p, wbuf);
     }
     return;
   }
@@ -766,8 +853,7 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
     const int r = r0 + q;
     if (r < k) loc += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
   }
-  uint64_t tot;
-  uint64_t P = block_excl_scan<uint64_t>(loc, sh_q, tot);
+  uint64_t P = block_excl_scan_u64(loc, sh_lo, sh_hi);
   int cut_local = k;
   for (int q = 0; q < R; q++) {
     const int r = r0 + q;
@@ -776,10 +862,7 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
       if (r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > top_p) cut_local = r;
     }
   }
-  /* min over the block */
-  int cm = cut_local;
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) cm = min(cm, __shfl_xor(cm, o));
+  const int cm = wave_min_i32(cut_local);
   if (lane == 0) sh_u32[wid] = (uint32_t)cm;
   __syncthreads();
   int cut = k;
@@ -789,12 +872,17 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
     const int r = r0 + q;
     if (r < k && r < cut) ks += d3s_fix40(d3s_expf(key_x(glist[r]) - v0));
   }
-  ks = wave_sum_u64(ks);
-  __syncthreads();
-  if (lane == 0) sh_q[wid] = ks;
+  {
+    const uint64_t w = wave_sum_u64(ks);
+    __syncthreads();
+    if (lane == 0) {
+      sh_lo[wid] = (uint32_t)w;
+      sh_hi[wid] = (uint32_t)(w >> 32);
+    }
+  }
   __syncthreads();
   uint64_t KS = 0;
-  for (int w = 0; w < GNW; w++) KS += sh_q[w];
+  for (int w = 0; w < GNW; w++) KS += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
   const float inv = 1.0f / d3s_fixsum_to_f32(KS);
   float bs = -1.0f;
   int br = 0x7fffffff;
@@ -814,15 +902,7 @@ __global__ __launch_bounds__(GBLOCK) void k_generic(SampleArgs a, int kpow) {
       if (a.cand) a.cand[(size_t)row * k + r] = key_idx(key);
     }
   }
-#pragma unroll
-  for (int o = WAVE / 2; o > 0; o >>= 1) {
-    const float os = __shfl_xor(bs, o);
-    const int ob = __shfl_xor(br, o);
-    if (os > bs || (os == bs && ob < br)) {
-      bs = os;
-      br = ob;
-    }
-  }
+  wave_argmax(bs, br);
   if (lane == 0) {
     sh_best[wid] = bs;
     sh_bestr[wid] = br;
@@ -852,7 +932,7 @@ __global__ void k_math(const float *in, float *oe, float *ol, float *od, uint64_
     const float x = in[i];
     oe[i] = d3s_expf(x);
     ol[i] = d3s_logf(x);
-    od[i] = x / divisor;
+    od[i] = d3s_div_rn(x, divisor, 1.0f / divisor);
     of[i] = d3s_fix40(x);
   }
 }
@@ -877,12 +957,8 @@ int fused_max_vocab(Dtype dt) {
 
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s) {
   if (a.k > KF) return false;
-  const bool wide = a.n_rows < 64; /* few rows: more waves per row for latency */
-  if (dt == DT_F32) {
-    if (!wide && try_fused<256, 5, false>(a, s)) return true;
-    return try_fused<1024, 2, false>(a, s) || try_fused<1024, 4, false>(a, s);
-  }
-  if (!wide && try_fused<256, 3, true>(a, s)) return true;
+  /* 1024 threads per row: a few elements per thread keeps the row's passes short */
+  if (dt == DT_F32) return try_fused<1024, 2, false>(a, s) || try_fused<1024, 4, false>(a, s);
   return try_fused<1024, 1, true>(a, s) || try_fused<1024, 2, true>(a, s) ||
          try_fused<1024, 4, true>(a, s);
 }

@@ -83,18 +83,18 @@ D3S_HD float d3s_from_ordkey(uint32_t k) {
 
 D3S_HD int d3s_isnan(float f) { return (d3s_f2u(f) & 0x7fffffffu) > 0x7f800000u; }
 
-/* e^a, correctly handling NaN, +-inf, overflow and subnormal results. */
+/* e^a, correctly handling NaN, +-inf, overflow and subnormal results.
+ * Branch-free: the main path runs on a clamped argument and the special cases
+ * are selected at the end (divergent branches are costly on a GPU wave). */
 D3S_HD float d3s_expf(float a) {
 #if defined(__clang__)
 #pragma clang fp contract(off)
 #endif
-  if (d3s_isnan(a)) return a;
-  if (a > 0x1.62e430p+6f) return D3S_INF;  /* > 88.7228394: overflows */
-  if (a < -0x1.a0p+6f) return 0.0f;        /* < -104: below half the least subnormal */
-  const float t = a * 0x1.715476p+0f;      /* a * log2(e) */
+  const float ac = fminf(fmaxf(a, -0x1.a0p+6f), 0x1.64p+6f); /* [-104, 89]; NaN -> -104 */
+  const float t = ac * 0x1.715476p+0f;                        /* a * log2(e) */
   /* round to nearest even: exact for |t| < 2^22 */
   const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
-  float r = D3S_FMAF(n, -0x1.62e400p-1f, a);  /* a - n*ln2_hi (exact) */
+  float r = D3S_FMAF(n, -0x1.62e400p-1f, ac); /* a - n*ln2_hi (exact) */
   r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);       /* - n*ln2_lo */
   float p = 0x1.a01a02p-13f;                  /* 1/7! */
   p = D3S_FMAF(p, r, 0x1.6c16c2p-10f);        /* 1/6! */
@@ -104,42 +104,32 @@ D3S_HD float d3s_expf(float a) {
   p = D3S_FMAF(p, r, 0x1.0p-1f);              /* 1/2! */
   p = D3S_FMAF(p, r, 1.0f);
   p = D3S_FMAF(p, r, 1.0f);
-  int ni = (int)n; /* -150 <= ni <= 128 */
+  const int ni = (int)n; /* -150 <= ni <= 128 */
   /* p * 2^ni with one rounding: the first product is exact, the second rounds
    * into the subnormal range (or overflows) when it has to. */
-  float s2 = 1.0f;
-  if (ni < -126) {
-    ni += 127;
-    s2 = 0x1.0p-127f;
-  } else if (ni > 127) {
-    ni -= 1;
-    s2 = 2.0f;
-  }
-  const float s1 = d3s_u2f((uint32_t)(ni + 127) << 23);
-  return (p * s1) * s2;
+  const int lo = ni < -126, hi = ni > 127;
+  const int ns = lo ? ni + 127 : (hi ? ni - 1 : ni);
+  const float s2 = lo ? 0x1.0p-127f : (hi ? 2.0f : 1.0f);
+  float res = (p * d3s_u2f((uint32_t)(ns + 127) << 23)) * s2;
+  res = a > 0x1.62e430p+6f ? D3S_INF : res; /* > 88.7228394: overflows */
+  res = a < -0x1.a0p+6f ? 0.0f : res;       /* < -104: below half the least subnormal */
+  return d3s_isnan(a) ? a : res;
 }
 
-/* natural log, correctly handling NaN, negative, zero, subnormal and +inf. */
+/* natural log, correctly handling NaN, negative, zero, subnormal and +inf;
+ * branch-free like d3s_expf. */
 D3S_HD float d3s_logf(float y) {
 #if defined(__clang__)
 #pragma clang fp contract(off)
 #endif
-  if (d3s_isnan(y)) return y;
-  if (y < 0.0f) return D3S_NAN;
-  if (y == 0.0f) return -D3S_INF;
-  if (y == D3S_INF) return y;
-  uint32_t b = d3s_f2u(y);
-  int e = 0;
-  if (b < 0x00800000u) { /* subnormal: scale into the normal range */
-    b = d3s_f2u(y * 0x1.0p+23f);
-    e = -23;
-  }
-  e += (int)(b >> 23) - 127;
+  const uint32_t b0 = d3s_f2u(y);
+  const int sub = b0 < 0x00800000u; /* +0 or a positive subnormal: scale into the normal range */
+  const uint32_t b = sub ? d3s_f2u(y * 0x1.0p+23f) : b0;
+  int e = (sub ? -23 : 0) + (int)((b >> 23) & 0xffu) - 127;
   float m = d3s_u2f((b & 0x007fffffu) | 0x3f800000u); /* [1, 2) */
-  if (m > 0x1.6a09e6p+0f) {                           /* > sqrt(2) */
-    m = m * 0.5f;
-    e += 1;
-  }
+  const int big = m > 0x1.6a09e6p+0f;                 /* > sqrt(2) */
+  m = big ? m * 0.5f : m;
+  e += big;
   const float f = m - 1.0f; /* exact */
   const float s = f / (2.0f + f);
   const float z = s * s;
@@ -156,7 +146,29 @@ D3S_HD float d3s_logf(float y) {
   const float ef = (float)e;
   float res = D3S_FMAF(ef, 0x1.7f7d1cp-20f, lm); /* + e*ln2_lo */
   res = D3S_FMAF(ef, 0x1.62e400p-1f, res);       /* + e*ln2_hi */
-  return res;
+  res = y == D3S_INF ? D3S_INF : res;
+  res = y == 0.0f ? -D3S_INF : res;
+  res = y < 0.0f ? D3S_NAN : res;
+  return d3s_isnan(y) ? y : res;
+}
+
+/* a / b correctly rounded, given y = RN(1/b) (b finite, nonzero, 2^-126 < |b| < 2^126):
+ * q = RN(a*y) is within one ulp of a/b, the remainder r = a - b*q is exact in
+ * one fused multiply-add, and RN(q + r*y) is RN(a/b) (Markstein, "Computation
+ * of elementary functions on the IBM RISC System/6000 processor", IBM J. Res.
+ * Dev. 34(1), 1990; Muller et al., Handbook of Floating-Point Arithmetic, 2nd
+ * ed., section 5.3).  Operands whose remainder or quotient could leave the
+ * normal range (|a| below 2^-60 or above 2^100, infinities, NaN) take the
+ * division instead; zero is exact either way up to the sign of a zero result. */
+D3S_HD float d3s_div_rn(float a, float b, float y) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  const uint32_t ea = (d3s_f2u(a) >> 23) & 0xffu; /* biased exponent of a */
+  if (ea < 127u - 60u || ea > 127u + 100u) return a / b;
+  const float q = a * y;
+  const float r = D3S_FMAF(-q, b, a);
+  return D3S_FMAF(r, y, q);
 }
 
 /* Fixed-point image of a probability-like term e in [0, 1]: floor(e * 2^40).
@@ -164,15 +176,46 @@ D3S_HD float d3s_logf(float y) {
  * depend on the order the terms are added in. */
 #define D3S_FIX_BITS 40
 D3S_HD uint64_t d3s_fix40(float e) {
-  if (!(e > 0.0f)) return 0; /* 0, -0, negative, NaN */
-  if (e >= 1.0f) return (uint64_t)1 << D3S_FIX_BITS;
   const uint32_t b = d3s_f2u(e);
-  const uint32_t E = b >> 23;
+  const uint32_t E = (b >> 23) & 0xffu;
   const uint64_t m = (uint64_t)((b & 0x007fffffu) | (E ? 0x00800000u : 0u));
-  /* e = m * 2^(max(E,1) - 150), so e * 2^40 = m * 2^(max(E,1) - 110); E <= 126 */
+  /* e = m * 2^(max(E,1) - 150), so e * 2^40 = m * 2^(max(E,1) - 110); the
+   * shifts are clamped so every lane computes both cases without overflow */
   const int sh = 110 - (int)(E ? E : 1u);
-  if (sh <= 0) return m << (-sh); /* at most 16: fits in 40 bits */
-  return sh >= 64 ? 0 : (m >> sh);
+  const uint64_t left = m << (sh < 0 ? (-sh > 16 ? 16 : -sh) : 0); /* e in [2^-17, 1) */
+  const uint64_t right = m >> (sh > 63 ? 63 : (sh > 0 ? sh : 0));
+  uint64_t r = sh <= 0 ? left : right;
+  r = e >= 1.0f ? ((uint64_t)1 << D3S_FIX_BITS) : r;
+  return e > 0.0f ? r : 0; /* 0, -0, negative, NaN */
+}
+
+/* d3s_fix40(d3s_expf(z)) for z <= 0 (or -0, or -inf), without forming the
+ * fp32 result: exp's polynomial value p lies in [2^-1/2, 2^1/2], so p * 2^24
+ * is an integer below 2^25 and floor(p * 2^n * 2^40) is that integer shifted
+ * by n + 16 (results below 2^-126 give 0 either way).  Same bits as the
+ * two-step form; fewer instructions for the per-element row sum. */
+D3S_HD uint64_t d3s_fix40_exp(float z) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  const float zc = fmaxf(z, -0x1.a0p+6f); /* [-104, 0]; -inf -> -104 */
+  const float t = zc * 0x1.715476p+0f;
+  const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
+  float r = D3S_FMAF(n, -0x1.62e400p-1f, zc);
+  r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = D3S_FMAF(p, r, 0x1.6c16c2p-10f);
+  p = D3S_FMAF(p, r, 0x1.111112p-7f);
+  p = D3S_FMAF(p, r, 0x1.555556p-5f);
+  p = D3S_FMAF(p, r, 0x1.555556p-3f);
+  p = D3S_FMAF(p, r, 0x1.0p-1f);
+  p = D3S_FMAF(p, r, 1.0f);
+  p = D3S_FMAF(p, r, 1.0f);
+  const uint64_t P = (uint64_t)(uint32_t)(p * 0x1.0p+24f);
+  const int sh = (int)n + 16; /* <= 16 */
+  const uint64_t left = P << (sh > 0 ? sh : 0);
+  const uint64_t right = P >> (sh < 0 ? (-sh > 63 ? 63 : -sh) : 0);
+  return sh >= 0 ? left : right;
 }
 
 /* uint64 -> fp32, round to nearest, ties to even (integer steps only). */

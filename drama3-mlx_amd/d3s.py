@@ -15,10 +15,9 @@ LIB_PATH = os.path.join(HERE, "libd3sampler.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FLAG_GENERIC = 1
-FLAG_EXACT_LSE = 2
 FLAG_EXACT_SELECT = 4
-COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
-NUM_COUNTERS = 4
+COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT = range(3)
+NUM_COUNTERS = 3
 OK = 0
 
 _lib = None

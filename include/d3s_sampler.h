@@ -30,17 +30,15 @@ extern "C" {
 #define D3S_ERR_DTYPE -4       /* unknown logits dtype */
 
 /* flags for d3s_sample */
-#define D3S_FLAG_GENERIC 1u     /* always the streaming kernel (the reference's
-                                   D3_NO_FUSED_SAMPLER switch, src/sampling.c:197) */
-#define D3S_FLAG_EXACT_LSE 2u   /* fused kernel: always the exact log-sum-exp */
+#define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the reference's
+                                    D3_NO_FUSED_SAMPLER switch, src/sampling.c:197) */
 #define D3S_FLAG_EXACT_SELECT 4u /* fused kernel: always the radix select */
 
 /* counters[] slots, when a counters array is given (atomic per-row increments) */
 #define D3S_COUNTER_REFUSED 0      /* rows with a NaN / +inf x: id -1 */
 #define D3S_COUNTER_ALL_MASKED 1   /* rows whose x are all -inf: id 0 */
 #define D3S_COUNTER_EXACT_SELECT 2 /* fused rows that took the radix select */
-#define D3S_COUNTER_EXACT_LSE 3    /* fused rows that computed the exact log-sum-exp */
-#define D3S_NUM_COUNTERS 4
+#define D3S_NUM_COUNTERS 3
 
 /* One sampled index per row of logits [n_rows, vocab] (row r at
  * logits + r * row_stride elements), with the uniform draws u [n_rows, k]

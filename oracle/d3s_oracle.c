@@ -259,6 +259,11 @@ void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40(in[i]);
 }
 
+void d3s_oracle_div_rn(const float *a, float b, float *out, int64_t n) {
+  const float y = 1.0f / b;
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_div_rn(a[i], b, y);
+}
+
 float d3s_oracle_u64_to_f32(uint64_t v) { return d3s_u64_to_f32(v); }
 
 void d3s_oracle_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {

@@ -66,6 +66,8 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
 void d3s_oracle_expf(const float *in, float *out, int64_t n);
 void d3s_oracle_logf(const float *in, float *out, int64_t n);
 void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n);
+/* out[i] = d3s_div_rn(a[i], b, RN(1/b)), the kernels' division */
+void d3s_oracle_div_rn(const float *a, float b, float *out, int64_t n);
 float d3s_oracle_u64_to_f32(uint64_t v);
 void d3s_oracle_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 /* u[r, j] = d3s_uniform(seed, stream0 + r, j) for r < rows, j < k */

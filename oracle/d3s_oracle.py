@@ -40,6 +40,8 @@ def lib():
         for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
+        L.d3s_oracle_div_rn.argtypes = [vp, f32, vp, i64]
+        L.d3s_oracle_div_rn.restype = None
         L.d3s_oracle_u64_to_f32.argtypes = [ctypes.c_uint64]
         L.d3s_oracle_u64_to_f32.restype = f32
         L.d3s_oracle_philox.argtypes = [vp, vp, vp]
@@ -115,6 +117,13 @@ def fix40(x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.shape, np.uint64)
     lib().d3s_oracle_fix40(_p(x), _p(out), x.size)
+    return out
+
+
+def div_rn(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    out = np.empty_like(a)
+    lib().d3s_oracle_div_rn(_p(a), float(b), _p(out), a.size)
     return out
 
 

@@ -94,7 +94,7 @@ def test_single_row_launches(gpu, oracle):
         assert np.array_equal(got["probs"][0], exp["probs"][r])
 
 
-@pytest.mark.parametrize("flags", [1, 2, 4, 6])
+@pytest.mark.parametrize("flags", [1, 4, 5])
 @pytest.mark.parametrize("name", ["C2", "C3"])
 def test_every_path_gives_the_same_bits(gpu, oracle, name, flags):
     w = W.make(name, rows=64 if name == "C3" else 9, seed=5, uniforms=False)
@@ -116,9 +116,10 @@ def test_ties_fused_equals_generic(gpu, oracle, V, k):
         assert np.array_equal(a["ids"], b["ids"])
 
 
-def test_ambiguous_top_p_takes_the_exact_lse(gpu, oracle):
-    """top_p placed on a row's own cumulative value: the fast sum of exp cannot
-    decide the cut, the kernel recomputes the exact lse and still matches."""
+def test_top_p_on_a_cumulative_boundary(gpu, oracle):
+    """top_p placed one ulp either side of a row's own cumulative value c_j: the
+    cut then depends on the last bit of every term, and the kernel's exact,
+    order-independent row sum still reproduces it."""
     w = W.make("C3", rows=64, seed=9, uniforms=False)
     u = oracle.uniform(9, 0, 64, 30)
     x = w["logits"]
@@ -135,8 +136,8 @@ def test_ambiguous_top_p_takes_the_exact_lse(gpu, oracle):
             cs.append(c)
         j = 1 + r % 5
         top_p[r] = np.nextafter(cs[j], np.float32(0 if r % 2 else 2))
-    got, _ = compare(oracle, gpu, x, u, T, top_p, label="ambiguous top_p")
-    assert got["counters"][gpu.COUNTER_EXACT_LSE] >= 60
+    compare(oracle, gpu, x, u, T, top_p, label="top_p on a boundary")
+    compare(oracle, gpu, x, u, T, top_p, flags=gpu.FLAG_GENERIC, label="top_p on a boundary, generic")
 
 
 def test_edge_rows(gpu, oracle):
@@ -174,7 +175,7 @@ def test_parameter_edges(gpu, oracle, T, top_p):
                                  (16381, 30), (16382, 30), (40000, 64), (40000, 300)])
 def test_shapes(gpu, oracle, V, k):
     rng = np.random.default_rng([V, k])
-    N = 70  # >= 64 rows: the 256-thread instantiations (fewer rows use 1024 threads)
+    N = 70
     x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
     u = oracle.uniform(1, 0, N, k)
     compare(oracle, gpu, x, u, 0.7, 0.8, label=f"V={V}")

@@ -93,6 +93,26 @@ def test_u64_to_f32_round_to_nearest_even(oracle):
         assert oracle.u64_to_f32(v) == float(best), v
 
 
+@pytest.mark.parametrize("b", [0.7, 1.0, 0.3, 1e-5, 1e4, 1.9999999, 1.0000001, 0.99999994, 3.9999998,
+                               1.4142135, 0.123456, 7.0, 1e-3])
+def test_fma_division_is_correctly_rounded(oracle, b):
+    """d3s_div_rn (Markstein's correction step) equals the IEEE division for
+    every significand in [1, 2) and for random operands over its whole range,
+    including the ones it hands to the division (tiny, huge, zero, inf, NaN)."""
+    b = np.float32(b)
+    a = (np.arange(1 << 23, dtype=np.uint32) | np.uint32(0x3F800000)).view(np.float32)
+    got = oracle.div_rn(a, b)
+    assert np.array_equal(got.view(np.uint32), (a / b).view(np.uint32))
+    rng = np.random.default_rng(int(b.view(np.uint32)))
+    bits = rng.integers(0, 2 ** 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    a = bits.view(np.float32)
+    a = np.concatenate([a[np.isfinite(a)], np.float32([0.0, -0.0, 1e-45, -3e-39, np.inf, -np.inf])])
+    got = oracle.div_rn(a, b)
+    ref = a / b
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.isnan(oracle.div_rn(np.float32([np.nan]), b))[0]
+
+
 @pytest.mark.parametrize("ctr,key,expected", [
     # Random123 kat_vectors, philox4x32 with 10 rounds
     ([0, 0, 0, 0], [0, 0], [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
