@@ -42,7 +42,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   if (!logits || !u || !ids) return D3S_ERR_ARG;
   /* rows are addressed in whole elements */
   if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
-  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_SELECT)) != 0u)
+  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT)) != 0u)
     return D3S_ERR_ARG;
   d3s::SampleArgs a;
   a.logits = logits;
@@ -64,6 +64,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
   hipStream_t s = (hipStream_t)stream;
   const bool generic = (flags & D3S_FLAG_GENERIC) || env_no_fused();
+  if (!generic && d3s::launch_wave(a, dt, s)) return launched();
   if (!generic && d3s::launch_fused(a, dt, s)) return launched();
   if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
   return launched();
@@ -89,6 +90,12 @@ int d3s_math_selftest(const float *in, float *out_exp, float *out_log, float *ou
   return n > 0 ? launched() : D3S_OK;
 }
 
-const char *d3s_version(void) { return "d3sampler 0.1 gfx950"; }
+int d3s_exp2_selftest(const float *in, float *out, int64_t n, void *stream) {
+  if (n < 0 || (n > 0 && (!in || !out))) return D3S_ERR_ARG;
+  d3s::launch_exp2_selftest(in, out, n, (hipStream_t)stream);
+  return n > 0 ? launched() : D3S_OK;
+}
+
+const char *d3s_version(void) { return "d3sampler 0.2 gfx950"; }
 
 }  // extern "C"

@@ -33,18 +33,26 @@ struct SampleArgs {
 enum {
   CNT_REFUSED = 0,      /* non-finite x: id -1 */
   CNT_ALL_MASKED = 1,   /* every x -inf */
-  CNT_EXACT_SELECT = 2, /* fused kernel fell back to the radix select */
-  CNT_NUM = 3
+  CNT_EXACT_SELECT = 2, /* fell back to the radix select */
+  CNT_EXACT_LSE = 3,    /* the wave kernel recomputed the row sum exactly */
+  CNT_NUM = 4
 };
 
 /* flags (same values as the public D3S_FLAG_*) */
 enum : unsigned {
   FLAG_GENERIC = 1u,
+  FLAG_EXACT_LSE = 2u,
   FLAG_EXACT_SELECT = 4u,
 };
 
 enum Dtype { DT_F32 = 0, DT_BF16 = 1 };
 
+/* Launch the one-wave-per-row kernel (k <= 64, V <= wave_max_vocab(dt)).
+ * Returns false if no instantiation fits. */
+bool launch_wave(const SampleArgs &a, Dtype dt, hipStream_t s);
+int wave_max_vocab(Dtype dt);
+/* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
+void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
 /* Launch the fused one-workgroup-per-row kernel (k <= 64, V within the
  * register-resident limit).  Returns false if no instantiation fits. */
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);

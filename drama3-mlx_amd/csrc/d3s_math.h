@@ -158,14 +158,16 @@ D3S_HD float d3s_logf(float y) {
  * of elementary functions on the IBM RISC System/6000 processor", IBM J. Res.
  * Dev. 34(1), 1990; Muller et al., Handbook of Floating-Point Arithmetic, 2nd
  * ed., section 5.3).  Operands whose remainder or quotient could leave the
- * normal range (|a| below 2^-60 or above 2^100, infinities, NaN) take the
- * division instead; zero is exact either way up to the sign of a zero result. */
+ * normal range (|a| below 2^-60 or above 2^100, b outside [2^-20, 2^21),
+ * infinities, NaN) take the division instead; zero is exact either way up to
+ * the sign of a zero result. */
 D3S_HD float d3s_div_rn(float a, float b, float y) {
 #if defined(__clang__)
 #pragma clang fp contract(off)
 #endif
   const uint32_t ea = (d3s_f2u(a) >> 23) & 0xffu; /* biased exponent of a */
-  if (ea < 127u - 60u || ea > 127u + 100u) return a / b;
+  const uint32_t eb = (d3s_f2u(b) >> 23) & 0xffu; /* of b (b > 0) */
+  if (ea < 127u - 60u || ea > 127u + 100u || eb < 127u - 20u || eb > 127u + 20u) return a / b;
   const float q = a * y;
   const float r = D3S_FMAF(-q, b, a);
   return D3S_FMAF(r, y, q);

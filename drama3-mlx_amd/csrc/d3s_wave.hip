@@ -1,0 +1,505 @@
+/* The one-wave-per-row sampler kernel (gfx950, wave64): k_wave.
+ *
+ * Each wave samples one row held in its registers (up to 96 fp32 or 128 bf16
+ * elements per lane); a 256-thread workgroup carries four independent rows and has no
+ * workgroup barrier, so a launch of many rows streams at HBM rate while a
+ * launch of one row runs on a single wave.  Semantics are the oracle's
+ * (src/sampling.c:1-3,:22-49,:53-140), bit for bit:
+ *
+ *  1. load the row (16-byte chunks), NaN-propagating max per lane and row:
+ *     refused / all -inf rows as the reference kernel (src/sampling.c:54-79);
+ *     m = max x = RN(max logit / T) (division is monotone).
+ *  2. tau = the k-th largest of the 64 lane maxima (a ballot radix search):
+ *     at least k elements reach it.  tau_lo steps tau down past logits whose
+ *     x ties with tau's x, so {logit >= tau_lo} holds every element whose x
+ *     reaches the k-th largest x: the top k (src/sampling.c:90-121) lie in it.
+ *  3. one pass over the registers: the fast row sum S' = sum 2^(logit*c - h)
+ *     (c = log2(e)/T, v_exp_f32) and the candidates {logit >= tau_lo} into
+ *     lane-private LDS lists.
+ *  4. candidates take their exact x, rank by (x desc, index asc) and the top k
+ *     run the reference kernel's tail (src/sampling.c:123-139) with
+ *     lse' = m + ln S'.  lse only decides the top-p cut (the probabilities use
+ *     exp(x - x_0)), so when every c'_r is farther from top_p than the proven
+ *     bound on |c'_r - c_r| the cut equals the one under the exact lse.
+ *     Otherwise the wave computes the exact row sum (2^-40 fixed point of
+ *     d3s_expf(x - m), as the oracle) and redoes the cumulative.
+ *  Exact fallbacks: more candidates than a wave holds -> 8-bit radix select
+ *  over order-preserving keys of x; T not finite or |m| beyond 2^24 -> every
+ *  quantity per element from x exactly (exact_row).
+ */
+#include "d3s_device.h"
+
+#pragma clang fp contract(off)
+
+namespace d3s {
+namespace {
+
+constexpr int WR = 4;   /* rows (waves) per 256-thread workgroup */
+constexpr int LCAP = 8; /* entries of a lane's private candidate list */
+/* relative error bound of v_exp_f32 (2^x) for every input with a normal
+ * result; the GPU tests check it over dense samples of [-126, 1] */
+constexpr float EPS_EXP2 = 0x1p-21f;
+constexpr float LOG2E_F = 1.44269504f;
+constexpr float LN2_F = 0.693147182f;
+
+struct __align__(16) WaveLds {
+  uint2 lst[LCAP * WAVE]; /* lane-private candidate lists, entry-major: (logit bits, index) */
+  uint64_t keys[WAVE + 1]; /* dense candidate keys (+ a zero pad for pair reads) */
+  uint64_t ranked[WAVE];   /* keys by rank */
+  uint32_t hist[NB];       /* radix-select histogram */
+  float buf[WAVE];         /* sequential sums */
+};
+
+__device__ __forceinline__ float fmaximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+/* wave max that propagates NaN (v_maximum), wave-uniform */
+__device__ __forceinline__ float wave_maximum_f(float v) {
+  const float ninf = -__builtin_inff();
+  v = fmaximum(v, dpp_f<DPP_SHR1, 0xf>(ninf, v));
+  v = fmaximum(v, dpp_f<DPP_SHR2, 0xf>(ninf, v));
+  v = fmaximum(v, dpp_f<DPP_SHR4, 0xf>(ninf, v));
+  v = fmaximum(v, dpp_f<DPP_SHR8, 0xf>(ninf, v));
+  v = fmaximum(v, dpp_f<DPP_BCAST15, 0xa>(ninf, v));
+  v = fmaximum(v, dpp_f<DPP_BCAST31, 0xc>(ninf, v));
+  return readlane_f(v, 63);
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v = v + dpp_f<DPP_SHR1, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR2, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR4, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR8, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_BCAST15, 0xa>(0.0f, v);
+  v = v + dpp_f<DPP_BCAST31, 0xc>(0.0f, v);
+  return readlane_f(v, 63);
+}
+
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+/* A refused row (id -1) or an all -inf row (id 0, ranks 0..k-1); one wave. */
+__device__ __forceinline__ void wave_write_special(const SampleArgs &a, int row, bool masked) {
+  const int lane = lane_id(), k = a.k;
+  if (lane == 0) {
+    a.ids[row] = masked ? 0 : -1;
+    if (a.counters) atomicAdd(&a.counters[masked ? CNT_ALL_MASKED : CNT_REFUSED], 1u);
+  }
+  if (lane < k) {
+    if (a.probs) a.probs[(size_t)row * k + lane] = __builtin_nanf("");
+    if (a.cand) a.cand[(size_t)row * k + lane] = masked ? lane : -1;
+  }
+}
+
+/* What the rare exact paths need of a row; they stream it from memory. */
+struct RowRef {
+  uint32_t *counters;
+  int32_t *ids;
+  float *probs;
+  int32_t *cand;
+  WaveLds *Sp;
+  const char *rowp;
+  int row, V, k, lane, banned;
+  float T, y;
+  bool t_finite, bf16;
+};
+
+/* Element i of the row read again from memory (L2 after the first pass),
+ * as x = L / T: the rare exact paths stream the row instead of keeping
+ * per-element values beside the registers that hold it. */
+__device__ __forceinline__ float gx(const RowRef &R, int i) {
+  float L;
+  if (R.bf16)
+    L = d3s_bf16_to_f32(((const uint16_t *)R.rowp)[i]);
+  else
+    L = ((const float *)R.rowp)[i];
+  return scale_logit(i == R.banned ? -__builtin_inff() : L, R.T, R.y, R.t_finite);
+}
+
+/* ---- exact 8-bit radix select of the top k by (x desc, index asc); writes
+ * exactly k keys to S.keys and returns k */
+__device__ __noinline__ int exact_select(const RowRef &R) {
+  if (R.lane == 0 && R.counters) atomicAdd(&R.counters[CNT_EXACT_SELECT], 1u);
+  WaveLds &S = *R.Sp;
+  uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)R.k;
+  bool done = false;
+  for (int pass = 0; pass < 4 && !done; pass++) {
+    const int shift = 24 - 8 * pass;
+    wave_lds_sync();
+    for (int i = R.lane; i < NB; i += WAVE) S.hist[i] = 0u;
+    wave_lds_sync();
+#pragma unroll 4
+    for (int i = R.lane; i < R.V; i += WAVE) {
+      const uint32_t key = d3s_ordkey(gx(R, i));
+      if ((key & pmask) == prefix) atomicAdd(&S.hist[(key >> shift) & 255u], 1u);
+    }
+    wave_lds_sync();
+    const BinSel b = wave_find_bin<false>(S.hist, need); /* holds >= need */
+    prefix |= b.bin << shift;
+    pmask |= 0xffu << shift;
+    done = b.count == need - b.above;
+    need -= b.above;
+  }
+  /* everything above the group, then the group (all of it when it holds
+   * exactly `need`, else its lowest-index `need`, in index order) */
+  uint32_t base = 0u;
+  for (int t0 = 0; t0 < R.V; t0 += WAVE) {
+    const int i = t0 + R.lane;
+    const float xi = i < R.V ? gx(R, i) : 0.0f;
+    const uint32_t key = d3s_ordkey(xi) & pmask;
+    const bool sel = i < R.V && (key > prefix || (done && key == prefix));
+    const uint64_t m = __ballot(sel);
+    if (sel) S.keys[base + (uint32_t)mbcnt64(m)] = composite_key(xi, i);
+    base += (uint32_t)__popcll(m);
+  }
+  if (!done) {
+    uint32_t ord0 = 0u;
+    for (int t0 = 0; t0 < R.V && ord0 < need; t0 += WAVE) {
+      const int i = t0 + R.lane;
+      const float xi = i < R.V ? gx(R, i) : 0.0f;
+      const bool tie = i < R.V && d3s_ordkey(xi) == prefix;
+      const uint64_t m = __ballot(tie);
+      const uint32_t ord = ord0 + (uint32_t)mbcnt64(m);
+      if (tie && ord < need) S.keys[base + ord] = composite_key(xi, i);
+      ord0 += (uint32_t)__popcll(m);
+    }
+  }
+  return R.k;
+}
+
+/* the exact row sum of the oracle: 2^-40 fixed point of d3s_expf(x - m) */
+__device__ __noinline__ float exact_lse(const RowRef &R, float M) {
+  uint64_t acc = 0;
+#pragma unroll 4
+  for (int i = R.lane; i < R.V; i += WAVE) acc += d3s_fix40(d3s_expf(gx(R, i) - M));
+  return M + d3s_logf(d3s_fixsum_to_f32(wave_sum_u64(acc)));
+}
+
+/* refusal and max of x = L / T element by element (T not finite, or logits
+ * too large for the fast row sum); returns false for a finished row */
+__device__ __noinline__ bool slow_max(const RowRef &R, float &M) {
+  float xm = -__builtin_inff();
+  bool bad = false;
+#pragma unroll 4
+  for (int i = R.lane; i < R.V; i += WAVE) {
+    const float xi = gx(R, i);
+    bad = bad || (classify(xi) & 1u);
+    xm = d3s_isnan(xi) ? xm : fmaxf(xm, xi);
+  }
+  if (__ballot(bad)) return false;
+  M = wave_max_f(xm);
+  return true;
+}
+
+template <int CPT, bool BF16>
+struct WaveRow {
+  static constexpr int ES = BF16 ? 2 : 4;
+  static constexpr int EPC = 16 / ES; /* elements per 16-byte chunk */
+  static constexpr int NV = CPT * EPC;
+
+  const SampleArgs a;
+  WaveLds &S;
+  int row, V, k, lane, pos0, nchunks, banned;
+  const char *rowp;
+  float T, y, uval, top_p;
+  bool t_finite;
+  /* the row as loaded: 16-byte chunks, 4 words each (fp32 bits, or two bf16
+   * halves); -inf outside the row and at the banned index */
+  uint32_t w[CPT * 4];
+
+  __device__ __forceinline__ float val(int i) const {
+    if (BF16) {
+      const uint32_t word = w[(i / EPC) * 4 + (i % EPC) / 2];
+      return d3s_u2f((i & 1) ? (word & 0xffff0000u) : (word << 16));
+    }
+    return d3s_u2f(w[i]);
+  }
+  /* element i becomes -inf when `on` */
+  __device__ __forceinline__ void mask(int i, bool on) {
+    uint32_t &word = w[BF16 ? (i / EPC) * 4 + (i % EPC) / 2 : i];
+    if (BF16)
+      word = on ? ((i & 1) ? ((word & 0x0000ffffu) | 0xff800000u) : ((word & 0xffff0000u) | 0x0000ff80u)) : word;
+    else
+      word = on ? 0xff800000u : word;
+  }
+
+  __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
+
+  /* element i: chunk row j = i / EPC (chunk j * 64 + lane), lane-in-chunk e = i % EPC;
+   * index order is (j, lane, e) */
+  __device__ __forceinline__ int pos(int i) const { return pos0 + (i / EPC) * WAVE * EPC + (i % EPC); }
+  __device__ __forceinline__ bool valid(int i) const { return (unsigned)pos(i) < (unsigned)V; }
+  /* chunk row j holds part of the row in some lane (wave-uniform) */
+  __device__ __forceinline__ bool live(int j) const { return j * WAVE < nchunks; }
+
+  __device__ __forceinline__ void load() {
+    const RowP rp = row_params(a, row);
+    T = rp.T;
+    top_p = rp.top_p;
+    t_finite = T < __builtin_inff(); /* false for +inf and NaN */
+    y = 1.0f / T;
+    uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
+    /* 16-byte chunks from the aligned address at or below the row start: a
+     * chunk never crosses a page, so the bytes outside the row it covers are
+     * readable; they become -inf below */
+    rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
+    banned = rp.banned;
+    const int off = (int)(((uintptr_t)rowp & 15u) / ES);
+    const uint4 *src = (const uint4 *)(rowp - off * ES);
+    nchunks = (off + V + EPC - 1) / EPC;
+    pos0 = lane * EPC - off;
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+      const uint4 q = src[min(j * WAVE + lane, nchunks - 1)]; /* past the row: masked below */
+      w[4 * j] = q.x;
+      w[4 * j + 1] = q.y;
+      w[4 * j + 2] = q.z;
+      w[4 * j + 3] = q.w;
+    }
+    /* the partial chunk at the row start and every chunk row from the one
+     * holding the row end on */
+    const int jlast = (nchunks - 1) / WAVE;
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      if ((j == 0 && off != 0) || j >= jlast) {
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          const int i = j * EPC + e;
+          mask(i, !valid(i));
+        }
+      }
+    if ((unsigned)rp.banned < (unsigned)V) {
+      const int bp = rp.banned + off;
+      const int jb = bp / (WAVE * EPC), lb = (bp / EPC) % WAVE, eb = bp % EPC;
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if (j == jb) {
+#pragma unroll
+          for (int e = 0; e < EPC; e++) mask(j * EPC + e, lane == lb && e == eb);
+        }
+    }
+  }
+
+  __device__ __forceinline__ void run() {
+    load();
+    const float ninf = -__builtin_inff();
+    /* slow: every quantity per element from x = L / T, as the oracle (T not
+     * finite, or logits too large for the fast row sum) */
+    bool slow = !t_finite;
+    float M = 0.0f, lse = 0.0f, eps_s = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
+    if (!slow) {
+      /* ---- row max of the logits; NaN propagates */
+#pragma unroll
+      for (int i = 0; i < NV; i++) lm = fmaximum(lm, val(i));
+      const float Lmax = wave_maximum_f(lm);
+      if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
+        wave_write_special(a, row, false);
+        return;
+      }
+      M = scale_logit(Lmax, T, y, true); /* = max x */
+      if (M == __builtin_inff()) {
+        wave_write_special(a, row, false);
+        return;
+      }
+      if (M == ninf) {
+        wave_write_special(a, row, true);
+        return;
+      }
+      cf = LOG2E_F / T;
+      const float h = Lmax * cf;
+      slow = !(fabsf(h) < 0x1p24f);
+      b = -h;
+      delta = __builtin_fmaf(Lmax, cf, b); /* Lmax * cf + b exactly */
+    }
+    const RowRef R{a.counters, a.ids, a.probs, a.cand, &S, rowp, row, V, k, lane, banned, T, y, t_finite, BF16};
+    if (slow) {
+      if (!slow_max(R, M)) {
+        wave_write_special(a, row, false);
+        return;
+      }
+      if (M == ninf) {
+        wave_write_special(a, row, true);
+        return;
+      }
+    }
+    bool need_sel = slow || (a.flags & FLAG_EXACT_SELECT) != 0;
+    int n = 0;
+    if (!slow) {
+      /* ---- tau: the k-th largest lane max (its key), by ballot radix search */
+      const uint32_t lkey = d3s_ordkey(lm);
+      uint32_t pre = 0u;
+#pragma unroll
+      for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t cnd = pre | (1u << bit);
+        if (__popcll(__ballot(lkey >= cnd)) >= (uint32_t)k) pre = cnd;
+      }
+      float tau_lo = __builtin_inff();
+      const float tau = d3s_from_ordkey(pre);
+      if (tau == ninf) {
+        need_sel = true;
+      } else if (!need_sel) {
+        /* tau_lo: the least logit whose x equals tau's x */
+        const float xt = scale_logit(tau, T, y, true);
+        uint32_t lo = pre;
+        int s = 0;
+        for (; s < 8; s++) {
+          if (scale_logit(d3s_from_ordkey(lo - 1u), T, y, true) != xt) break;
+          lo -= 1u;
+        }
+        if (s == 8)
+          need_sel = true;
+        else
+          tau_lo = d3s_from_ordkey(lo);
+      }
+
+      /* ---- one pass: the fast row sum and the candidates */
+      float acc[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if (live(j)) {
+#pragma unroll
+          for (int e = 0; e < EPC; e++) {
+            const float v = val(j * EPC + e);
+            acc[e] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
+            if (v >= tau_lo) {
+              S.lst[min(cnt, LCAP - 1) * WAVE + lane] =
+                  make_uint2(d3s_f2u(v), (uint32_t)(pos0 + j * WAVE * EPC + e));
+              cnt++;
+            }
+          }
+        }
+#pragma unroll
+      for (int w = EPC / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
+      const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
+      lse = M + (d3s_logf(sp) - delta * LN2_F);
+      /* relative error bound of 2^-delta S' against the exact row sum: the
+       * rounding of x, m, x - m and log2(e)/T, the fast exponent's error,
+       * d3s_expf's, the terms below e^-40, the fixed-point truncation, and
+       * the accumulation (CPT + 3 + 6 roundings) and the final rounding */
+      eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
+              (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
+
+      const uint32_t tot = wave_sum_u32((uint32_t)cnt);
+      if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
+      if (!need_sel) {
+        const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
+#pragma unroll 1
+        for (int e = 0; e < LCAP; e++) {
+          if (!__ballot(e < cnt)) break;
+          if (e < cnt) {
+            const uint2 p = S.lst[e * WAVE + lane];
+            S.keys[excl + e] = composite_key(scale_logit(d3s_u2f(p.x), T, y, true), (int)p.y);
+          }
+        }
+        n = (int)tot;
+      }
+    }
+    if (need_sel) n = exact_select(R);
+
+    /* ---- rank the n >= k candidates by key */
+    if (lane == 0) S.keys[n] = 0ull; /* pad for the pair reads; below every key */
+    wave_lds_sync();
+    const uint64_t my = lane < n ? S.keys[lane] : 0ull;
+    int rank = 0;
+    const ulonglong2 *k2 = (const ulonglong2 *)S.keys;
+#pragma unroll 4
+    for (int j2 = 0; j2 < (n + 1) / 2; j2++) {
+      const ulonglong2 q = k2[j2];
+      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
+    }
+    if (lane < n && rank < k) S.ranked[rank] = my;
+    wave_lds_sync();
+    const bool act = lane < k;
+    const uint64_t key = act ? S.ranked[lane] : 0ull;
+    const float v = key_x(key);
+    const int idx = key_idx(key);
+
+    /* ---- the cumulative c_r (src/sampling.c:126-127).  With the fast lse,
+     * |c'_r - c_r| <= c'_r * (eps_e + (2k + 2) 2^-24), eps_e bounding the
+     * relative change of a term exp(v - lse) between the two lse values; the
+     * exact row sum is computed when a cut could fall differently. */
+    bool exact = slow || (a.flags & FLAG_EXACT_LSE) != 0;
+    float c = 0.0f;
+    if (!exact) {
+      c = wave_seq_cumsum(act ? d3s_expf(v - lse) : 0.0f, k, S.buf);
+      const float D = wave_max_f(act ? lse - v : 0.0f);
+      const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
+      const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
+      const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+      exact = __ballot(act && lane > 0 && fabsf(c - top_p) <= B * c + 0x1p-60f) != 0ull;
+    }
+    if (exact) {
+      if (!slow && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+      const float lx = exact_lse(R, M);
+      c = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
+    }
+    const float ep = act ? d3s_expf(v - M) : 0.0f; /* x_0 = m */
+    const float noise = -d3s_logf(1.0f - uval);
+    wave_race(a, row, idx, c, ep, noise, top_p, S.buf);
+  }
+};
+
+/* waves per SIMD the register budget is set for: the row's 4 * CPT
+ * registers plus about 45 */
+template <int CPT, bool BF16>
+constexpr int wave_occupancy() {
+  return CPT <= 9 ? 5 : CPT <= 17 ? 4 : 3;
+}
+
+template <int CPT, bool BF16>
+__global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
+void k_wave(SampleArgs a) {
+  __shared__ WaveLds lds_all[WR];
+  /* wave-uniform (the compiler cannot see it): row and all that follows stay scalar */
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int row = (int)blockIdx.x * WR + wid;
+  if (row >= a.n_rows) return;
+  WaveRow<CPT, BF16> r(a, lds_all[wid], row);
+  r.V = a.vocab;
+  r.k = a.k;
+  r.lane = lane_id();
+  r.run();
+}
+
+__global__ void k_exp2(const float *in, float *out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __builtin_amdgcn_exp2f(in[i]);
+}
+
+template <int CPT, bool BF16>
+constexpr int wave_vmax() {
+  return WAVE * CPT * (16 / (BF16 ? 2 : 4)) - (16 / (BF16 ? 2 : 4) - 1);
+}
+
+template <int CPT, bool BF16>
+bool try_wave(const SampleArgs &a, hipStream_t s) {
+  if (a.vocab > wave_vmax<CPT, BF16>()) return false;
+  const unsigned blocks = (unsigned)((a.n_rows + WR - 1) / WR);
+  hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3(blocks), dim3(WAVE * WR), 0, s, a);
+  return true;
+}
+
+}  // namespace
+
+int wave_max_vocab(Dtype dt) { return dt == DT_F32 ? wave_vmax<24, false>() : wave_vmax<16, true>(); }
+
+void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  const int B = 256;
+  hipLaunchKernelGGL(k_exp2, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, in, out, n);
+}
+
+bool launch_wave(const SampleArgs &a, Dtype dt, hipStream_t s) {
+  if (a.k > KF) return false;
+  if (dt == DT_F32)
+    return try_wave<4, false>(a, s) || try_wave<8, false>(a, s) || try_wave<17, false>(a, s) ||
+           try_wave<24, false>(a, s);
+  return try_wave<4, true>(a, s) || try_wave<9, true>(a, s) || try_wave<16, true>(a, s);
+}
+
+}  // namespace d3s

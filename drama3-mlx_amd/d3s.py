@@ -15,9 +15,10 @@ LIB_PATH = os.path.join(HERE, "libd3sampler.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FLAG_GENERIC = 1
+FLAG_EXACT_LSE = 2
 FLAG_EXACT_SELECT = 4
-COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT = range(3)
-NUM_COUNTERS = 3
+COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
+NUM_COUNTERS = 4
 OK = 0
 
 _lib = None
@@ -43,6 +44,8 @@ def lib():
         L.d3s_fused_max_vocab.restype = i32
         L.d3s_math_selftest.argtypes = [vp, vp, vp, vp, vp, i64, f32, vp]
         L.d3s_math_selftest.restype = i32
+        L.d3s_exp2_selftest.argtypes = [vp, vp, i64, vp]
+        L.d3s_exp2_selftest.restype = i32
         L.d3s_version.argtypes = []
         L.d3s_version.restype = ctypes.c_char_p
         L.d3_sample.argtypes = [vp, i32, i32, f32, i32, f32, ctypes.c_ulonglong, vp]
@@ -138,6 +141,18 @@ def math_selftest(x, divisor):
     hiprt.synchronize()
     return (be.download((n,), np.float32), bl.download((n,), np.float32),
             bd.download((n,), np.float32), bf.download((n,), np.uint64))
+
+
+def exp2_selftest(x):
+    """The hardware 2^x (v_exp_f32) behind the wave kernel's fast row sum."""
+    import hiprt
+    x = np.ascontiguousarray(x, np.float32)
+    bi, bo = hiprt.to_device(x), hiprt.DeviceBuffer(4 * x.size)
+    rc = lib().d3s_exp2_selftest(bi.ptr, bo.ptr, x.size, None)
+    if rc != OK:
+        raise RuntimeError(f"d3s_exp2_selftest: {rc}")
+    hiprt.synchronize()
+    return bo.download((x.size,), np.float32)
 
 
 def d3_sample(logits, temperature, top_k, top_p, seed):

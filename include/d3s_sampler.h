@@ -32,13 +32,17 @@ extern "C" {
 /* flags for d3s_sample */
 #define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the reference's
                                     D3_NO_FUSED_SAMPLER switch, src/sampling.c:197) */
-#define D3S_FLAG_EXACT_SELECT 4u /* fused kernel: always the radix select */
+#define D3S_FLAG_EXACT_LSE 2u    /* register kernels: always compute the exact row
+                                    sum (by default only rows whose top-p cut it
+                                    could change) */
+#define D3S_FLAG_EXACT_SELECT 4u /* register kernels: always the radix select */
 
 /* counters[] slots, when a counters array is given (atomic per-row increments) */
 #define D3S_COUNTER_REFUSED 0      /* rows with a NaN / +inf x: id -1 */
 #define D3S_COUNTER_ALL_MASKED 1   /* rows whose x are all -inf: id 0 */
-#define D3S_COUNTER_EXACT_SELECT 2 /* fused rows that took the radix select */
-#define D3S_NUM_COUNTERS 3
+#define D3S_COUNTER_EXACT_SELECT 2 /* rows that took the radix select */
+#define D3S_COUNTER_EXACT_LSE 3    /* rows that took the exact row sum */
+#define D3S_NUM_COUNTERS 4
 
 /* One sampled index per row of logits [n_rows, vocab] (row r at
  * logits + r * row_stride elements), with the uniform draws u [n_rows, k]
@@ -80,6 +84,11 @@ int d3s_fused_max_vocab(int dtype);
  * image), elementwise over in[0..n), for bit-exact comparison with the CPU. */
 int d3s_math_selftest(const float *in, float *out_exp, float *out_log, float *out_div,
                       uint64_t *out_fix, int64_t n, float divisor, void *stream);
+
+/* Diagnostic, no counterpart in the reference: out[i] = the hardware 2^in[i]
+ * (v_exp_f32) behind the fast row sum, whose error bound the kernel's top-p
+ * margin relies on (checked by the tests). */
+int d3s_exp2_selftest(const float *in, float *out, int64_t n, void *stream);
 
 /* "d3sampler <version> gfx950" */
 const char *d3s_version(void);

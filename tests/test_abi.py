@@ -71,7 +71,8 @@ def test_argument_validation_without_device(lib):
     assert d3s.sample_raw(**{**base, "n_rows": -1}) == -1
     assert d3s.sample_raw(**{**base, "ids": None}) == -1
     assert d3s.sample_raw(**{**base, "flags": 64}) == -1
-    assert d3s.sample_raw(**{**base, "flags": 2}) == -1
+    assert d3s.sample_raw(**{**base, "flags": 8}) == -1
+    assert d3s.sample_raw(**{**base, "flags": 2 | 64}) == -1
     big = dict(base, vocab=20000, row_stride=20000, k=16385)
     assert d3s.sample_raw(**big) == -2
     assert d3s.sample_raw(**{**base, "n_rows": 0}) == 0  # nothing to do, nothing launched

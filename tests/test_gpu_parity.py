@@ -70,6 +70,28 @@ def test_device_math_is_bit_exact(gpu, oracle):
         assert np.array_equal(f, oracle.fix40(x))
 
 
+EPS_EXP2 = 2.0 ** -21  # the bound the wave kernel's top-p margin assumes for v_exp_f32
+
+
+def test_hardware_exp2_error_bound(gpu):
+    """The wave kernel's fast row sum uses the hardware 2^x; its margin test
+    assumes a relative error below 2^-21 wherever the result is normal.  Dense
+    grid over [-126, 1], every float in [-1, 0] near the grid, random points."""
+    rng = np.random.default_rng(21)
+    t = np.concatenate([np.linspace(-126, 1, 1 << 22, dtype=np.float32),
+                        rng.uniform(-126, 1, 1 << 22).astype(np.float32),
+                        (np.arange(-(1 << 20), 0, dtype=np.int64) + 0x3f800000).astype(np.uint32)
+                        .view(np.float32) * np.float32(-1),
+                        np.array([0.0, -0.0, 1.0, -1.0, -126.0, 0.5, -0.5], np.float32)])
+    got = gpu.exp2_selftest(t).astype(np.float64)
+    ref = np.exp2(t.astype(np.float64))
+    ok = ref >= 2.0 ** -126
+    rel = np.abs(got[ok] - ref[ok]) / ref[ok]
+    banner(f"v_exp_f32: max relative error {rel.max():.3e} over {ok.sum()} inputs")
+    assert rel.max() < EPS_EXP2
+    assert gpu.exp2_selftest(np.array([-np.inf], np.float32))[0] == 0.0
+
+
 def test_uniform_fill_matches_host(gpu, oracle):
     u = gpu.uniform_fill(100_003, 42, 7)
     assert np.array_equal(u, oracle.uniform(42, 7, 1, 100_003)[0])
@@ -94,7 +116,7 @@ def test_single_row_launches(gpu, oracle):
         assert np.array_equal(got["probs"][0], exp["probs"][r])
 
 
-@pytest.mark.parametrize("flags", [1, 4, 5])
+@pytest.mark.parametrize("flags", [1, 2, 4, 6, 5])
 @pytest.mark.parametrize("name", ["C2", "C3"])
 def test_every_path_gives_the_same_bits(gpu, oracle, name, flags):
     w = W.make(name, rows=64 if name == "C3" else 9, seed=5, uniforms=False)
@@ -136,8 +158,27 @@ def test_top_p_on_a_cumulative_boundary(gpu, oracle):
             cs.append(c)
         j = 1 + r % 5
         top_p[r] = np.nextafter(cs[j], np.float32(0 if r % 2 else 2))
-    compare(oracle, gpu, x, u, T, top_p, label="top_p on a boundary")
+    got, _ = compare(oracle, gpu, x, u, T, top_p, label="top_p on a boundary")
+    # every row is within the wave kernel's margin: each takes the exact row sum
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] == 64
     compare(oracle, gpu, x, u, T, top_p, flags=gpu.FLAG_GENERIC, label="top_p on a boundary, generic")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_many_rows_per_row_parameters(gpu, oracle, bf16):
+    """1001 rows (four rows per workgroup, a ragged last workgroup), a
+    different temperature and top_p on every row."""
+    rng = np.random.default_rng(14)
+    x = (rng.standard_normal((1001, 4097)) * 2.5).astype(np.float32)
+    x[np.arange(1001), rng.integers(0, 4097, 1001)] += 8.0
+    T = rng.uniform(0.2, 1.5, 1001).astype(np.float32)
+    top_p = rng.uniform(0.3, 1.0, 1001).astype(np.float32)
+    u = oracle.uniform(14, 0, 1001, 30)
+    if bf16:
+        x = W.f32_to_bf16_bits(x)
+    got, _ = compare(oracle, gpu, x, u, T, top_p, label="1001 rows")
+    # the fast row sum settles almost every row
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] < 50
 
 
 def test_edge_rows(gpu, oracle):
