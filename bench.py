@@ -1,15 +1,15 @@
 """Benchmark of the MI355X token sampler on BASELINE.json's configurations.
 
 Headline (`value`): sampled rows/s on C3, the batched backbone head
-(fp32 [256, 4097], per-row T/top_p, k = 30), one d3s_sample launch per batch
-of 256 rows, batches rotating over a pool larger than 512 MB so every launch
-reads HBM rather than the 256 MB Infinity Cache.  `--streams S` spreads the
-batches over S HIP streams (independent batches in flight, as a server would
-have); the single-stream rate is reported beside it.
+(fp32 [256, 4097], per-row T/top_p, k = 30) in steady state: a persistent
+multi-batch launch, `--batches-per-launch` batches of 256 rows per d3s_sample
+call, back to back on one stream, rotating over a pool larger than 512 MB so
+every launch reads HBM rather than the 256 MB Infinity Cache.  Beside it: one
+batch per launch on one stream and on `--streams` streams.
 
-roofline.achieved = algorithmic bytes per launch (16 524 B per row)
-divided by the kernel's mean duration, timed with HIP events around each
-launch on its own stream.  cpu_baseline = the C oracle (the port of the
+roofline.achieved = algorithmic bytes per launch (16 524 B per row) divided by
+the mean launch duration, timed with HIP events on the launching stream
+around the back-to-back launches.  cpu_baseline = the C oracle (the port of the
 reference semantics; the reference's own CPU path needs mlx-c, absent here)
 on a bounded sample of the same workload, all host cores.
 Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32).
@@ -37,49 +37,54 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_pool(n_batches, n_distinct):
-    """n_batches device batches of C3 (fp32 [256, 4097]) cycling over
-    n_distinct generated batches, each with its own device uniforms."""
-    import d3s
-    import d3s_workloads as W
-    import hiprt
-    batches = []
-    distinct = [W.make("C3", rows=ROWS, seed=1000 + i, uniforms=False) for i in range(n_distinct)]
-    for b in range(n_batches):
-        w = distinct[b % n_distinct]
-        lg = hiprt.to_device(w["logits"])
-        u = hiprt.DeviceBuffer(4 * ROWS * K)
-        assert d3s.lib().d3s_uniform_fill(u.ptr, ROWS * K, 42, b, None) == 0
-        batches.append((lg, u))
-    params = (hiprt.to_device(distinct[0]["temperature"]), hiprt.to_device(distinct[0]["top_p"]))
-    hiprt.synchronize()
-    return batches, params
+class Pool:
+    """n_batches C3 batches (fp32 [256, 4097] each) in one contiguous device
+    buffer, cycling over n_distinct generated batches, each batch with its own
+    device uniforms (draw b) and the per-row T / top_p of C3."""
+
+    def __init__(self, n_batches, n_distinct):
+        import d3s
+        import d3s_workloads as W
+        import hiprt
+        self.n = n_batches
+        distinct = [W.make("C3", rows=ROWS, seed=1000 + i, uniforms=False) for i in range(n_distinct)]
+        self.logits = hiprt.DeviceBuffer(n_batches * ROWS * V * 4)
+        for b in range(n_batches):
+            self.logits.upload(distinct[b % n_distinct]["logits"], offset=b * ROWS * V * 4)
+        self.u = hiprt.DeviceBuffer(n_batches * ROWS * K * 4)
+        for b in range(n_batches):
+            assert d3s.lib().d3s_uniform_fill(self.u.ptr + b * ROWS * K * 4, ROWS * K, 42, b, None) == 0
+        self.T = hiprt.to_device(np.tile(distinct[0]["temperature"], n_batches))
+        self.top_p = hiprt.to_device(np.tile(distinct[0]["top_p"], n_batches))
+        hiprt.synchronize()
+
+    def launch(self, b, g, ids, stream):
+        """one d3s_sample call over batches b .. b+g-1 (g * 256 rows)"""
+        import d3s
+        r0 = b * ROWS
+        return d3s.sample_raw(self.logits.ptr + r0 * V * 4, d3s.DTYPE_F32, g * ROWS, V, V,
+                              self.u.ptr + r0 * K * 4, K, ("ptr", self.T.ptr + r0 * 4),
+                              ("ptr", self.top_p.ptr + r0 * 4), None, ids.ptr, stream=stream)
 
 
-def launch(batch, params, ids, stream):
-    import d3s
-    lg, u = batch
-    return d3s.sample_raw(lg.ptr, d3s.DTYPE_F32, ROWS, V, V, u.ptr, K, ("ptr", params[0].ptr),
-                          ("ptr", params[1].ptr), None, ids.ptr, stream=stream)
-
-
-def time_throughput(batches, params, steps, warmup, n_streams):
+def time_batches(pool, batches, warmup, g, n_streams):
+    """`batches` batches, g per launch, round robin over n_streams streams;
+    returns (device ms between the first and last event, host wall s)."""
     import hiprt
     streams = [hiprt.Stream() for _ in range(n_streams)]
-    ids = [hiprt.DeviceBuffer(4 * ROWS) for _ in range(n_streams)]
-    nb = len(batches)
-    for i in range(warmup):
+    ids = [hiprt.DeviceBuffer(4 * ROWS * g) for _ in range(n_streams)]
+    windows = pool.n // g
+    for i in range(max(1, warmup // g)):
         s = i % n_streams
-        assert launch(batches[i % nb], params, ids[s], streams[s].ptr) == 0
+        assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
     hiprt.synchronize()
+    launches = max(1, batches // g)
     start, stop = hiprt.Event(), hiprt.Event()
     t0 = time.perf_counter()
     start.record(streams[0])
-    # every stream waits for `start` implicitly through the device sync above;
-    # the end is the last stream's event after all streams are joined
-    for i in range(steps):
+    for i in range(launches):
         s = i % n_streams
-        assert launch(batches[i % nb], params, ids[s], streams[s].ptr) == 0
+        assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
     for st in streams[1:]:
         st.synchronize()
     stop.record(streams[0])
@@ -89,48 +94,34 @@ def time_throughput(batches, params, steps, warmup, n_streams):
     hiprt.synchronize()
     for st in streams:
         st.destroy()
-    return ms, wall
+    return ms, wall, launches
 
 
-def time_kernel(batches, params, n):
-    """Mean duration of one launch: n launches back to back on one stream,
-    bracketed by HIP events recorded on that stream.  This is what a kernel
-    trace reports as the kernel's duration plus the dispatch gap between two
-    launches, so it is an upper bound of the traced mean."""
-    import hiprt
-    s = hiprt.Stream()
-    ids = hiprt.DeviceBuffer(4 * ROWS)
-    nb = len(batches)
-    for i in range(50):
-        assert launch(batches[i % nb], params, ids, s.ptr) == 0
-    a, b = hiprt.Event(), hiprt.Event()
-    a.record(s)
-    for i in range(n):
-        assert launch(batches[i % nb], params, ids, s.ptr) == 0
-    b.record(s)
-    b.synchronize()
-    mean = a.elapsed_ms(b) * 1e3 / n
-    a.destroy()
-    b.destroy()
-    s.destroy()
-    return float(mean)
+def time_kernel(pool, g, n):
+    """Mean duration of one g-batch launch: n launches back to back on one
+    stream, bracketed by HIP events recorded on that stream.  This is what a
+    kernel trace reports as the kernel's duration plus the dispatch gap
+    between two launches, so it is an upper bound of the traced mean."""
+    ms, _, launches = time_batches(pool, n * g, 50 * g, g, 1)
+    return ms * 1e3 / launches
 
 
-def traffic_probe(batches, params, n):
+def traffic_probe(pool, g, n):
     """For rocprofv3 --pmc runs: one 256 MiB device-to-device copy (the
     calibration dispatch of known traffic: 256 MiB read, 256 MiB written),
-    then n C3 launches on one stream."""
+    then n launches of g C3 batches on one stream."""
     import hiprt
     nbytes = 256 << 20
     src, dst = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
     hiprt.synchronize()
     hiprt.check(hiprt.hip().hipMemcpyAsync(dst.ptr, src.ptr, nbytes, hiprt.D2D, None), "copy")
     hiprt.synchronize()
-    ids = hiprt.DeviceBuffer(4 * ROWS)
+    ids = hiprt.DeviceBuffer(4 * ROWS * g)
     for i in range(n):
-        assert launch(batches[i % len(batches)], params, ids, None) == 0
+        assert pool.launch((i % (pool.n // g)) * g, g, ids, None) == 0
     hiprt.synchronize()
-    log(f"traffic probe: 1 copy of {nbytes} B, {n} C3 launches")
+    log(f"traffic probe: 1 copy of {nbytes} B, {n} launches of {g} C3 batches")
+
 
 def launch_floor(n):
     """Events around a near-empty launch (the uniform fill of 64 values): the
@@ -209,15 +200,18 @@ def cpu_baseline(seconds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20000)
-    ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--streams", type=int, default=4)
+    ap.add_argument("--steps", type=int, default=20480, help="C3 batches timed")
+    ap.add_argument("--warmup", type=int, default=512, help="C3 batches before timing")
+    ap.add_argument("--batches-per-launch", type=int, default=16,
+                    help="C3 batches one d3s_sample call carries in the headline figure")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="streams for the one-batch-per-launch figure beside the headline")
     ap.add_argument("--pool-batches", type=int, default=128)
     ap.add_argument("--single-rows", type=int, default=10000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="N",
-                    help="only run the copy calibration and N C3 launches (for --pmc runs)")
+                    help="only run the copy calibration and N headline launches (for --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -230,25 +224,34 @@ def main():
         sys.exit(1)
     import d3s
     d3s.lib()
+    G = args.batches_per_launch
+    if args.pool_batches % G:
+        sys.exit("bench.py: --pool-batches must be a multiple of --batches-per-launch")
 
     log("building the C3 batch pool")
-    batches, params = build_pool(args.pool_batches, 16)
+    pool = Pool(args.pool_batches, 16)
     pool_mb = args.pool_batches * ROWS * BYTES_PER_ROW / 1e6
     log(f"pool: {args.pool_batches} batches, {pool_mb:.0f} MB")
     if args.traffic_probe:
-        traffic_probe(batches, params, args.traffic_probe)
+        traffic_probe(pool, G, args.traffic_probe)
         return
-    ms, wall = time_throughput(batches, params, args.steps, args.warmup, args.streams)
-    value = args.steps * ROWS / (ms * 1e-3)
-    log(f"throughput: {args.steps} launches on {args.streams} streams in {ms:.2f} ms "
-        f"({value:.3e} rows/s, host wall {wall:.3f} s)")
-    ms1, _ = time_throughput(batches, params, min(args.steps, 5000), 100, 1)
-    single_stream = min(args.steps, 5000) * ROWS / (ms1 * 1e-3)
-    log(f"single stream: {single_stream:.3e} rows/s ({ms1 / min(args.steps, 5000) * 1e3:.2f} us/launch)")
-    kmean = time_kernel(batches, params, 2000)
-    bytes_per_launch = ROWS * BYTES_PER_ROW
+    # headline: G batches per launch, back to back on one stream
+    ms, wall, launches = time_batches(pool, args.steps, args.warmup, G, 1)
+    batches = launches * G
+    value = batches * ROWS / (ms * 1e-3)
+    kmean = ms * 1e3 / launches
+    bytes_per_launch = G * ROWS * BYTES_PER_ROW
     achieved = bytes_per_launch / (kmean * 1e-6) / 1e9
-    log(f"kernel: {kmean:.2f} us per launch back to back on one stream -> {achieved:.0f} GB/s")
+    log(f"steady state: {batches} batches in {launches} launches of {G} in {ms:.2f} ms: "
+        f"{value:.3e} rows/s, {kmean:.2f} us per launch -> {achieved:.0f} GB/s (host wall {wall:.3f} s)")
+    # one batch per launch, one stream and several
+    n1 = min(args.steps, 5000)
+    ms1, _, l1 = time_batches(pool, n1, 100, 1, 1)
+    single = l1 * ROWS / (ms1 * 1e-3)
+    log(f"one batch per launch, one stream: {single:.3e} rows/s ({ms1 * 1e3 / l1:.2f} us/launch)")
+    msS, _, lS = time_batches(pool, n1, 100, 1, args.streams)
+    multi = lS * ROWS / (msS * 1e-3)
+    log(f"one batch per launch, {args.streams} streams: {multi:.3e} rows/s")
     floor_us = launch_floor(500)
     log(f"empty-launch floor (events): {floor_us:.2f} us")
     lat = None
@@ -258,7 +261,9 @@ def main():
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_C3.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+        t = json.load(open(tpath))
+        if t.get("batches_per_launch") == G:
+            traffic = t.get("hbm_bytes_per_launch")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -269,9 +274,9 @@ def main():
         "value": value,
         "unit": "rows/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": batches,
         "warmup": args.warmup,
-        "ms_per_step": ms / args.steps,
+        "ms_per_step": ms / batches,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -280,14 +285,18 @@ def main():
         "config": {"workload": "C3 batched backbone head: fp32 logits [256,4097], N(0,2.5) + 1-8 "
                                "peaks, rows 0-127 T 0.7/top_p 0.7, rows 128-255 T 1.0/top_p 0.9, "
                                "top_k 30, per-row Philox uniforms",
-                   "global_batch": ROWS, "vocab": V, "k": K, "streams": args.streams,
-                   "pool_MB": round(pool_mb), "step": "one d3s_sample launch over one batch"},
+                   "global_batch": ROWS, "vocab": V, "k": K, "pool_MB": round(pool_mb),
+                   "step": "one batch of 256 rows",
+                   "steady_state": f"persistent multi-batch launch: {G} batches per d3s_sample call, "
+                                   "back to back on one stream",
+                   "batches_per_launch": G},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel_us_mean": kmean,
-                     "bytes_per_launch": bytes_per_launch},
+                     "kernel_us_mean": kmean, "bytes_per_launch": bytes_per_launch,
+                     "kernel": "k_wave<17, fp32>"},
         "cpu_baseline": cpu,
-        "single_stream_rows_per_s": single_stream,
+        "one_batch_per_launch": {"rows_per_s": single, "us_per_launch": ms1 * 1e3 / l1,
+                                 "rows_per_s_streams": multi, "streams": args.streams},
         "p50_us_single_row": lat["p50_us"] if lat else None,
         "event_floor_us": floor_us,
         "single_row": lat,

@@ -91,122 +91,31 @@ __device__ __forceinline__ void wave_write_special(const SampleArgs &a, int row,
   }
 }
 
-/* What the rare exact paths need of a row; they stream it from memory. */
-struct RowRef {
-  uint32_t *counters;
-  int32_t *ids;
-  float *probs;
-  int32_t *cand;
-  WaveLds *Sp;
-  const char *rowp;
-  int row, V, k, lane, banned;
-  float T, y;
-  bool t_finite, bf16;
-};
-
-/* Element i of the row read again from memory (L2 after the first pass),
- * as x = L / T: the rare exact paths stream the row instead of keeping
- * per-element values beside the registers that hold it. */
-__device__ __forceinline__ float gx(const RowRef &R, int i) {
-  float L;
-  if (R.bf16)
-    L = d3s_bf16_to_f32(((const uint16_t *)R.rowp)[i]);
-  else
-    L = ((const float *)R.rowp)[i];
-  return scale_logit(i == R.banned ? -__builtin_inff() : L, R.T, R.y, R.t_finite);
-}
-
-/* ---- exact 8-bit radix select of the top k by (x desc, index asc); writes
- * exactly k keys to S.keys and returns k */
-__device__ __noinline__ int exact_select(const RowRef &R) {
-  if (R.lane == 0 && R.counters) atomicAdd(&R.counters[CNT_EXACT_SELECT], 1u);
-  WaveLds &S = *R.Sp;
-  uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)R.k;
-  bool done = false;
-  for (int pass = 0; pass < 4 && !done; pass++) {
-    const int shift = 24 - 8 * pass;
-    wave_lds_sync();
-    for (int i = R.lane; i < NB; i += WAVE) S.hist[i] = 0u;
-    wave_lds_sync();
-#pragma unroll 4
-    for (int i = R.lane; i < R.V; i += WAVE) {
-      const uint32_t key = d3s_ordkey(gx(R, i));
-      if ((key & pmask) == prefix) atomicAdd(&S.hist[(key >> shift) & 255u], 1u);
-    }
-    wave_lds_sync();
-    const BinSel b = wave_find_bin<false>(S.hist, need); /* holds >= need */
-    prefix |= b.bin << shift;
-    pmask |= 0xffu << shift;
-    done = b.count == need - b.above;
-    need -= b.above;
-  }
-  /* everything above the group, then the group (all of it when it holds
-   * exactly `need`, else its lowest-index `need`, in index order) */
-  uint32_t base = 0u;
-  for (int t0 = 0; t0 < R.V; t0 += WAVE) {
-    const int i = t0 + R.lane;
-    const float xi = i < R.V ? gx(R, i) : 0.0f;
-    const uint32_t key = d3s_ordkey(xi) & pmask;
-    const bool sel = i < R.V && (key > prefix || (done && key == prefix));
-    const uint64_t m = __ballot(sel);
-    if (sel) S.keys[base + (uint32_t)mbcnt64(m)] = composite_key(xi, i);
-    base += (uint32_t)__popcll(m);
-  }
-  if (!done) {
-    uint32_t ord0 = 0u;
-    for (int t0 = 0; t0 < R.V && ord0 < need; t0 += WAVE) {
-      const int i = t0 + R.lane;
-      const float xi = i < R.V ? gx(R, i) : 0.0f;
-      const bool tie = i < R.V && d3s_ordkey(xi) == prefix;
-      const uint64_t m = __ballot(tie);
-      const uint32_t ord = ord0 + (uint32_t)mbcnt64(m);
-      if (tie && ord < need) S.keys[base + ord] = composite_key(xi, i);
-      ord0 += (uint32_t)__popcll(m);
-    }
-  }
-  return R.k;
-}
-
-/* the exact row sum of the oracle: 2^-40 fixed point of d3s_expf(x - m) */
-__device__ __noinline__ float exact_lse(const RowRef &R, float M) {
-  uint64_t acc = 0;
-#pragma unroll 4
-  for (int i = R.lane; i < R.V; i += WAVE) acc += d3s_fix40(d3s_expf(gx(R, i) - M));
-  return M + d3s_logf(d3s_fixsum_to_f32(wave_sum_u64(acc)));
-}
-
-/* refusal and max of x = L / T element by element (T not finite, or logits
- * too large for the fast row sum); returns false for a finished row */
-__device__ __noinline__ bool slow_max(const RowRef &R, float &M) {
-  float xm = -__builtin_inff();
-  bool bad = false;
-#pragma unroll 4
-  for (int i = R.lane; i < R.V; i += WAVE) {
-    const float xi = gx(R, i);
-    bad = bad || (classify(xi) & 1u);
-    xm = d3s_isnan(xi) ? xm : fmaxf(xm, xi);
-  }
-  if (__ballot(bad)) return false;
-  M = wave_max_f(xm);
-  return true;
-}
-
+/* A row in registers: CPT 16-byte chunks per lane (chunk j * 64 + lane, from
+ * the aligned address at or below the row start), 4 words each: fp32 bits or
+ * two bf16 halves.  Element i of a lane is chunk row i / EPC, lane-in-chunk
+ * i % EPC; index order is (chunk row, lane, lane-in-chunk). */
 template <int CPT, bool BF16>
-struct WaveRow {
-  static constexpr int ES = BF16 ? 2 : 4;
-  static constexpr int EPC = 16 / ES; /* elements per 16-byte chunk */
+struct Chunks {
+  static constexpr int EPC = BF16 ? 8 : 4; /* elements per 16-byte chunk */
   static constexpr int NV = CPT * EPC;
-
-  const SampleArgs a;
-  WaveLds &S;
-  int row, V, k, lane, pos0, nchunks, banned;
-  const char *rowp;
-  float T, y, uval, top_p;
-  bool t_finite;
-  /* the row as loaded: 16-byte chunks, 4 words each (fp32 bits, or two bf16
-   * halves); -inf outside the row and at the banned index */
   uint32_t w[CPT * 4];
 
+  /* every chunk past the row's last reads that last chunk (masked by the
+   * caller).  `again`: a second read of the row, kept a real load so the
+   * compiler does not hold the first read's registers until it. */
+  template <bool again = false>
+  __device__ __forceinline__ void load(const uint4 *src, int nchunks, int lane) {
+    if (again) asm volatile("" : "+s"(src)); /* an address the compiler cannot match */
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+      const uint4 q = src[min(j * WAVE + lane, nchunks - 1)];
+      w[4 * j] = q.x;
+      w[4 * j + 1] = q.y;
+      w[4 * j + 2] = q.z;
+      w[4 * j + 3] = q.w;
+    }
+  }
   __device__ __forceinline__ float val(int i) const {
     if (BF16) {
       const uint32_t word = w[(i / EPC) * 4 + (i % EPC) / 2];
@@ -222,40 +131,206 @@ struct WaveRow {
     else
       word = on ? 0xff800000u : word;
   }
+  __device__ __forceinline__ static int pos(int pos0, int i) { return pos0 + (i / EPC) * WAVE * EPC + (i % EPC); }
+};
+
+/* What a row's rare exact paths need.  They read the row again (from L2),
+ * four chunk rows at a time (four 16-byte loads in flight per lane), so their
+ * registers stay few next to the fast path's. */
+struct RowRef {
+  uint32_t *counters;
+  WaveLds *Sp;
+  const uint4 *src;
+  int nchunks, pos0, V, k, lane, banned;
+  float T, y;
+  bool t_finite;
+};
+
+constexpr int GROUP = 4; /* chunk rows per group of the rare paths */
+
+/* f(i, x, in) for every element of chunk rows j0 .. j0 + GROUP - 1 (in: the
+ * position lies in the row; x = L / T, -inf at the banned index) */
+template <int CPT, bool BF16, class F>
+__device__ __forceinline__ void for_group(const RowRef &R, int j0, F &&f) {
+  using C = Chunks<1, BF16>;
+  constexpr int EPC = C::EPC;
+  const uint4 *src = R.src;
+  asm volatile("" : "+s"(src)); /* a second read: not to be matched with the first */
+  uint4 q[GROUP];
+#pragma unroll
+  for (int g = 0; g < GROUP; g++)
+    if (j0 + g < CPT) q[g] = src[min((j0 + g) * WAVE + R.lane, R.nchunks - 1)];
+#pragma unroll
+  for (int g = 0; g < GROUP; g++)
+    if (j0 + g < CPT) {
+      C c;
+      c.w[0] = q[g].x;
+      c.w[1] = q[g].y;
+      c.w[2] = q[g].z;
+      c.w[3] = q[g].w;
+#pragma unroll
+      for (int e = 0; e < EPC; e++) {
+        const int i = (j0 + g) * EPC + e;
+        const int p = R.pos0 + (j0 + g) * WAVE * EPC + e;
+        const bool in = (unsigned)p < (unsigned)R.V;
+        f(i, scale_logit(p == R.banned ? -__builtin_inff() : c.val(e), R.T, R.y, R.t_finite), in);
+      }
+    }
+}
+
+/* ---- exact 8-bit radix select of the top k by (x desc, index asc); writes
+ * exactly k keys to S.keys and returns k */
+template <int CPT, bool BF16>
+__device__ __forceinline__ int exact_select(const RowRef &R) {
+  constexpr int EPC = Chunks<1, BF16>::EPC;
+  if (R.lane == 0 && R.counters) atomicAdd(&R.counters[CNT_EXACT_SELECT], 1u);
+  WaveLds &S = *R.Sp;
+  uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)R.k;
+  bool done = false;
+#pragma unroll 1
+  for (int pass = 0; pass < 4 && !done; pass++) {
+    const int shift = 24 - 8 * pass;
+    wave_lds_sync();
+    for (int i = R.lane; i < NB; i += WAVE) S.hist[i] = 0u;
+    wave_lds_sync();
+#pragma unroll 1
+    for (int j0 = 0; j0 < CPT; j0 += GROUP)
+      for_group<CPT, BF16>(R, j0, [&](int, float x, bool in) {
+        const uint32_t key = d3s_ordkey(x);
+        if (in && (key & pmask) == prefix) atomicAdd(&S.hist[(key >> shift) & 255u], 1u);
+      });
+    wave_lds_sync();
+    const BinSel b = wave_find_bin<false>(S.hist, need); /* holds >= need */
+    prefix |= b.bin << shift;
+    pmask |= 0xffu << shift;
+    done = b.count == need - b.above;
+    need -= b.above;
+  }
+  /* everything above the group, then the group (all of it when it holds
+   * exactly `need`, else its lowest-index `need`, in index order) */
+  uint32_t base = 0u;
+#pragma unroll 1
+  for (int j0 = 0; j0 < CPT; j0 += GROUP)
+    for_group<CPT, BF16>(R, j0, [&](int i, float x, bool in) {
+      const uint32_t km = d3s_ordkey(x) & pmask;
+      const bool sel = in && (km > prefix || (done && km == prefix));
+      const uint64_t m = __ballot(sel);
+      if (sel) S.keys[base + (uint32_t)mbcnt64(m)] = composite_key(x, Chunks<1, BF16>::pos(R.pos0, i));
+      base += (uint32_t)__popcll(m);
+    });
+  if (!done) {
+    uint32_t ord0 = 0u, cnt = 0u, ord = 0u;
+    /* chunk row by chunk row: the lane's tie count, an exclusive scan, then
+     * each tie's ordinal in index order */
+#pragma unroll 1
+    for (int j0 = 0; j0 < CPT; j0 += GROUP)
+      for_group<CPT, BF16>(R, j0, [&](int i, float x, bool in) {
+        const int e = i % EPC;
+        if (e == 0) cnt = 0u;
+        cnt += (in && d3s_ordkey(x) == prefix) ? 1u : 0u;
+        if (e == EPC - 1) {
+          const uint32_t incl = wave_scan_add_u32(cnt);
+          ord = ord0 + incl - cnt;
+          ord0 += readlane_u(incl, 63);
+        }
+      });
+    /* second sweep: the same order, now writing the first `need` ties */
+    ord0 = 0u;
+#pragma unroll 1
+    for (int j0 = 0; j0 < CPT; j0 += GROUP) {
+      uint32_t cnts[GROUP * EPC];
+      for_group<CPT, BF16>(R, j0, [&](int i, float x, bool in) {
+        cnts[(i - j0 * EPC)] = (in && d3s_ordkey(x) == prefix) ? 1u : 0u;
+      });
+#pragma unroll
+      for (int g = 0; g < GROUP; g++)
+        if (j0 + g < CPT) {
+          uint32_t c = 0u;
+#pragma unroll
+          for (int e = 0; e < EPC; e++) c += cnts[g * EPC + e];
+          const uint32_t incl = wave_scan_add_u32(c);
+          uint32_t o = ord0 + incl - c;
+          ord0 += readlane_u(incl, 63);
+#pragma unroll
+          for (int e = 0; e < EPC; e++) {
+            if (cnts[g * EPC + e] && o < need) {
+              const int i = (j0 + g) * EPC + e;
+              const int p = Chunks<1, BF16>::pos(R.pos0, i);
+              S.keys[base + o] = ((uint64_t)prefix << 32) | (uint64_t)(uint32_t)(~(uint32_t)p);
+            }
+            o += cnts[g * EPC + e];
+          }
+        }
+    }
+  }
+  return R.k;
+}
+
+/* the exact row sum of the oracle: 2^-40 fixed point of d3s_expf(x - m) */
+template <int CPT, bool BF16>
+__device__ __forceinline__ float exact_lse(const RowRef &R, float M) {
+  uint64_t acc = 0;
+#pragma unroll 1
+  for (int j0 = 0; j0 < CPT; j0 += GROUP)
+    for_group<CPT, BF16>(R, j0, [&](int, float x, bool in) { acc += in ? d3s_fix40(d3s_expf(x - M)) : 0ull; });
+  return M + d3s_logf(d3s_fixsum_to_f32(wave_sum_u64(acc)));
+}
+
+/* refusal and max of x = L / T element by element (T not finite, or logits
+ * too large for the fast row sum): the max, or NaN when some x is NaN or +inf */
+template <int CPT, bool BF16>
+__device__ __forceinline__ float slow_max(const RowRef &R) {
+  float xm = -__builtin_inff();
+  bool bad = false;
+#pragma unroll 1
+  for (int j0 = 0; j0 < CPT; j0 += GROUP)
+    for_group<CPT, BF16>(R, j0, [&](int, float x, bool in) {
+      bad = bad || (in && (classify(x) & 1u));
+      xm = (in && !d3s_isnan(x)) ? fmaxf(xm, x) : xm;
+    });
+  return __ballot(bad) ? __builtin_nanf("") : wave_max_f(xm);
+}
+
+template <int CPT, bool BF16>
+struct WaveRow {
+  using C = Chunks<CPT, BF16>;
+  static constexpr int ES = BF16 ? 2 : 4;
+  static constexpr int EPC = C::EPC;
+  static constexpr int NV = C::NV;
+
+  const SampleArgs a;
+  WaveLds &S;
+  int row, V, k, lane, pos0, nchunks, banned;
+  const uint4 *src;
+  float T, y, uval, top_p;
+  bool t_finite;
+  C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
 
-  /* element i: chunk row j = i / EPC (chunk j * 64 + lane), lane-in-chunk e = i % EPC;
-   * index order is (j, lane, e) */
-  __device__ __forceinline__ int pos(int i) const { return pos0 + (i / EPC) * WAVE * EPC + (i % EPC); }
-  __device__ __forceinline__ bool valid(int i) const { return (unsigned)pos(i) < (unsigned)V; }
+  __device__ __forceinline__ bool valid(int i) const { return (unsigned)C::pos(pos0, i) < (unsigned)V; }
   /* chunk row j holds part of the row in some lane (wave-uniform) */
   __device__ __forceinline__ bool live(int j) const { return j * WAVE < nchunks; }
+  __device__ __forceinline__ RowRef ref() const {
+    return RowRef{a.counters, &S, src, nchunks, pos0, V, k, lane, banned, T, y, t_finite};
+  }
 
   __device__ __forceinline__ void load() {
     const RowP rp = row_params(a, row);
     T = rp.T;
     top_p = rp.top_p;
+    banned = rp.banned;
     t_finite = T < __builtin_inff(); /* false for +inf and NaN */
     y = 1.0f / T;
     uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
-    /* 16-byte chunks from the aligned address at or below the row start: a
-     * chunk never crosses a page, so the bytes outside the row it covers are
-     * readable; they become -inf below */
-    rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
-    banned = rp.banned;
+    /* a chunk never crosses a page, so the bytes outside the row it covers
+     * are readable; they become -inf below */
+    const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
     const int off = (int)(((uintptr_t)rowp & 15u) / ES);
-    const uint4 *src = (const uint4 *)(rowp - off * ES);
+    src = (const uint4 *)(rowp - off * ES);
     nchunks = (off + V + EPC - 1) / EPC;
     pos0 = lane * EPC - off;
-#pragma unroll
-    for (int j = 0; j < CPT; j++) {
-      const uint4 q = src[min(j * WAVE + lane, nchunks - 1)]; /* past the row: masked below */
-      w[4 * j] = q.x;
-      w[4 * j + 1] = q.y;
-      w[4 * j + 2] = q.z;
-      w[4 * j + 3] = q.w;
-    }
+    c.load(src, nchunks, lane);
     /* the partial chunk at the row start and every chunk row from the one
      * holding the row end on */
     const int jlast = (nchunks - 1) / WAVE;
@@ -263,145 +338,27 @@ struct WaveRow {
     for (int j = 0; j < CPT; j++)
       if ((j == 0 && off != 0) || j >= jlast) {
 #pragma unroll
-        for (int e = 0; e < EPC; e++) {
-          const int i = j * EPC + e;
-          mask(i, !valid(i));
-        }
+        for (int e = 0; e < EPC; e++) c.mask(j * EPC + e, !valid(j * EPC + e));
       }
-    if ((unsigned)rp.banned < (unsigned)V) {
-      const int bp = rp.banned + off;
+    if ((unsigned)banned < (unsigned)V) {
+      const int bp = banned + off;
       const int jb = bp / (WAVE * EPC), lb = (bp / EPC) % WAVE, eb = bp % EPC;
 #pragma unroll
       for (int j = 0; j < CPT; j++)
         if (j == jb) {
 #pragma unroll
-          for (int e = 0; e < EPC; e++) mask(j * EPC + e, lane == lb && e == eb);
+          for (int e = 0; e < EPC; e++) c.mask(j * EPC + e, lane == lb && e == eb);
         }
     }
   }
 
-  __device__ __forceinline__ void run() {
-    load();
-    const float ninf = -__builtin_inff();
-    /* slow: every quantity per element from x = L / T, as the oracle (T not
-     * finite, or logits too large for the fast row sum) */
-    bool slow = !t_finite;
-    float M = 0.0f, lse = 0.0f, eps_s = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
-    if (!slow) {
-      /* ---- row max of the logits; NaN propagates */
-#pragma unroll
-      for (int i = 0; i < NV; i++) lm = fmaximum(lm, val(i));
-      const float Lmax = wave_maximum_f(lm);
-      if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
-        wave_write_special(a, row, false);
-        return;
-      }
-      M = scale_logit(Lmax, T, y, true); /* = max x */
-      if (M == __builtin_inff()) {
-        wave_write_special(a, row, false);
-        return;
-      }
-      if (M == ninf) {
-        wave_write_special(a, row, true);
-        return;
-      }
-      cf = LOG2E_F / T;
-      const float h = Lmax * cf;
-      slow = !(fabsf(h) < 0x1p24f);
-      b = -h;
-      delta = __builtin_fmaf(Lmax, cf, b); /* Lmax * cf + b exactly */
-    }
-    const RowRef R{a.counters, a.ids, a.probs, a.cand, &S, rowp, row, V, k, lane, banned, T, y, t_finite, BF16};
-    if (slow) {
-      if (!slow_max(R, M)) {
-        wave_write_special(a, row, false);
-        return;
-      }
-      if (M == ninf) {
-        wave_write_special(a, row, true);
-        return;
-      }
-    }
-    bool need_sel = slow || (a.flags & FLAG_EXACT_SELECT) != 0;
-    int n = 0;
-    if (!slow) {
-      /* ---- tau: the k-th largest lane max (its key), by ballot radix search */
-      const uint32_t lkey = d3s_ordkey(lm);
-      uint32_t pre = 0u;
-#pragma unroll
-      for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t cnd = pre | (1u << bit);
-        if (__popcll(__ballot(lkey >= cnd)) >= (uint32_t)k) pre = cnd;
-      }
-      float tau_lo = __builtin_inff();
-      const float tau = d3s_from_ordkey(pre);
-      if (tau == ninf) {
-        need_sel = true;
-      } else if (!need_sel) {
-        /* tau_lo: the least logit whose x equals tau's x */
-        const float xt = scale_logit(tau, T, y, true);
-        uint32_t lo = pre;
-        int s = 0;
-        for (; s < 8; s++) {
-          if (scale_logit(d3s_from_ordkey(lo - 1u), T, y, true) != xt) break;
-          lo -= 1u;
-        }
-        if (s == 8)
-          need_sel = true;
-        else
-          tau_lo = d3s_from_ordkey(lo);
-      }
-
-      /* ---- one pass: the fast row sum and the candidates */
-      float acc[EPC];
-#pragma unroll
-      for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
-      int cnt = 0;
-#pragma unroll
-      for (int j = 0; j < CPT; j++)
-        if (live(j)) {
-#pragma unroll
-          for (int e = 0; e < EPC; e++) {
-            const float v = val(j * EPC + e);
-            acc[e] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
-            if (v >= tau_lo) {
-              S.lst[min(cnt, LCAP - 1) * WAVE + lane] =
-                  make_uint2(d3s_f2u(v), (uint32_t)(pos0 + j * WAVE * EPC + e));
-              cnt++;
-            }
-          }
-        }
-#pragma unroll
-      for (int w = EPC / 2; w >= 1; w /= 2)
-#pragma unroll
-        for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
-      const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
-      lse = M + (d3s_logf(sp) - delta * LN2_F);
-      /* relative error bound of 2^-delta S' against the exact row sum: the
-       * rounding of x, m, x - m and log2(e)/T, the fast exponent's error,
-       * d3s_expf's, the terms below e^-40, the fixed-point truncation, and
-       * the accumulation (CPT + 3 + 6 roundings) and the final rounding */
-      eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
-              (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
-
-      const uint32_t tot = wave_sum_u32((uint32_t)cnt);
-      if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
-      if (!need_sel) {
-        const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
-#pragma unroll 1
-        for (int e = 0; e < LCAP; e++) {
-          if (!__ballot(e < cnt)) break;
-          if (e < cnt) {
-            const uint2 p = S.lst[e * WAVE + lane];
-            S.keys[excl + e] = composite_key(scale_logit(d3s_u2f(p.x), T, y, true), (int)p.y);
-          }
-        }
-        n = (int)tot;
-      }
-    }
-    if (need_sel) n = exact_select(R);
-
-    /* ---- rank the n >= k candidates by key */
+  /* Rank the n >= k candidates in S.keys by key and run the tail (the
+   * reference kernel's cumulative, cut, softmax and race, src/sampling.c:
+   * 123-139).  With the fast lse, |c'_r - c_r| <= c'_r * (eps_e + (2k + 2)
+   * 2^-24), eps_e bounding the relative change of a term exp(v - lse) between
+   * the two lse values; the exact row sum is computed when a cut could fall
+   * differently. */
+  __device__ __forceinline__ void finish(int n, float M, float lse, bool exact, float eps_s) {
     if (lane == 0) S.keys[n] = 0ull; /* pad for the pair reads; below every key */
     wave_lds_sync();
     const uint64_t my = lane < n ? S.keys[lane] : 0ull;
@@ -418,37 +375,154 @@ struct WaveRow {
     const uint64_t key = act ? S.ranked[lane] : 0ull;
     const float v = key_x(key);
     const int idx = key_idx(key);
-
-    /* ---- the cumulative c_r (src/sampling.c:126-127).  With the fast lse,
-     * |c'_r - c_r| <= c'_r * (eps_e + (2k + 2) 2^-24), eps_e bounding the
-     * relative change of a term exp(v - lse) between the two lse values; the
-     * exact row sum is computed when a cut could fall differently. */
-    bool exact = slow || (a.flags & FLAG_EXACT_LSE) != 0;
-    float c = 0.0f;
+    float cc = 0.0f;
     if (!exact) {
-      c = wave_seq_cumsum(act ? d3s_expf(v - lse) : 0.0f, k, S.buf);
+      cc = wave_seq_cumsum(act ? d3s_expf(v - lse) : 0.0f, k, S.buf);
       const float D = wave_max_f(act ? lse - v : 0.0f);
       const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
       const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
       const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-      exact = __ballot(act && lane > 0 && fabsf(c - top_p) <= B * c + 0x1p-60f) != 0ull;
+      exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
+              (a.flags & FLAG_EXACT_LSE) != 0;
+      if (exact && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
     }
     if (exact) {
-      if (!slow && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-      const float lx = exact_lse(R, M);
-      c = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
+      const float lx = exact_lse<CPT, BF16>(ref(), M);
+      cc = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
     }
     const float ep = act ? d3s_expf(v - M) : 0.0f; /* x_0 = m */
     const float noise = -d3s_logf(1.0f - uval);
-    wave_race(a, row, idx, c, ep, noise, top_p, S.buf);
+    wave_race(a, row, idx, cc, ep, noise, top_p, S.buf);
+  }
+
+  /* every quantity per element from x = L / T, as the oracle (T not finite,
+   * or logits too large for the fast row sum) */
+  __device__ __forceinline__ void slow_row() {
+    const RowRef R = ref();
+    const float M = slow_max<CPT, BF16>(R);
+    if (d3s_isnan(M) || M == -__builtin_inff()) {
+      wave_write_special(a, row, !d3s_isnan(M));
+      return;
+    }
+    finish(exact_select<CPT, BF16>(R), M, 0.0f, true, 0.0f);
+  }
+
+  __device__ __forceinline__ void run() {
+    load();
+    const float ninf = -__builtin_inff();
+    bool slow = !t_finite;
+    float M = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
+    if (!slow) {
+      /* ---- row max of the logits; NaN propagates */
+#pragma unroll
+      for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
+      const float Lmax = wave_maximum_f(lm);
+      if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
+        wave_write_special(a, row, false);
+        return;
+      }
+      M = scale_logit(Lmax, T, y, true); /* = max x */
+      if (M == __builtin_inff() || M == ninf) {
+        wave_write_special(a, row, M == ninf);
+        return;
+      }
+      cf = LOG2E_F / T;
+      const float h = Lmax * cf;
+      slow = !(fabsf(h) < 0x1p24f);
+      b = -h;
+      delta = __builtin_fmaf(Lmax, cf, b); /* Lmax * cf + b exactly */
+    }
+    if (slow) {
+      slow_row();
+      return;
+    }
+
+    /* ---- tau: the k-th largest lane max (its key), by ballot radix search */
+    bool need_sel = (a.flags & FLAG_EXACT_SELECT) != 0;
+    const uint32_t lkey = d3s_ordkey(lm);
+    uint32_t pre = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 0; bit--) {
+      const uint32_t cnd = pre | (1u << bit);
+      if (__popcll(__ballot(lkey >= cnd)) >= (uint32_t)k) pre = cnd;
+    }
+    float tau_lo = __builtin_inff();
+    const float tau = d3s_from_ordkey(pre);
+    if (tau == ninf) {
+      need_sel = true;
+    } else if (!need_sel) {
+      /* tau_lo: the least logit whose x equals tau's x */
+      const float xt = scale_logit(tau, T, y, true);
+      uint32_t lo = pre;
+      int s = 0;
+      for (; s < 8; s++) {
+        if (scale_logit(d3s_from_ordkey(lo - 1u), T, y, true) != xt) break;
+        lo -= 1u;
+      }
+      if (s == 8)
+        need_sel = true;
+      else
+        tau_lo = d3s_from_ordkey(lo);
+    }
+
+    /* ---- one pass: the fast row sum and the candidates */
+    float acc[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      if (live(j)) {
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          const float v = c.val(j * EPC + e);
+          acc[e] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
+          if (v >= tau_lo) {
+            S.lst[min(cnt, LCAP - 1) * WAVE + lane] =
+                make_uint2(d3s_f2u(v), (uint32_t)(pos0 + j * WAVE * EPC + e));
+            cnt++;
+          }
+        }
+      }
+#pragma unroll
+    for (int w = EPC / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
+    const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
+    const float lse = M + (d3s_logf(sp) - delta * LN2_F);
+    /* relative error bound of 2^-delta S' against the exact row sum: the
+     * rounding of x, m, x - m and log2(e)/T, the fast exponent's error,
+     * d3s_expf's, the terms below e^-40, the fixed-point truncation, and the
+     * accumulation (CPT + 3 + 6 roundings) and the final rounding */
+    const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
+                        (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
+
+    const uint32_t tot = wave_sum_u32((uint32_t)cnt);
+    if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
+    int n;
+    if (need_sel) {
+      n = exact_select<CPT, BF16>(ref());
+    } else {
+      const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
+#pragma unroll 1
+      for (int e = 0; e < LCAP; e++) {
+        if (!__ballot(e < cnt)) break;
+        if (e < cnt) {
+          const uint2 p = S.lst[e * WAVE + lane];
+          S.keys[excl + e] = composite_key(scale_logit(d3s_u2f(p.x), T, y, true), (int)p.y);
+        }
+      }
+      n = (int)tot;
+    }
+    finish(n, M, lse, false, eps_s);
   }
 };
 
-/* waves per SIMD the register budget is set for: the row's 4 * CPT
- * registers plus about 45 */
+/* waves per SIMD the register budget is set for (the row's 4 * CPT
+ * registers plus the rest; checked for spills at build time) */
 template <int CPT, bool BF16>
 constexpr int wave_occupancy() {
-  return CPT <= 9 ? 5 : CPT <= 17 ? 4 : 3;
+  return BF16 ? (CPT <= 8 ? 5 : 4) : (CPT <= 17 ? 5 : 3);
 }
 
 template <int CPT, bool BF16>
@@ -471,14 +545,16 @@ __global__ void k_exp2(const float *in, float *out, int64_t n) {
   if (i < n) out[i] = __builtin_amdgcn_exp2f(in[i]);
 }
 
+/* the widest row k_wave<CPT, BF16> holds: rows starting off elements past a
+ * 16-byte boundary need off more slots */
 template <int CPT, bool BF16>
-constexpr int wave_vmax() {
-  return WAVE * CPT * (16 / (BF16 ? 2 : 4)) - (16 / (BF16 ? 2 : 4) - 1);
+constexpr int wave_vmax(int off) {
+  return WAVE * CPT * (16 / (BF16 ? 2 : 4)) - off;
 }
 
 template <int CPT, bool BF16>
-bool try_wave(const SampleArgs &a, hipStream_t s) {
-  if (a.vocab > wave_vmax<CPT, BF16>()) return false;
+bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
+  if (a.vocab > wave_vmax<CPT, BF16>(max_off)) return false;
   const unsigned blocks = (unsigned)((a.n_rows + WR - 1) / WR);
   hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3(blocks), dim3(WAVE * WR), 0, s, a);
   return true;
@@ -486,20 +562,28 @@ bool try_wave(const SampleArgs &a, hipStream_t s) {
 
 }  // namespace
 
-int wave_max_vocab(Dtype dt) { return dt == DT_F32 ? wave_vmax<24, false>() : wave_vmax<16, true>(); }
-
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s) {
   if (n <= 0) return;
   const int B = 256;
   hipLaunchKernelGGL(k_exp2, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, in, out, n);
 }
 
+int wave_max_vocab(Dtype dt) { return dt == DT_F32 ? wave_vmax<24, false>(3) : wave_vmax<16, true>(7); }
+
 bool launch_wave(const SampleArgs &a, Dtype dt, hipStream_t s) {
   if (a.k > KF) return false;
+  /* the largest start offset of a row within its 16-byte chunk: 0 when the
+   * base and the stride are both 16-byte multiples */
+  const int es = dt == DT_F32 ? 4 : 2;
+  const bool aligned = ((uintptr_t)a.logits % 16u) == 0u && (a.row_stride * es) % 16 == 0;
+  const int max_off = aligned ? 0 : 16 / es - 1;
   if (dt == DT_F32)
-    return try_wave<4, false>(a, s) || try_wave<8, false>(a, s) || try_wave<17, false>(a, s) ||
-           try_wave<24, false>(a, s);
-  return try_wave<4, true>(a, s) || try_wave<9, true>(a, s) || try_wave<16, true>(a, s);
+    return try_wave<4, false>(a, max_off, s) || try_wave<8, false>(a, max_off, s) ||
+           try_wave<16, false>(a, max_off, s) || try_wave<17, false>(a, max_off, s) ||
+           try_wave<24, false>(a, max_off, s);
+  /* (9 chunk rows per lane is left out: it allocates registers badly) */
+  return try_wave<4, true>(a, max_off, s) || try_wave<8, true>(a, max_off, s) ||
+         try_wave<10, true>(a, max_off, s) || try_wave<16, true>(a, max_off, s);
 }
 
 }  // namespace d3s
