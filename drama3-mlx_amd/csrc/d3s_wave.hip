@@ -40,6 +40,8 @@ constexpr int LCAP = 8; /* entries of a lane's private candidate list */
  * result; the GPU tests check it over dense samples of [-126, 1] */
 constexpr float EPS_EXP2 = 0x1p-21f;
 constexpr float LOG2E_F = 1.44269504f;
+/* dword 3 of a gfx9 buffer resource: 32-bit data format, raw addressing */
+constexpr int BUFFER_FLAGS = 0x00020000;
 constexpr float LN2_F = 0.693147182f;
 
 struct __align__(16) WaveLds {
@@ -48,6 +50,7 @@ struct __align__(16) WaveLds {
   uint64_t ranked[WAVE];   /* keys by rank */
   uint32_t hist[NB];       /* radix-select histogram */
   float buf[WAVE];         /* sequential sums */
+  float buf2[WAVE];
 };
 
 __device__ __forceinline__ float fmaximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
@@ -78,6 +81,68 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+/* Lane r (< k) gets the left-to-right fp32 prefix sums c_r = e_0 + ... + e_r
+ * and s_r = f_0 + ... + f_r (the reference kernel's sequential cumulative,
+ * src/sampling.c:126-127, and its kept sum, :129-131, whose value at the cut
+ * is s_{cut-1}).  One lane runs both chains side by side over the terms in
+ * LDS and writes each prefix back in place; every lane then reads its own. */
+__device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float *be, float *bf, float &c,
+                                                 float &s) {
+  const int lane = lane_id();
+  be[lane] = lane < k ? e : 0.0f;
+  bf[lane] = lane < k ? f : 0.0f;
+  wave_lds_sync();
+  if (lane == 0) {
+    float4 *e4 = (float4 *)be;
+    float4 *f4 = (float4 *)bf;
+    float ce = 0.0f, cf = 0.0f;
+    for (int r4 = 0; r4 < (k + 3) / 4; r4++) {
+      float4 qe = e4[r4], qf = f4[r4];
+      qe.x = ce = ce + qe.x;
+      qf.x = cf = cf + qf.x;
+      qe.y = ce = ce + qe.y;
+      qf.y = cf = cf + qf.y;
+      qe.z = ce = ce + qe.z;
+      qf.z = cf = cf + qf.z;
+      qe.w = ce = ce + qe.w;
+      qf.w = cf = cf + qf.w;
+      e4[r4] = qe;
+      f4[r4] = qf;
+    }
+  }
+  wave_lds_sync();
+  c = be[lane];
+  s = bf[lane];
+  wave_lds_sync();
+}
+
+/* The exclusive top-p cut over c_r, the probabilities and the race
+ * (src/sampling.c:128-139); lane r < k holds rank r's index, c_r, ep_r =
+ * exp(x_r - x_0), the prefix s_r of ep and noise -log(1 - u_r). */
+__device__ __forceinline__ void wave_race_prefix(const SampleArgs &a, int row, int idx, float c, float ep,
+                                                 float s, float noise, float top_p) {
+  const int lane = lane_id();
+  const int k = a.k;
+  const bool act = lane < k;
+  const uint64_t dm = __ballot(act && lane > 0 && c > top_p);
+  const int cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
+  const float inv = 1.0f / readlane_f(s, cut - 1);
+  const float p = (act && lane < cut) ? ep * inv : 0.0f;
+  float sc = -1.0f;
+  if (act) {
+    const float score = p / noise;
+    sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
+  }
+  int best = lane;
+  wave_argmax(sc, best);
+  const int id = (int)readlane_u((uint32_t)idx, best);
+  if (lane == 0) a.ids[row] = id;
+  if (act) {
+    if (a.probs) a.probs[(size_t)row * k + lane] = p;
+    if (a.cand) a.cand[(size_t)row * k + lane] = idx;
+  }
+}
+
 /* A refused row (id -1) or an all -inf row (id 0, ranks 0..k-1); one wave. */
 __device__ __forceinline__ void wave_write_special(const SampleArgs &a, int row, bool masked) {
   const int lane = lane_id(), k = a.k;
@@ -101,15 +166,16 @@ struct Chunks {
   static constexpr int NV = CPT * EPC;
   uint32_t w[CPT * 4];
 
-  /* every chunk past the row's last reads that last chunk (masked by the
-   * caller).  `again`: a second read of the row, kept a real load so the
-   * compiler does not hold the first read's registers until it. */
-  template <bool again = false>
+  /* through a buffer resource spanning the row's chunks: a chunk past the
+   * row's last reads as zeros (masked by the caller), and no per-chunk
+   * address arithmetic is needed */
   __device__ __forceinline__ void load(const uint4 *src, int nchunks, int lane) {
-    if (again) asm volatile("" : "+s"(src)); /* an address the compiler cannot match */
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, nchunks * 16, BUFFER_FLAGS);
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
-      const uint4 q = src[min(j * WAVE + lane, nchunks - 1)];
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane * 16, j * WAVE * 16, 0);
+      const uint4 q = make_uint4(v[0], v[1], v[2], v[3]);
       w[4 * j] = q.x;
       w[4 * j + 1] = q.y;
       w[4 * j + 2] = q.z;
@@ -134,9 +200,9 @@ struct Chunks {
   __device__ __forceinline__ static int pos(int pos0, int i) { return pos0 + (i / EPC) * WAVE * EPC + (i % EPC); }
 };
 
-/* What a row's rare exact paths need.  They read the row again (from L2),
- * four chunk rows at a time (four 16-byte loads in flight per lane), so their
- * registers stay few next to the fast path's. */
+/* What a row's rare exact paths need.  They read the row again (from L2), a
+ * group of chunk rows at a time (every load of a group in flight at once), so
+ * their registers stay few next to the fast path's. */
 struct RowRef {
   uint32_t *counters;
   WaveLds *Sp;
@@ -146,12 +212,18 @@ struct RowRef {
   bool t_finite;
 };
 
-constexpr int GROUP = 4; /* chunk rows per group of the rare paths */
+/* chunk rows the rare paths read at once (the most that leaves the kernel's
+ * register count where the fast path puts it) */
+template <int CPT, bool BF16>
+constexpr int rare_group() {
+  return BF16 ? 4 : 6;
+}
 
 /* f(i, x, in) for every element of chunk rows j0 .. j0 + GROUP - 1 (in: the
  * position lies in the row; x = L / T, -inf at the banned index) */
 template <int CPT, bool BF16, class F>
 __device__ __forceinline__ void for_group(const RowRef &R, int j0, F &&f) {
+  constexpr int GROUP = rare_group<CPT, BF16>();
   using C = Chunks<1, BF16>;
   constexpr int EPC = C::EPC;
   const uint4 *src = R.src;
@@ -175,6 +247,7 @@ __device__ __forceinline__ void for_group(const RowRef &R, int j0, F &&f) {
         const bool in = (unsigned)p < (unsigned)R.V;
         f(i, scale_logit(p == R.banned ? -__builtin_inff() : c.val(e), R.T, R.y, R.t_finite), in);
       }
+      __builtin_amdgcn_sched_barrier(0); /* one chunk at a time */
     }
 }
 
@@ -182,6 +255,7 @@ __device__ __forceinline__ void for_group(const RowRef &R, int j0, F &&f) {
  * exactly k keys to S.keys and returns k */
 template <int CPT, bool BF16>
 __device__ __forceinline__ int exact_select(const RowRef &R) {
+  constexpr int GROUP = rare_group<CPT, BF16>();
   constexpr int EPC = Chunks<1, BF16>::EPC;
   if (R.lane == 0 && R.counters) atomicAdd(&R.counters[CNT_EXACT_SELECT], 1u);
   WaveLds &S = *R.Sp;
@@ -269,6 +343,7 @@ __device__ __forceinline__ int exact_select(const RowRef &R) {
 /* the exact row sum of the oracle: 2^-40 fixed point of d3s_expf(x - m) */
 template <int CPT, bool BF16>
 __device__ __forceinline__ float exact_lse(const RowRef &R, float M) {
+  constexpr int GROUP = rare_group<CPT, BF16>();
   uint64_t acc = 0;
 #pragma unroll 1
   for (int j0 = 0; j0 < CPT; j0 += GROUP)
@@ -280,6 +355,7 @@ __device__ __forceinline__ float exact_lse(const RowRef &R, float M) {
  * too large for the fast row sum): the max, or NaN when some x is NaN or +inf */
 template <int CPT, bool BF16>
 __device__ __forceinline__ float slow_max(const RowRef &R) {
+  constexpr int GROUP = rare_group<CPT, BF16>();
   float xm = -__builtin_inff();
   bool bad = false;
 #pragma unroll 1
@@ -302,6 +378,7 @@ struct WaveRow {
   WaveLds &S;
   int row, V, k, lane, pos0, nchunks, banned;
   const uint4 *src;
+  const char *rowp;
   float T, y, uval, top_p;
   bool t_finite;
   C c; /* -inf outside the row and at the banned index */
@@ -325,7 +402,7 @@ struct WaveRow {
     uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
     /* a chunk never crosses a page, so the bytes outside the row it covers
      * are readable; they become -inf below */
-    const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
+    rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
     const int off = (int)(((uintptr_t)rowp & 15u) / ES);
     src = (const uint4 *)(rowp - off * ES);
     nchunks = (off + V + EPC - 1) / EPC;
@@ -358,7 +435,7 @@ struct WaveRow {
    * 2^-24), eps_e bounding the relative change of a term exp(v - lse) between
    * the two lse values; the exact row sum is computed when a cut could fall
    * differently. */
-  __device__ __forceinline__ void finish(int n, float M, float lse, bool exact, float eps_s) {
+  __device__ __forceinline__ void finish(int n, float M, float lse, bool exact, float eps_s, float noise) {
     if (lane == 0) S.keys[n] = 0ull; /* pad for the pair reads; below every key */
     wave_lds_sync();
     const uint64_t my = lane < n ? S.keys[lane] : 0ull;
@@ -375,24 +452,23 @@ struct WaveRow {
     const uint64_t key = act ? S.ranked[lane] : 0ull;
     const float v = key_x(key);
     const int idx = key_idx(key);
-    float cc = 0.0f;
+    const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    float cc, sp;
+    wave_seq_prefix2(act ? d3s_expf(v - lse) : 0.0f, ep, k, S.buf, S.buf2, cc, sp);
     if (!exact) {
-      cc = wave_seq_cumsum(act ? d3s_expf(v - lse) : 0.0f, k, S.buf);
-      const float D = wave_max_f(act ? lse - v : 0.0f);
+      const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
       const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
       const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
       const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
       exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
               (a.flags & FLAG_EXACT_LSE) != 0;
       if (exact && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+      if (exact) {
+        const float lx = exact_lse<CPT, BF16>(ref(), M);
+        cc = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
+      }
     }
-    if (exact) {
-      const float lx = exact_lse<CPT, BF16>(ref(), M);
-      cc = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
-    }
-    const float ep = act ? d3s_expf(v - M) : 0.0f; /* x_0 = m */
-    const float noise = -d3s_logf(1.0f - uval);
-    wave_race(a, row, idx, cc, ep, noise, top_p, S.buf);
+    wave_race_prefix(a, row, idx, cc, ep, sp, noise, top_p);
   }
 
   /* every quantity per element from x = L / T, as the oracle (T not finite,
@@ -404,12 +480,14 @@ struct WaveRow {
       wave_write_special(a, row, !d3s_isnan(M));
       return;
     }
-    finish(exact_select<CPT, BF16>(R), M, 0.0f, true, 0.0f);
+    const int n = exact_select<CPT, BF16>(R);
+    finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, -d3s_logf(1.0f - uval));
   }
 
   __device__ __forceinline__ void run() {
     load();
     const float ninf = -__builtin_inff();
+    const float noise = -d3s_logf(1.0f - uval); /* the race's noise needs only u */
     bool slow = !t_finite;
     float M = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
     if (!slow) {
@@ -437,53 +515,45 @@ struct WaveRow {
       return;
     }
 
-    /* ---- tau: the k-th largest lane max (its key), by ballot radix search */
+    /* ---- tau: the k-th largest lane max, to 20 bits of its order key (a
+     * lower bound: at least k elements reach it), by ballot radix search */
     bool need_sel = (a.flags & FLAG_EXACT_SELECT) != 0;
     const uint32_t lkey = d3s_ordkey(lm);
     uint32_t pre = 0u;
 #pragma unroll
-    for (int bit = 31; bit >= 0; bit--) {
+    for (int bit = 31; bit >= 12; bit--) {
       const uint32_t cnd = pre | (1u << bit);
       if (__popcll(__ballot(lkey >= cnd)) >= (uint32_t)k) pre = cnd;
     }
-    float tau_lo = __builtin_inff();
+    /* keys below -FLT_MAX's: the k-th lane max is -inf */
+    if (pre < d3s_ordkey(-0x1.fffffep127f)) need_sel = true;
     const float tau = d3s_from_ordkey(pre);
-    if (tau == ninf) {
-      need_sel = true;
-    } else if (!need_sel) {
-      /* tau_lo: the least logit whose x equals tau's x */
-      const float xt = scale_logit(tau, T, y, true);
-      uint32_t lo = pre;
-      int s = 0;
-      for (; s < 8; s++) {
-        if (scale_logit(d3s_from_ordkey(lo - 1u), T, y, true) != xt) break;
-        lo -= 1u;
-      }
-      if (s == 8)
-        need_sel = true;
-      else
-        tau_lo = d3s_from_ordkey(lo);
-    }
+    /* tau_lo: below every logit whose x ties with tau's (|L - tau| <=
+     * T ulp(x_tau) <= 2^-22 |tau|, or T 2^-149 for a subnormal x_tau), so
+     * {L >= tau_lo} holds every element whose x reaches the k-th largest */
+    const float tau_lo = need_sel ? __builtin_inff() : tau - (fabsf(tau) * 0x1p-21f + T * 0x1p-120f);
 
-    /* ---- one pass: the fast row sum and the candidates */
+    /* ---- one pass: the fast row sum, and the candidates as a bit per
+     * element (element i of word i / 32 at bit 31 - i % 32, no branches) */
+    constexpr int NWORD = (NV + 31) / 32;
     float acc[EPC];
 #pragma unroll
     for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
-    int cnt = 0;
+    uint32_t bits[NWORD];
 #pragma unroll
-    for (int j = 0; j < CPT; j++)
-      if (live(j)) {
+    for (int w = 0; w < NWORD; w++) bits[w] = 0u;
 #pragma unroll
-        for (int e = 0; e < EPC; e++) {
-          const float v = c.val(j * EPC + e);
-          acc[e] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
-          if (v >= tau_lo) {
-            S.lst[min(cnt, LCAP - 1) * WAVE + lane] =
-                make_uint2(d3s_f2u(v), (uint32_t)(pos0 + j * WAVE * EPC + e));
-            cnt++;
-          }
-        }
-      }
+    for (int i = 0; i < NV; i++) {
+      const float v = c.val(i);
+      acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
+      /* bits = 2 bits + (v >= tau_lo): the compare's lane mask as the carry in
+       * (two wait states between a VALU write of vcc and its use as a mask) */
+      asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+          : "+v"(bits[i / 32])
+          : "v"(v), "v"(tau_lo)
+          : "vcc");
+    }
+    if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
 #pragma unroll
     for (int w = EPC / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -497,24 +567,52 @@ struct WaveRow {
     const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
                         (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
 
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
     const uint32_t tot = wave_sum_u32((uint32_t)cnt);
     if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
     int n;
     if (need_sel) {
       n = exact_select<CPT, BF16>(ref());
     } else {
+      /* each lane takes its candidates in element order, reads their logits
+       * again (L2) and files their keys; slots excl .. excl + cnt - 1 */
       const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
-#pragma unroll 1
-      for (int e = 0; e < LCAP; e++) {
-        if (!__ballot(e < cnt)) break;
-        if (e < cnt) {
-          const uint2 p = S.lst[e * WAVE + lane];
-          S.keys[excl + e] = composite_key(scale_logit(d3s_u2f(p.x), T, y, true), (int)p.y);
+      int cpos[LCAP];
+#pragma unroll
+      for (int q = 0; q < LCAP; q++) {
+        cpos[q] = 0;
+        if (q > 0 && !__ballot(q < cnt)) break;
+        int i = 0;
+        bool found = false;
+#pragma unroll
+        for (int w = 0; w < NWORD; w++) {
+          const int e = __builtin_clz(bits[w] | 1u); /* bits[w] != 0 below */
+          const bool here = !found && bits[w] != 0u;
+          i = here ? 32 * w + e : i;
+          bits[w] = here ? bits[w] & ~(0x80000000u >> e) : bits[w];
+          found = found || here;
+        }
+        cpos[q] = pos0 + (i / EPC) * WAVE * EPC + (i % EPC);
+      }
+      float cl[LCAP];
+#pragma unroll
+      for (int q = 0; q < LCAP; q++) {
+        cl[q] = 0.0f;
+        if (q < cnt) {
+          if (BF16)
+            cl[q] = d3s_bf16_to_f32(((const uint16_t *)rowp)[cpos[q]]);
+          else
+            cl[q] = ((const float *)rowp)[cpos[q]];
         }
       }
+#pragma unroll
+      for (int q = 0; q < LCAP; q++)
+        if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(cl[q], T, y, true), cpos[q]);
       n = (int)tot;
     }
-    finish(n, M, lse, false, eps_s);
+    finish(n, M, lse, false, eps_s, noise);
   }
 };
 
