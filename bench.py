@@ -3,9 +3,11 @@
 Headline (`value`): sampled rows/s on C3, the batched backbone head
 (fp32 [256, 4097], per-row T/top_p, k = 30) in steady state: a persistent
 multi-batch launch, `--batches-per-launch` batches of 256 rows per d3s_sample
-call, back to back on one stream, rotating over a pool larger than 512 MB so
-every launch reads HBM rather than the 256 MB Infinity Cache.  Beside it: one
-batch per launch on one stream and on `--streams` streams.
+call, back to back on one stream, over a pool of `--pool-batches` batches in
+device memory (default 256 batches, 1.08 GB, over four times the 256 MB
+Infinity Cache, so every launch reads HBM; 16 distinct generated contents,
+every batch with its own uniforms).  Beside it: one batch per launch on one
+stream and on `--streams` streams.
 
 roofline.achieved = algorithmic bytes per launch (16 524 B per row) divided by
 the mean launch duration, timed with HIP events on the launching stream
@@ -202,11 +204,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20480, help="C3 batches timed")
     ap.add_argument("--warmup", type=int, default=512, help="C3 batches before timing")
-    ap.add_argument("--batches-per-launch", type=int, default=16,
+    ap.add_argument("--batches-per-launch", type=int, default=128,
                     help="C3 batches one d3s_sample call carries in the headline figure")
     ap.add_argument("--streams", type=int, default=4,
                     help="streams for the one-batch-per-launch figure beside the headline")
-    ap.add_argument("--pool-batches", type=int, default=128)
+    ap.add_argument("--pool-batches", type=int, default=256)
     ap.add_argument("--single-rows", type=int, default=10000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -259,7 +261,7 @@ def main():
         lat = single_row_latency(args.single_rows)
         log(f"C1 single row: p50 {lat['p50_us']:.2f} us (GPU), host p50 {lat['host_p50_us']:.2f} us")
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_C3.json")
+    tpath = os.path.join(ROOT, "profiles", "traffic_k_wave_C3.json")
     if os.path.exists(tpath):
         t = json.load(open(tpath))
         if t.get("batches_per_launch") == G:
@@ -293,7 +295,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel_us_mean": kmean, "bytes_per_launch": bytes_per_launch,
-                     "kernel": "k_wave<17, fp32>"},
+                     "kernel": "k_wave<17, fp32> (one wave per row)"},
         "cpu_baseline": cpu,
         "one_batch_per_launch": {"rows_per_s": single, "us_per_launch": ms1 * 1e3 / l1,
                                  "rows_per_s_streams": multi, "streams": args.streams},

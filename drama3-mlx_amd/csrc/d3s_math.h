@@ -16,11 +16,12 @@
  *     "Software Manual for the Elementary Functions", 1980) with a two-part ln2,
  *     then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2 (truncation
  *     error < 6e-9 relative), then exact scaling by 2^n.
- *   - d3s_logf: y = 2^e * m with m in [sqrt(2)/2, sqrt(2)), s = (m-1)/(m+1),
- *     log(m) = 2*atanh(s) = 2s + 2s^3/3 + ... + 2s^9/9 (|s| <= 0.1716, truncation
+ *   - d3s_logf: y = 2^e * m with m in [sqrt(2)/2, sqrt(2)), f = m - 1,
+ *     s = f/(2+f), log(m) = 2*atanh(s) evaluated as f - s*(f - R) with
+ *     R = s*z*(2/3 + 2z/5 + 2z^2/7 + 2z^3/9), z = s^2 (|s| <= 0.1716, truncation
  *     error < 3e-9 relative), log(y) = e*ln2 + log(m) with the two-part ln2.
  * Both are checked against double-precision libm over dense sweeps by the
- * tests (error <= 2 ulp), on the CPU and, bit for bit, on the GPU.
+ * tests (error below 1 ulp), on the CPU and, bit for bit, on the GPU.
  */
 #ifndef D3S_MATH_H
 #define D3S_MATH_H
