@@ -35,7 +35,7 @@ namespace d3s {
 namespace {
 
 constexpr int WR = 4;   /* rows (waves) per 256-thread workgroup */
-constexpr int LCAP = 8; /* entries of a lane's private candidate list */
+constexpr int LCAP = 8;  /* candidates a lane files before the exact select takes over */
 /* relative error bound of v_exp_f32 (2^x) for every input with a normal
  * result; the GPU tests check it over dense samples of [-126, 1] */
 constexpr float EPS_EXP2 = 0x1p-21f;
@@ -45,7 +45,6 @@ constexpr int BUFFER_FLAGS = 0x00020000;
 constexpr float LN2_F = 0.693147182f;
 
 struct __align__(16) WaveLds {
-  uint2 lst[LCAP * WAVE]; /* lane-private candidate lists, entry-major: (logit bits, index) */
   uint64_t keys[WAVE + 1]; /* dense candidate keys (+ a zero pad for pair reads) */
   uint64_t ranked[WAVE];   /* keys by rank */
   uint32_t hist[NB];       /* radix-select histogram */
@@ -198,6 +197,12 @@ struct Chunks {
       word = on ? 0xff800000u : word;
   }
   __device__ __forceinline__ static int pos(int pos0, int i) { return pos0 + (i / EPC) * WAVE * EPC + (i % EPC); }
+  /* opaque to the compiler: a pass after this unpacks the words again
+   * instead of holding every unpacked element from the pass before */
+  __device__ __forceinline__ void launder() {
+#pragma unroll
+    for (int j = 0; j < CPT * 4; j++) asm volatile("" : "+v"(w[j]));
+  }
 };
 
 /* What a row's rare exact paths need.  They read the row again (from L2), a
@@ -369,6 +374,8 @@ __device__ __forceinline__ float slow_max(const RowRef &R) {
 
 template <int CPT, bool BF16>
 struct WaveRow {
+  /* candidates per lane read again while the row is still in L2 */
+  static constexpr int EARLY = 3;
   using C = Chunks<CPT, BF16>;
   static constexpr int ES = BF16 ? 2 : 4;
   static constexpr int EPC = C::EPC;
@@ -533,27 +540,69 @@ struct WaveRow {
      * {L >= tau_lo} holds every element whose x reaches the k-th largest */
     const float tau_lo = need_sel ? __builtin_inff() : tau - (fabsf(tau) * 0x1p-21f + T * 0x1p-120f);
 
-    /* ---- one pass: the fast row sum, and the candidates as a bit per
-     * element (element i of word i / 32 at bit 31 - i % 32, no branches) */
+    /* ---- the candidates as a bit per element (element i of word i / 32
+     * at bit 31 - i % 32), no branches */
     constexpr int NWORD = (NV + 31) / 32;
-    float acc[EPC];
-#pragma unroll
-    for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
     uint32_t bits[NWORD];
 #pragma unroll
     for (int w = 0; w < NWORD; w++) bits[w] = 0u;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-      const float v = c.val(i);
-      acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(v, cf, b));
       /* bits = 2 bits + (v >= tau_lo): the compare's lane mask as the carry in
        * (two wait states between a VALU write of vcc and its use as a mask) */
       asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
           : "+v"(bits[i / 32])
-          : "v"(v), "v"(tau_lo)
+          : "v"(c.val(i)), "v"(tau_lo)
           : "vcc");
     }
     if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
+    const uint32_t tot = wave_sum_u32((uint32_t)cnt);
+    if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
+    /* each lane takes its candidates in element order: the first EARLY are
+     * read again now, while the row is still in L2 (the reads land during the
+     * row sum below), the rest, rarely, after it */
+    auto next_cand = [&]() {
+      int i = 0;
+      bool found = false;
+#pragma unroll
+      for (int w = 0; w < NWORD; w++) {
+        const int e = __builtin_clz(bits[w] | 1u); /* bits[w] != 0 below */
+        const bool here = !found && bits[w] != 0u;
+        i = here ? 32 * w + e : i;
+        bits[w] = here ? bits[w] & ~(0x80000000u >> e) : bits[w];
+        found = found || here;
+      }
+      return pos0 + (i / EPC) * WAVE * EPC + (i % EPC);
+    };
+    auto read_logit = [&](int p) {
+      return BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[p]) : ((const float *)rowp)[p];
+    };
+    int cpos[EARLY];
+    float cl[EARLY];
+#pragma unroll
+    for (int q = 0; q < EARLY; q++) {
+      cpos[q] = 0;
+      cl[q] = 0.0f;
+    }
+    if (!need_sel) {
+#pragma unroll
+      for (int q = 0; q < EARLY; q++) {
+        if (q > 0 && !__ballot(q < cnt)) break;
+        cpos[q] = next_cand();
+        if (q < cnt) cl[q] = read_logit(cpos[q]);
+      }
+    }
+
+    /* ---- the fast row sum */
+    if (BF16) c.launder();
+    float acc[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(c.val(i), cf, b));
 #pragma unroll
     for (int w = EPC / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -567,49 +616,20 @@ struct WaveRow {
     const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
                         (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
 
-    int cnt = 0;
-#pragma unroll
-    for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
-    const uint32_t tot = wave_sum_u32((uint32_t)cnt);
-    if (__ballot(cnt > LCAP) || tot > (uint32_t)WAVE) need_sel = true;
     int n;
     if (need_sel) {
       n = exact_select<CPT, BF16>(ref());
     } else {
-      /* each lane takes its candidates in element order, reads their logits
-       * again (L2) and files their keys; slots excl .. excl + cnt - 1 */
       const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
-      int cpos[LCAP];
 #pragma unroll
-      for (int q = 0; q < LCAP; q++) {
-        cpos[q] = 0;
-        if (q > 0 && !__ballot(q < cnt)) break;
-        int i = 0;
-        bool found = false;
-#pragma unroll
-        for (int w = 0; w < NWORD; w++) {
-          const int e = __builtin_clz(bits[w] | 1u); /* bits[w] != 0 below */
-          const bool here = !found && bits[w] != 0u;
-          i = here ? 32 * w + e : i;
-          bits[w] = here ? bits[w] & ~(0x80000000u >> e) : bits[w];
-          found = found || here;
-        }
-        cpos[q] = pos0 + (i / EPC) * WAVE * EPC + (i % EPC);
-      }
-      float cl[LCAP];
-#pragma unroll
-      for (int q = 0; q < LCAP; q++) {
-        cl[q] = 0.0f;
-        if (q < cnt) {
-          if (BF16)
-            cl[q] = d3s_bf16_to_f32(((const uint16_t *)rowp)[cpos[q]]);
-          else
-            cl[q] = ((const float *)rowp)[cpos[q]];
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < LCAP; q++)
+      for (int q = 0; q < EARLY; q++)
         if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(cl[q], T, y, true), cpos[q]);
+#pragma unroll 1
+      for (int q = EARLY; q < LCAP; q++) {
+        if (!__ballot(q < cnt)) break;
+        const int p = next_cand();
+        if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(read_logit(p), T, y, true), p);
+      }
       n = (int)tot;
     }
     finish(n, M, lse, false, eps_s, noise);
