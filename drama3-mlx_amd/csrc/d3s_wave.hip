@@ -1,7 +1,8 @@
 /* The one-wave-per-row sampler kernel (gfx950, wave64): k_wave.
  *
  * Each wave samples one row held in its registers (up to 96 fp32 or 128 bf16
- * elements per lane); a 256-thread workgroup carries four independent rows and has no
+ * elements per lane); a 256-thread workgroup carries four independent rows (a
+ * launch of at most 1024 rows takes one per workgroup) and has no
  * workgroup barrier, so a launch of many rows streams at HBM rate while a
  * launch of one row runs on a single wave.  Semantics are the oracle's
  * (src/sampling.c:1-3,:22-49,:53-140), bit for bit:
@@ -35,6 +36,7 @@ namespace d3s {
 namespace {
 
 constexpr int WR = 4;   /* rows (waves) per 256-thread workgroup */
+constexpr int WR_SPREAD_ROWS = 1024; /* up to this many rows, one row per workgroup */
 constexpr int LCAP = 8;  /* candidates a lane files before the exact select takes over */
 /* relative error bound of v_exp_f32 (2^x) for every input with a normal
  * result; the GPU tests check it over dense samples of [-126, 1] */
@@ -649,7 +651,7 @@ void k_wave(SampleArgs a) {
   __shared__ WaveLds lds_all[WR];
   /* wave-uniform (the compiler cannot see it): row and all that follows stay scalar */
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
-  const int row = (int)blockIdx.x * WR + wid;
+  const int row = (int)(blockIdx.x * (blockDim.x / WAVE)) + wid;
   if (row >= a.n_rows) return;
   WaveRow<CPT, BF16> r(a, lds_all[wid], row);
   r.V = a.vocab;
@@ -673,8 +675,11 @@ constexpr int wave_vmax(int off) {
 template <int CPT, bool BF16>
 bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
   if (a.vocab > wave_vmax<CPT, BF16>(max_off)) return false;
-  const unsigned blocks = (unsigned)((a.n_rows + WR - 1) / WR);
-  hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3(blocks), dim3(WAVE * WR), 0, s, a);
+  /* a launch too small to fill the chip spreads its rows one per workgroup
+   * over more CUs; larger ones pack WR, which keeps the CUs fuller */
+  const int wr = a.n_rows <= WR_SPREAD_ROWS ? 1 : WR;
+  const unsigned blocks = (unsigned)((a.n_rows + wr - 1) / wr);
+  hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3(blocks), dim3(WAVE * wr), 0, s, a);
   return true;
 }
 

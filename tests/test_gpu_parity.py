@@ -166,17 +166,18 @@ def test_top_p_on_a_cumulative_boundary(gpu, oracle):
 
 @pytest.mark.parametrize("bf16", [False, True])
 def test_many_rows_per_row_parameters(gpu, oracle, bf16):
-    """1001 rows (four rows per workgroup, a ragged last workgroup), a
-    different temperature and top_p on every row."""
+    """1501 rows (past 1024 rows the wave kernel packs four rows per
+    workgroup: the last one is ragged), a different temperature and top_p on
+    every row."""
     rng = np.random.default_rng(14)
-    x = (rng.standard_normal((1001, 4097)) * 2.5).astype(np.float32)
-    x[np.arange(1001), rng.integers(0, 4097, 1001)] += 8.0
-    T = rng.uniform(0.2, 1.5, 1001).astype(np.float32)
-    top_p = rng.uniform(0.3, 1.0, 1001).astype(np.float32)
-    u = oracle.uniform(14, 0, 1001, 30)
+    x = (rng.standard_normal((1501, 4097)) * 2.5).astype(np.float32)
+    x[np.arange(1501), rng.integers(0, 4097, 1501)] += 8.0
+    T = rng.uniform(0.2, 1.5, 1501).astype(np.float32)
+    top_p = rng.uniform(0.3, 1.0, 1501).astype(np.float32)
+    u = oracle.uniform(14, 0, 1501, 30)
     if bf16:
         x = W.f32_to_bf16_bits(x)
-    got, _ = compare(oracle, gpu, x, u, T, top_p, label="1001 rows")
+    got, _ = compare(oracle, gpu, x, u, T, top_p, label="1501 rows")
     # the fast row sum settles almost every row
     assert got["counters"][gpu.COUNTER_EXACT_LSE] < 50
 
