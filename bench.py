@@ -14,7 +14,8 @@ the mean launch duration, timed with HIP events on the launching stream
 around the back-to-back launches.  cpu_baseline = the C oracle (the port of the
 reference semantics; the reference's own CPU path needs mlx-c, absent here)
 on a bounded sample of the same workload, all host cores.
-Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32).
+Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), and
+launch times of C2, C4 and C5 at their own shapes (`other_configs`).
 """
 import argparse
 import json
@@ -178,6 +179,88 @@ def single_row_latency(n):
                 host_p50_us=float(np.median(h)), host_p90_us=float(np.percentile(h, 90)), rows=n)
 
 
+def other_configs(reps):
+    """Launch times of C2, C4 and C5 at their own shapes (BASELINE.json's
+    configs; C3 and C1 are the headline).  Events on one stream around
+    back-to-back launches.  C4 and C5 rotate over copies of the inputs
+    totalling over 600 MB (more than twice the 256 MB Infinity Cache), so the
+    reads come from HBM.  C2 (75 KB a launch) is a latency figure: the nine
+    codebook rows as nine one-row launches (as the tower samples them) and as
+    one nine-row launch, p50 over `reps` repetitions."""
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    out = {}
+    s = hiprt.Stream()
+    a, b = hiprt.Event(), hiprt.Event()
+    for name in ("C2", "C4", "C5"):
+        w = W.make(name, seed=5, uniforms=False)
+        x = w["logits"]
+        N, Vc = x.shape
+        k = w["k"]
+        es = x.itemsize
+        dt = d3s.DTYPE_F32 if x.dtype == np.float32 else d3s.DTYPE_BF16
+        b_row = Vc * es + k * 4 + 4 + 12 + (4 if w["banned"] is not None else 0)
+        per_launch = N * b_row
+        copies = 1 if name == "C2" else -(-600_000_000 // per_launch)
+        lg = hiprt.DeviceBuffer(copies * x.nbytes)
+        for c in range(copies):
+            lg.upload(x, offset=c * x.nbytes)
+        u = hiprt.DeviceBuffer(copies * N * k * 4)
+        for c in range(copies):
+            assert d3s.lib().d3s_uniform_fill(u.ptr + c * N * k * 4, N * k, 42, c, None) == 0
+        ban = hiprt.to_device(w["banned"]) if w["banned"] is not None else None
+        ids = hiprt.DeviceBuffer(4 * N)
+        T, P = float(w["temperature"]), float(w["top_p"])
+
+        def launch(c, r0=0, n=N):
+            return d3s.sample_raw(lg.ptr + c * x.nbytes + r0 * Vc * es, dt, n, Vc, Vc,
+                                  u.ptr + (c * N + r0) * k * 4, k, T, P,
+                                  ban.ptr + 4 * r0 if ban is not None else None, ids.ptr, stream=s.ptr)
+        hiprt.synchronize()
+        if name == "C2":
+            fused, rows = [], []
+            for i in range(reps + 20):
+                a.record(s)
+                assert launch(0) == 0
+                b.record(s)
+                b.synchronize()
+                t_f = a.elapsed_ms(b) * 1e3
+                a.record(s)
+                for r in range(N):
+                    assert launch(0, r, 1) == 0
+                b.record(s)
+                b.synchronize()
+                if i >= 20:
+                    fused.append(t_f)
+                    rows.append(a.elapsed_ms(b) * 1e3)
+            out[name] = {"shape": [N, Vc], "dtype": "bf16", "k": k,
+                         "one_launch_p50_us": float(np.median(fused)),
+                         "nine_launches_p50_us": float(np.median(rows))}
+            log(f"C2: one 9-row launch p50 {out[name]['one_launch_p50_us']:.2f} us, "
+                f"9 one-row launches p50 {out[name]['nine_launches_p50_us']:.2f} us")
+            continue
+        for c in range(copies):
+            assert launch(c) == 0
+        n = max(2 * copies, 20)
+        a.record(s)
+        for i in range(n):
+            assert launch(i % copies) == 0
+        b.record(s)
+        b.synchronize()
+        us = a.elapsed_ms(b) * 1e3 / n
+        gbs = per_launch / (us * 1e-6) / 1e9
+        out[name] = {"shape": [N, Vc], "dtype": "bf16" if es == 2 else "f32", "k": k,
+                     "us_per_launch": us, "rows_per_s": N / (us * 1e-6),
+                     "bytes_per_launch": per_launch, "achieved_GBs": gbs,
+                     "frac": gbs / HBM_PEAK_GBS}
+        log(f"{name}: {us:.1f} us per launch of {N} rows, {gbs:.0f} GB/s "
+            f"({100 * gbs / HBM_PEAK_GBS:.1f} % of HBM peak)")
+        del lg, u
+    s.destroy()
+    return out
+
+
 def cpu_baseline(seconds):
     """The oracle on all host cores over a bounded sample of C3 rows."""
     import d3s_oracle
@@ -212,6 +295,7 @@ def main():
     ap.add_argument("--single-rows", type=int, default=10000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip the C2 / C4 / C5 figures")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="N",
                     help="only run the copy calibration and N headline launches (for --pmc runs)")
     args = ap.parse_args()
@@ -260,6 +344,9 @@ def main():
     if args.single_rows:
         lat = single_row_latency(args.single_rows)
         log(f"C1 single row: p50 {lat['p50_us']:.2f} us (GPU), host p50 {lat['host_p50_us']:.2f} us")
+    others = None
+    if not args.no_other:
+        others = other_configs(200)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_k_wave_C3.json")
     if os.path.exists(tpath):
@@ -302,6 +389,7 @@ def main():
         "p50_us_single_row": lat["p50_us"] if lat else None,
         "event_floor_us": floor_us,
         "single_row": lat,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
 

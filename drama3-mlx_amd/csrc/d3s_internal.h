@@ -53,6 +53,10 @@ bool launch_wave(const SampleArgs &a, Dtype dt, hipStream_t s);
 int wave_max_vocab(Dtype dt);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
+/* Launch the wide kernel: one 1024-thread workgroup per row, the row in the
+ * registers of its 16 waves (k <= 64, V <= wide_max_vocab(dt)). */
+bool launch_wide(const SampleArgs &a, Dtype dt, hipStream_t s);
+int wide_max_vocab(Dtype dt);
 /* Launch the fused one-workgroup-per-row kernel (k <= 64, V within the
  * register-resident limit).  Returns false if no instantiation fits. */
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);

@@ -28,7 +28,7 @@
  *  over order-preserving keys of x; T not finite or |m| beyond 2^24 -> every
  *  quantity per element from x exactly (exact_row).
  */
-#include "d3s_device.h"
+#include "d3s_generic.h"
 
 #pragma clang fp contract(off)
 
@@ -638,6 +638,294 @@ struct WaveRow {
   }
 };
 
+/* ------------------------------------------------------------------------
+ * k_wide: one 1024-thread workgroup per row too wide for one wave (k <= 64).
+ * Wave w holds chunks [w * CPT * 64, (w + 1) * CPT * 64) of the row in its
+ * registers and runs the wave kernel's passes over them; the workgroup
+ * combines in LDS the maxima, the threshold (the k-th largest of its 1024
+ * lane maxima, by 8-bit histogram passes), the candidates and the fast row
+ * sums, and wave 0 runs the tail.  A row that needs an exact path (T not
+ * finite, logits too large for the fast sum, more candidates than the
+ * workgroup files, or a top-p cut within the fast sum's margin) is sampled
+ * again by the generic row procedure: the same definition, bit for bit. */
+constexpr int WIDE_NW = 16;  /* waves per row */
+constexpr int WCAP = 512;    /* candidates the workgroup files */
+
+struct __align__(16) WideLds {
+  uint64_t keys[WCAP + 2]; /* candidates, then zero pads for the pair reads */
+  uint64_t ranked[WAVE];
+  uint32_t hist[NB];
+  float buf[WAVE], buf2[WAVE];
+  float wmax[WIDE_NW], wsum[WIDE_NW];
+  uint32_t wcnt[WIDE_NW];
+  uint32_t exact;
+};
+
+template <int CPT, bool BF16>
+__global__ __launch_bounds__(WAVE *WIDE_NW) __attribute__((amdgpu_waves_per_eu(4)))
+void k_wide(SampleArgs a) {
+  using C = Chunks<CPT, BF16>;
+  constexpr int ES = BF16 ? 2 : 4, EPC = C::EPC, NV = C::NV, NW = WIDE_NW;
+  constexpr int EARLY = 3;
+  __shared__ WideLds S;
+  __shared__ uint64_t glist[KF]; /* the generic procedure's sort list */
+  const int row = (int)blockIdx.x;
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int lane = lane_id();
+  const int V = a.vocab, k = a.k;
+  int kpow = 2;
+  while (kpow < k) kpow <<= 1;
+  const RowP rp = row_params(a, row);
+  const float T = rp.T, top_p = rp.top_p;
+  const int banned = rp.banned;
+  const bool t_finite = T < __builtin_inff(); /* false for +inf and NaN */
+  const float y = 1.0f / T;
+  const float uval = (wid == 0 && lane < k) ? a.u[(size_t)row * k + lane] : 0.0f;
+  /* a chunk never crosses a page, so the bytes outside the row it covers are
+   * readable; they become -inf below */
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
+  const int off = (int)(((uintptr_t)rowp & 15u) / ES);
+  const uint4 *src = (const uint4 *)(rowp - off * ES);
+  const int nchunks = (off + V + EPC - 1) / EPC;
+  const int cbase = wid * CPT * WAVE; /* this wave's first chunk */
+  C c;
+  c.load(src + cbase, min(max(nchunks - cbase, 0), CPT * WAVE), lane);
+  const int pos0 = (cbase + lane) * EPC - off;
+  auto valid = [&](int i) { return (unsigned)C::pos(pos0, i) < (unsigned)V; };
+#pragma unroll
+  for (int j = 0; j < CPT; j++) {
+    const int p_lo = (cbase + j * WAVE) * EPC - off; /* wave-uniform */
+    if (p_lo < 0 || p_lo + WAVE * EPC > V) {
+#pragma unroll
+      for (int e = 0; e < EPC; e++) c.mask(j * EPC + e, !valid(j * EPC + e));
+    }
+  }
+  if ((unsigned)banned < (unsigned)V) {
+    const int bc = (banned + off) / EPC, eb = (banned + off) % EPC;
+    if (bc / (CPT * WAVE) == wid) {
+      const int jb = (bc % (CPT * WAVE)) / WAVE, lb = bc % WAVE;
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if (j == jb) {
+#pragma unroll
+          for (int e = 0; e < EPC; e++) c.mask(j * EPC + e, lane == lb && e == eb);
+        }
+    }
+  }
+
+  /* ---- row max of the logits; NaN propagates */
+  const float ninf = -__builtin_inff();
+  float lm = ninf;
+#pragma unroll
+  for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
+  {
+    const float wm = wave_maximum_f(lm);
+    if (lane == 0) S.wmax[wid] = wm;
+  }
+  if (threadIdx.x == 0) S.exact = 0u;
+  const float noise = wid == 0 ? -d3s_logf(1.0f - uval) : 0.0f; /* the race's noise needs only u */
+  __syncthreads();
+  bool slow = !t_finite;
+  float M = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f;
+  if (!slow) {
+    float Lmax = S.wmax[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) Lmax = fmaximum(Lmax, S.wmax[w]);
+    if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
+      if (wid == 0) wave_write_special(a, row, false);
+      return;
+    }
+    M = scale_logit(Lmax, T, y, true); /* = max x */
+    if (M == __builtin_inff() || M == ninf) {
+      if (wid == 0) wave_write_special(a, row, M == ninf);
+      return;
+    }
+    cf = LOG2E_F / T;
+    const float h = Lmax * cf;
+    slow = !(fabsf(h) < 0x1p24f);
+    b = -h;
+    delta = __builtin_fmaf(Lmax, cf, b); /* Lmax * cf + b exactly */
+  }
+  if (slow) {
+    generic_row<BF16>(a, row, kpow, glist);
+    return;
+  }
+
+  /* ---- tau: the k-th largest of the 1024 lane maxima to 24 bits of its
+   * order key (a lower bound: at least k elements reach it) */
+  const uint32_t lkey = d3s_ordkey(lm);
+  uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)k;
+#pragma unroll
+  for (int pass = 0; pass < 3; pass++) {
+    const int shift = 24 - 8 * pass;
+    if (threadIdx.x < NB) S.hist[threadIdx.x] = 0u;
+    __syncthreads();
+    if ((lkey & pmask) == prefix) atomicAdd(&S.hist[(lkey >> shift) & 255u], 1u);
+    __syncthreads();
+    const BinSel bs = wave_find_bin<false>(S.hist, need); /* 1024 keys >= need */
+    prefix |= bs.bin << shift;
+    pmask |= 0xffu << shift;
+    need -= bs.above;
+    __syncthreads(); /* every wave has read the histogram */
+  }
+  /* keys below -FLT_MAX's: the k-th lane max is -inf */
+  bool need_sel = (a.flags & FLAG_EXACT_SELECT) != 0 || prefix < d3s_ordkey(-0x1.fffffep127f);
+  const float tau = d3s_from_ordkey(prefix);
+  /* below every logit whose x ties with tau's (as in the wave kernel) */
+  const float tau_lo = need_sel ? __builtin_inff() : tau - (fabsf(tau) * 0x1p-21f + T * 0x1p-120f);
+
+  /* ---- the candidates as a bit per element, no branches */
+  if (BF16) c.launder();
+  constexpr int NWORD = (NV + 31) / 32;
+  uint32_t bits[NWORD];
+#pragma unroll
+  for (int w = 0; w < NWORD; w++) bits[w] = 0u;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+        : "+v"(bits[i / 32])
+        : "v"(c.val(i)), "v"(tau_lo)
+        : "vcc");
+  }
+  if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
+  int cnt = 0;
+#pragma unroll
+  for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
+  const uint32_t wtot = wave_sum_u32((uint32_t)cnt);
+  const bool over = __ballot(cnt > LCAP) != 0ull;
+  auto next_cand = [&]() {
+    int i = 0;
+    bool found = false;
+#pragma unroll
+    for (int w = 0; w < NWORD; w++) {
+      const int e = __builtin_clz(bits[w] | 1u); /* bits[w] != 0 below */
+      const bool here = !found && bits[w] != 0u;
+      i = here ? 32 * w + e : i;
+      bits[w] = here ? bits[w] & ~(0x80000000u >> e) : bits[w];
+      found = found || here;
+    }
+    return C::pos(pos0, i);
+  };
+  auto read_logit = [&](int p) {
+    return BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[p]) : ((const float *)rowp)[p];
+  };
+  /* the first candidates read again now, while the row is in L2 */
+  int cpos[EARLY];
+  float cl[EARLY];
+#pragma unroll
+  for (int q = 0; q < EARLY; q++) {
+    cpos[q] = 0;
+    cl[q] = 0.0f;
+  }
+  if (!need_sel && !over) {
+#pragma unroll
+    for (int q = 0; q < EARLY; q++) {
+      if (q > 0 && !__ballot(q < cnt)) break;
+      cpos[q] = next_cand();
+      if (q < cnt) cl[q] = read_logit(cpos[q]);
+    }
+  }
+
+  /* ---- the fast row sum */
+  if (BF16) c.launder();
+  float acc[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(c.val(i), cf, b));
+#pragma unroll
+  for (int w = EPC / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
+  {
+    const float ws = wave_sum_f(acc[0]);
+    if (lane == 0) {
+      S.wsum[wid] = ws;
+      S.wcnt[wid] = over ? 0xffffffffu : wtot;
+    }
+  }
+  __syncthreads();
+  uint32_t tot = 0u, base = 0u;
+  float sp = S.wsum[0];
+#pragma unroll
+  for (int w = 0; w < NW; w++) {
+    const uint32_t t = S.wcnt[w];
+    need_sel = need_sel || t == 0xffffffffu;
+    base += w < wid ? t : 0u;
+    tot += t;
+    if (w > 0) sp = sp + S.wsum[w]; /* the same order in every wave */
+  }
+  need_sel = need_sel || tot > (uint32_t)WCAP;
+  if (need_sel) {
+    if (threadIdx.x == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_SELECT], 1u);
+    generic_row<BF16>(a, row, kpow, glist);
+    return;
+  }
+  const float lse = M + (d3s_logf(sp) - delta * LN2_F);
+  /* relative error bound of 2^-delta S' against the exact row sum: the wave
+   * kernel's, with NW - 1 more roundings for the sum over the waves */
+  const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
+                      (float)(CPT + 11 + NW) * 0x1p-24f + (float)V * 0x1p-40f;
+
+  /* ---- file the keys: this wave's slots from base on, lane by lane */
+  {
+    const uint32_t excl = base + wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
+#pragma unroll
+    for (int q = 0; q < EARLY; q++)
+      if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(cl[q], T, y, true), cpos[q]);
+#pragma unroll 1
+    for (int q = EARLY; q < LCAP; q++) {
+      if (!__ballot(q < cnt)) break;
+      const int p = next_cand();
+      if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(read_logit(p), T, y, true), p);
+    }
+  }
+  if (threadIdx.x == 0) {
+    S.keys[tot] = 0ull; /* pads below every key */
+    S.keys[tot + 1] = 0ull;
+  }
+  __syncthreads();
+  /* ---- ranks: candidate t counts the keys above its own */
+  if (threadIdx.x < tot) {
+    const uint64_t my = S.keys[threadIdx.x];
+    const ulonglong2 *k2 = (const ulonglong2 *)S.keys;
+    int rank = 0;
+#pragma unroll 4
+    for (int j2 = 0; j2 < (int)(tot + 1) / 2; j2++) {
+      const ulonglong2 q = k2[j2];
+      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
+    }
+    if (rank < k) S.ranked[rank] = my;
+  }
+  __syncthreads();
+  /* ---- the tail on wave 0 (the wave kernel's, with its margin test) */
+  if (wid == 0) {
+    const bool act = lane < k;
+    const uint64_t key = act ? S.ranked[lane] : 0ull;
+    const float v = key_x(key);
+    const int idx = key_idx(key);
+    const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    float cc, spp;
+    wave_seq_prefix2(act ? d3s_expf(v - lse) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
+    const float D = lse - readlane_f(v, k - 1);
+    const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
+    const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
+    const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+    const bool exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
+                       (a.flags & FLAG_EXACT_LSE) != 0;
+    if (exact) {
+      if (lane == 0) {
+        S.exact = 1u;
+        if (a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+      }
+    } else {
+      wave_race_prefix(a, row, idx, cc, ep, spp, noise, top_p);
+    }
+  }
+  __syncthreads();
+  if (S.exact) generic_row<BF16>(a, row, kpow, glist);
+}
+
 /* waves per SIMD the register budget is set for (the row's 4 * CPT
  * registers plus the rest; checked for spills at build time) */
 template <int CPT, bool BF16>
@@ -683,12 +971,32 @@ bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
   return true;
 }
 
+/* the widest row k_wide<CPT, BF16> holds, at any start offset */
+template <int CPT, bool BF16>
+constexpr int wide_vmax() {
+  return WIDE_NW * WAVE * CPT * (16 / (BF16 ? 2 : 4)) - (16 / (BF16 ? 2 : 4) - 1);
+}
+
+template <int CPT, bool BF16>
+bool try_wide(const SampleArgs &a, hipStream_t s) {
+  if (a.vocab > wide_vmax<CPT, BF16>()) return false;
+  hipLaunchKernelGGL((k_wide<CPT, BF16>), dim3(a.n_rows), dim3(WAVE * WIDE_NW), 0, s, a);
+  return true;
+}
+
 }  // namespace
 
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s) {
   if (n <= 0) return;
   const int B = 256;
   hipLaunchKernelGGL(k_exp2, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, in, out, n);
+}
+
+int wide_max_vocab(Dtype dt) { return dt == DT_F32 ? wide_vmax<19, false>() : wide_vmax<19, true>(); }
+
+bool launch_wide(const SampleArgs &a, Dtype dt, hipStream_t s) {
+  if (a.k > KF) return false;
+  return dt == DT_F32 ? try_wide<19, false>(a, s) : try_wide<19, true>(a, s);
 }
 
 int wave_max_vocab(Dtype dt) { return dt == DT_F32 ? wave_vmax<24, false>(3) : wave_vmax<16, true>(7); }

@@ -225,6 +225,89 @@ def test_shapes(gpu, oracle, V, k):
     compare(oracle, gpu, xb, u, 0.7, 0.8, label=f"V={V} bf16")
 
 
+WIDE_MAX = {False: 77821, True: 155641}  # k_wide: 16 waves x 19 chunk rows, any start offset
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_wide_rows_at_and_past_the_limit(gpu, oracle, bf16):
+    """Rows held by a whole workgroup's registers, at the widest such row and
+    one past it (the generic kernel's); per-row T and top_p."""
+    rng = np.random.default_rng(31 + bf16)
+    for V in (WIDE_MAX[bf16], WIDE_MAX[bf16] + 1, 33000):
+        N = 6
+        x = (rng.standard_normal((N, V)) * 3).astype(np.float32)
+        x[np.arange(N), rng.integers(0, V, N)] += 7.0
+        T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+        top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
+        u = oracle.uniform(31, 0, N, 30)
+        if bf16:
+            x = W.f32_to_bf16_bits(x)
+        compare(oracle, gpu, x, u, T, top_p, label=f"wide V={V} bf16={bf16}")
+
+
+@pytest.mark.parametrize("flags", [0, 1, 2, 4])
+def test_wide_paths_give_the_same_bits(gpu, oracle, flags):
+    """C4 rows through the wide kernel's fast path and each forced exact path
+    (the generic row procedure), and through the generic kernel."""
+    w = W.make("C4", rows=12, seed=8, uniforms=False)
+    u = oracle.uniform(8, 0, 12, 30)
+    got, _ = compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], flags=flags,
+                     label=f"C4 flags={flags}")
+    if flags == 2:
+        assert got["counters"][gpu.COUNTER_EXACT_LSE] == 12
+    if flags == 4:
+        assert got["counters"][gpu.COUNTER_EXACT_SELECT] == 12
+
+
+def test_wide_unaligned_banned_and_edge_rows(gpu, oracle):
+    rng = np.random.default_rng(33)
+    V, stride, N = 100000, 100003, 14
+    x = (rng.standard_normal((N, stride)) * 3).astype(np.float32)
+    x[0, 5] = np.nan                 # refused
+    x[1, 99999] = np.inf             # refused (last element)
+    x[2, :] = -np.inf                # all masked: id 0
+    x[3, ::2] = -np.inf              # half masked
+    x[4, :] = 1.5                    # every element ties: too many candidates, exact select
+    x[5, 40000:40010] = 1e30         # logits too large for the fast row sum
+    x[6, :] = np.round(x[6])         # heavy ties across the k-th place
+    x[7, 0] = 40.0                   # the maximum at the row start
+    x[8, V - 1] = 40.0               # the maximum at the row end
+    ban = np.full(N, -1, np.int32)
+    ban[7], ban[8], ban[9] = 0, V - 1, int(np.argmax(x[9, :V]))
+    u = oracle.uniform(33, 0, N, 30)
+    for bf16 in (False, True):
+        xs = W.f32_to_bf16_bits(x) if bf16 else x
+        got, _ = compare(oracle, gpu, xs, u, 0.8, 0.9, banned=ban, row_stride=stride, vocab=V,
+                         label=f"wide edge rows bf16={bf16}")
+        assert got["ids"][0] == -1 and got["ids"][1] == -1 and got["ids"][2] == 0
+    for T in (np.inf, 0.0, 1e-5):
+        compare(oracle, gpu, x[6:12], u[6:12], T, 0.9, row_stride=stride, vocab=V,
+                label=f"wide rows T={T}")
+
+
+def test_wide_top_p_on_a_cumulative_boundary(gpu, oracle):
+    """top_p one ulp either side of a row's own cumulative value: every row is
+    within the fast sum's margin and takes the exact fallback."""
+    w = W.make("C4", rows=8, seed=9, uniforms=False)
+    u = oracle.uniform(9, 0, 8, 30)
+    x = w["logits"]
+    xf = (x.astype(np.uint32) << 16).view(np.float32)
+    top_p = np.empty(8, np.float32)
+    for r in range(8):
+        o = oracle.sample(x[r:r + 1], u[r:r + 1], 1.0, 2.0)
+        lse = o["lse"][0]
+        xs = np.sort(xf[r])[::-1][:30]
+        c = np.float32(0)
+        cs = []
+        for v in xs:
+            c = np.float32(c + oracle.expf(np.array([v - lse], np.float32))[0])
+            cs.append(c)
+        j = 1 + r % 5
+        top_p[r] = np.nextafter(cs[j], np.float32(0 if r % 2 else 2))
+    got, _ = compare(oracle, gpu, x, u, 1.0, top_p, label="wide top_p on a boundary")
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] == 8
+
+
 def test_strided_and_unaligned_rows(gpu, oracle):
     rng = np.random.default_rng(13)
     for stride, V in [(4099, 4097), (4097, 4000), (301, 300), (8195, 8190)]:
