@@ -67,6 +67,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   if (!generic && d3s::launch_wave(a, dt, s)) return launched();
   if (!generic && d3s::launch_fused(a, dt, s)) return launched();
   if (!generic && d3s::launch_wide(a, dt, s)) return launched();
+  if (!generic && d3s::launch_topp(a, dt, s)) return launched();
   if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
   return launched();
 }

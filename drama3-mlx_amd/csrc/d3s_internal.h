@@ -62,6 +62,9 @@ int wide_max_vocab(Dtype dt);
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);
 /* Largest V the fused kernel accepts for this dtype. */
 int fused_max_vocab(Dtype dt);
+/* Launch the ranked-nucleus kernel (k > 64, V <= topp_max_vocab()). */
+bool launch_topp(const SampleArgs &a, Dtype dt, hipStream_t s);
+int topp_max_vocab();
 /* Launch the streaming generic kernel (any V, k <= generic_max_k()). */
 bool launch_generic(const SampleArgs &a, Dtype dt, hipStream_t s);
 int generic_max_k();

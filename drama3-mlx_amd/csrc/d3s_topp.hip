@@ -1,0 +1,289 @@
+/* The ranked-nucleus kernel of the MI355X token sampler (gfx950, wave64):
+ * k_topp, for k > 64 (the reference's op-graph case, src/sampling.c:22-49,
+ * with k up to V: "top-k disabled") on rows of at most 1024 * EPT elements.
+ *
+ * One 1024-thread workgroup per row, EPT elements per thread in registers
+ * (element j * 1024 + t of thread t).  Every element needs its exact rank:
+ * the race draws u[rank] for every kept rank (src/sampling.c:45-47).
+ *
+ *  1. x = L / T exactly, classification, max m and the smallest finite x.
+ *  2. e = d3s_expf(x - m) per element: its 2^-40 fixed-point sum is the exact
+ *     row sum (lse = m + log S, src/sampling.c:37-38); with x_0 = m the same
+ *     e is each element's term of the renormalised softmax (:43-44).
+ *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 4096
+ *     buckets of m - x, scaled to the row's range (a non-decreasing function
+ *     of -x, so buckets are ordered), then each element counts the larger
+ *     keys of its own bucket.  The keys end in LDS in rank order.
+ *  4. The cut: exact fixed-point prefix sums of d3s_expf(x_r - lse) over
+ *     ranks (the op graph's cumsum, :39-42, rounded once), first r > 0 whose
+ *     prefix exceeds top_p.
+ *  5. The kept sum of e (exact, fixed point), the probabilities e * inv and
+ *     the race p / -log(1 - u[rank]), first maximum (:45-48).
+ * The definition is the generic kernel's for k > 64, bit for bit.  A row
+ * whose x fall in few buckets (heavy ties) is still exact, only slower. */
+#include "d3s_generic.h"
+
+#pragma clang fp contract(off)
+
+namespace d3s {
+namespace {
+
+constexpr int TBLOCK = 1024;
+constexpr int TNW = TBLOCK / WAVE;
+constexpr int NBK = 4096; /* buckets of finite x; bucket NBK holds -inf */
+
+/* workgroup reductions through LDS; every thread gets the result */
+struct TRed {
+  float f[TNW];
+  uint32_t lo[TNW], hi[TNW];
+  int r[TNW];
+};
+
+__device__ __forceinline__ float block_max_f(float v, TRed &R) {
+  v = wave_max_f(v);
+  const int wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) R.f[wid] = v;
+  __syncthreads();
+  float m = R.f[0];
+#pragma unroll
+  for (int w = 1; w < TNW; w++) m = fmaxf(m, R.f[w]);
+  return m;
+}
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
+  const uint64_t w = wave_sum_u64(v);
+  const int wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) {
+    R.lo[wid] = (uint32_t)w;
+    R.hi[wid] = (uint32_t)(w >> 32);
+  }
+  __syncthreads();
+  uint64_t s = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < TNW; w2++) s += ((uint64_t)R.hi[w2] << 32) | R.lo[w2];
+  return s;
+}
+
+__device__ __forceinline__ int block_min_i32(int v, TRed &R) {
+  v = wave_min_i32(v);
+  const int wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) R.r[wid] = v;
+  __syncthreads();
+  int m = R.r[0];
+#pragma unroll
+  for (int w = 1; w < TNW; w++) m = min(m, R.r[w]);
+  return m;
+}
+
+template <int EPT, bool BF16>
+__global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
+  __shared__ uint64_t keys[EPT * TBLOCK]; /* by bucket, then by rank */
+  __shared__ uint32_t bstart[NBK + 2];    /* bucket counts, then first slots */
+  __shared__ uint32_t bfill[NBK + 1];
+  __shared__ uint32_t scan_sh[TNW];
+  __shared__ TRed R;
+  __shared__ float sh_best[TNW];
+  __shared__ int sh_bestr[TNW], sh_besti[TNW];
+
+  const int row = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int V = a.vocab, k = a.k;
+  const RowP rp = row_params(a, row);
+  const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+
+  /* ---- 1. x, classification, max and smallest finite x */
+  float x[EPT];
+  uint32_t fl = 0u;
+  float xm = -__builtin_inff(), xl = __builtin_inff();
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    x[j] = -__builtin_inff();
+    if (i < V) {
+      const float xi = scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite);
+      x[j] = xi;
+      const uint32_t c = classify(xi);
+      fl |= c;
+      if (!(c & 1u)) xm = fmaxf(xm, xi);
+      if (!c) xl = fminf(xl, xi); /* finite */
+    }
+  }
+  const bool bad = __syncthreads_or((int)(fl & 1u)) != 0;
+  if (bad) {
+    write_special(a, row, false);
+    return;
+  }
+  const float m = block_max_f(xm, R);
+  if (m == -__builtin_inff()) {
+    write_special(a, row, true);
+    return;
+  }
+  const float xmin = -block_max_f(-xl, R);
+
+  /* ---- 2. e = exp(x - m), the exact row sum and lse */
+  float e[EPT];
+  uint64_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    e[j] = d3s_expf(x[j] - m); /* 0 for -inf (and for i >= V, x = -inf) */
+    acc += d3s_fix40(e[j]);
+  }
+  const uint64_t S = block_sum_u64(acc, R);
+  const float lse = m + d3s_logf(d3s_fixsum_to_f32(S));
+
+  /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
+  const float dmax = m - xmin;
+  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
+  for (int b = tid; b < NBK + 2; b += TBLOCK) bstart[b] = 0u;
+  for (int b = tid; b < NBK + 1; b += TBLOCK) bfill[b] = 0u;
+  __syncthreads();
+  int bk[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    int b = NBK;
+    if (x[j] != -__builtin_inff()) b = scale > 0.0f ? min((int)((m - x[j]) * scale), NBK - 1) : 0;
+    bk[j] = b;
+    if (i < V) atomicAdd(&bstart[b], 1u);
+  }
+  __syncthreads();
+  {
+    /* exclusive scan of the NBK + 1 counts: thread t owns 4 or 5 buckets */
+    constexpr int PER = (NBK + 1 + TBLOCK - 1) / TBLOCK;
+    uint32_t c[PER], loc = 0u;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+      const int b = tid * PER + q;
+      c[q] = b <= NBK ? bstart[b] : 0u;
+      loc += c[q];
+    }
+    uint32_t tot;
+    uint32_t run = block_excl_scan_u32(loc, scan_sh, tot);
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+      const int b = tid * PER + q;
+      if (b <= NBK) bstart[b] = run;
+      run += c[q];
+    }
+    if (tid == 0) bstart[NBK + 1] = tot;
+  }
+  __syncthreads();
+  uint64_t key[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    key[j] = composite_key(x[j], i);
+    if (i < V) keys[bstart[bk[j]] + atomicAdd(&bfill[bk[j]], 1u)] = key[j];
+  }
+  __syncthreads();
+  int rank[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    rank[j] = 0x7fffffff;
+    if (i < V) {
+      const uint32_t s0 = bstart[bk[j]], s1 = bstart[bk[j] + 1];
+      uint32_t r = s0;
+      for (uint32_t s = s0; s < s1; s++) r += keys[s] > key[j] ? 1u : 0u;
+      rank[j] = (int)r;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < EPT; j++)
+    if (rank[j] < V) keys[rank[j]] = key[j];
+  __syncthreads();
+
+  /* ---- 4. the cut: exact prefix sums of exp(x_r - lse) over ranks r < k */
+  const int RPT = (k + TBLOCK - 1) / TBLOCK;
+  const int r0 = tid * RPT;
+  uint64_t loc = 0;
+  for (int q = 0; q < RPT; q++) {
+    const int r = r0 + q;
+    if (r < k) loc += d3s_fix40(d3s_expf(key_x(keys[r]) - lse));
+  }
+  uint64_t P = block_excl_scan_u64(loc, R.lo, R.hi);
+  int cut_local = k;
+  for (int q = 0; q < RPT; q++) {
+    const int r = r0 + q;
+    if (r < k) {
+      P += d3s_fix40(d3s_expf(key_x(keys[r]) - lse));
+      if (r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > rp.top_p) cut_local = r;
+    }
+  }
+  const int cut = block_min_i32(cut_local, R);
+
+  /* ---- 5. kept sum, probabilities and the race */
+  uint64_t ks = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) ks += rank[j] < cut ? d3s_fix40(e[j]) : 0ull;
+  const float inv = 1.0f / d3s_fixsum_to_f32(block_sum_u64(ks, R));
+  float bs = -1.0f;
+  int br = 0x7fffffff, bi = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int r = rank[j];
+    if (r < k) {
+      const float p = r < cut ? e[j] * inv : 0.0f;
+      const float noise = -d3s_logf(1.0f - a.u[(size_t)row * k + r]);
+      const float score = p / noise;
+      const float sc = score > -1.0f ? score : -1.0f; /* NaN, -inf, <= -1 never beat -1 */
+      if (sc > bs || (sc == bs && r < br)) {
+        bs = sc;
+        br = r;
+        bi = j * TBLOCK + tid;
+      }
+      if (a.probs) a.probs[(size_t)row * k + r] = p;
+      if (a.cand) a.cand[(size_t)row * k + r] = j * TBLOCK + tid;
+    }
+  }
+  /* the first maximum over ranks: the greatest score, ties to the lower rank */
+  {
+    int rr = br;
+    float ss = bs;
+    wave_argmax(ss, rr);
+    const int ii = (int)readlane_u((uint32_t)bi, (int)__builtin_ctzll(__ballot(br == rr && bs == ss)));
+    if (lane == 0) {
+      sh_best[wid] = ss;
+      sh_bestr[wid] = rr;
+      sh_besti[wid] = ii;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float b = sh_best[0];
+    int r = sh_bestr[0], id = sh_besti[0];
+    for (int w = 1; w < TNW; w++)
+      if (sh_best[w] > b || (sh_best[w] == b && sh_bestr[w] < r)) {
+        b = sh_best[w];
+        r = sh_bestr[w];
+        id = sh_besti[w];
+      }
+    a.ids[row] = id;
+  }
+}
+
+template <int EPT, bool BF16>
+bool try_topp(const SampleArgs &a, hipStream_t s) {
+  if (a.vocab > EPT * TBLOCK) return false;
+  hipLaunchKernelGGL((k_topp<EPT, BF16>), dim3(a.n_rows), dim3(TBLOCK), 0, s, a);
+  return true;
+}
+
+}  // namespace
+
+int topp_max_vocab() { return 8 * TBLOCK; }
+
+bool launch_topp(const SampleArgs &a, Dtype dt, hipStream_t s) {
+  if (a.k <= KF) return false;
+  if (dt == DT_F32) return try_topp<5, false>(a, s) || try_topp<8, false>(a, s);
+  return try_topp<5, true>(a, s) || try_topp<8, true>(a, s);
+}
+
+}  // namespace d3s

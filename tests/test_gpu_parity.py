@@ -308,6 +308,47 @@ def test_wide_top_p_on_a_cumulative_boundary(gpu, oracle):
     assert got["counters"][gpu.COUNTER_EXACT_LSE] == 8
 
 
+@pytest.mark.parametrize("V,k", [(4097, 4097), (5120, 5120), (5121, 700), (8192, 8192), (8193, 300),
+                                 (300, 200)])
+def test_ranked_nucleus_rows(gpu, oracle, V, k):
+    """k > 64 (the op graph's semantics: every rank exact, prefix sums exact):
+    near-flat rows, per-row T and top_p, and the same bits as the generic
+    kernel."""
+    rng = np.random.default_rng([V, k, 3])
+    N = 24
+    x = (rng.standard_normal((N, V)) * 0.3).astype(np.float32)
+    T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    u = oracle.uniform(5, 0, N, k)
+    for bf16 in (False, True):
+        xs = W.f32_to_bf16_bits(x) if bf16 else x
+        a, _ = compare(oracle, gpu, xs, u, T, top_p, label=f"nucleus V={V} k={k} bf16={bf16}")
+        b, _ = compare(oracle, gpu, xs, u, T, top_p, flags=gpu.FLAG_GENERIC, label="nucleus generic")
+        assert np.array_equal(a["ids"], b["ids"])
+
+
+def test_ranked_nucleus_edge_rows(gpu, oracle):
+    rng = np.random.default_rng(34)
+    V, N = 4097, 12
+    x = (rng.standard_normal((N, V)) * 0.3).astype(np.float32)
+    x[0, 17] = np.nan                # refused
+    x[1, 4096] = np.inf              # refused
+    x[2, :] = -np.inf                # all masked
+    x[3, :] = 0.25                   # one bucket: every rank by index
+    x[4, :] = np.round(x[4] * 4)     # a few values, many ties each
+    x[5, ::3] = -np.inf              # a third masked
+    x[6, 100] = 30.0                 # one logit holds the nucleus
+    x[7, :2048] = -1e30              # a huge range of x
+    ban = np.where(np.arange(N) % 2 == 0, 0, -1).astype(np.int32)
+    ban[9] = 4096
+    u = oracle.uniform(34, 0, N, V)
+    u[10, :5] = 0.0                  # u = 0: noise 0, score infinite or NaN
+    got, _ = compare(oracle, gpu, x, u, 1.0, 0.95, banned=ban, label="nucleus edge rows")
+    assert got["ids"][0] == -1 and got["ids"][1] == -1 and got["ids"][2] == 0
+    for T in (np.inf, 0.0, 3.0):
+        compare(oracle, gpu, x[3:], u[3:], T, 0.9, label=f"nucleus rows T={T}")
+
+
 def test_strided_and_unaligned_rows(gpu, oracle):
     rng = np.random.default_rng(13)
     for stride, V in [(4099, 4097), (4097, 4000), (301, 300), (8195, 8190)]:
