@@ -34,7 +34,7 @@ constexpr int NBK = 4096; /* buckets of finite x; bucket NBK holds -inf */
 
 /* workgroup reductions through LDS; every thread gets the result */
 struct TRed {
-  float f[TNW];
+  float f[TNW], g[TNW];
   uint32_t lo[TNW], hi[TNW];
   int r[TNW];
 };
@@ -49,6 +49,26 @@ __device__ __forceinline__ float block_max_f(float v, TRed &R) {
 #pragma unroll
   for (int w = 1; w < TNW; w++) m = fmaxf(m, R.f[w]);
   return m;
+}
+
+/* the maxima of two values in one round */
+__device__ __forceinline__ void block_max2_f(float &v, float &w, TRed &R) {
+  v = wave_max_f(v);
+  w = wave_max_f(w);
+  const int wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) {
+    R.f[wid] = v;
+    R.g[wid] = w;
+  }
+  __syncthreads();
+  v = R.f[0];
+  w = R.g[0];
+#pragma unroll
+  for (int q = 1; q < TNW; q++) {
+    v = fmaxf(v, R.f[q]);
+    w = fmaxf(w, R.g[q]);
+  }
 }
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
@@ -79,7 +99,7 @@ __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
 }
 
 template <int EPT, bool BF16>
-__global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_topp(SampleArgs a) {
   __shared__ uint64_t keys[EPT * TBLOCK]; /* by bucket, then by rank */
   __shared__ uint32_t bstart[NBK + 2];    /* bucket counts, then first slots */
   __shared__ uint32_t bfill[NBK + 1];
@@ -119,12 +139,13 @@ __global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
     write_special(a, row, false);
     return;
   }
-  const float m = block_max_f(xm, R);
+  float m = xm, nxl = -xl;
+  block_max2_f(m, nxl, R);
   if (m == -__builtin_inff()) {
     write_special(a, row, true);
     return;
   }
-  const float xmin = -block_max_f(-xl, R);
+  const float xmin = -nxl;
 
   /* ---- 2. e = exp(x - m), the exact row sum and lse */
   float e[EPT];
@@ -182,18 +203,26 @@ __global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
     if (i < V) keys[bstart[bk[j]] + atomicAdd(&bfill[bk[j]], 1u)] = key[j];
   }
   __syncthreads();
+  /* the elements' buckets side by side, one member of each per step */
   int rank[EPT];
+  uint32_t b0[EPT], bn[EPT], most = 0u;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
-    const int i = j * TBLOCK + tid;
-    rank[j] = 0x7fffffff;
-    if (i < V) {
-      const uint32_t s0 = bstart[bk[j]], s1 = bstart[bk[j] + 1];
-      uint32_t r = s0;
-      for (uint32_t s = s0; s < s1; s++) r += keys[s] > key[j] ? 1u : 0u;
-      rank[j] = (int)r;
-    }
+    const bool in = j * TBLOCK + tid < V;
+    b0[j] = in ? bstart[bk[j]] : 0u;
+    bn[j] = in ? bstart[bk[j] + 1] - b0[j] : 0u;
+    rank[j] = in ? (int)b0[j] : 0x7fffffff;
+    most = max(most, bn[j]);
   }
+  for (uint32_t q = 0; q < most; q++) {
+#pragma unroll
+    for (int j = 0; j < EPT; j++)
+      if (q < bn[j]) rank[j] += keys[b0[j] + q] > key[j] ? 1 : 0;
+  }
+  /* this element's uniform, read now: the race needs it last */
+  float uv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) uv[j] = rank[j] < k ? a.u[(size_t)row * k + rank[j]] : 0.0f;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < EPT; j++)
@@ -201,20 +230,26 @@ __global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
   __syncthreads();
 
   /* ---- 4. the cut: exact prefix sums of exp(x_r - lse) over ranks r < k */
-  const int RPT = (k + TBLOCK - 1) / TBLOCK;
+  const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
   const int r0 = tid * RPT;
+  uint64_t term[EPT];
   uint64_t loc = 0;
-  for (int q = 0; q < RPT; q++) {
+#pragma unroll
+  for (int q = 0; q < EPT; q++) {
     const int r = r0 + q;
-    if (r < k) loc += d3s_fix40(d3s_expf(key_x(keys[r]) - lse));
+    term[q] = (q < RPT && r < k) ? d3s_fix40(d3s_expf(key_x(keys[r]) - lse)) : 0ull;
+    loc += term[q];
   }
   uint64_t P = block_excl_scan_u64(loc, R.lo, R.hi);
   int cut_local = k;
-  for (int q = 0; q < RPT; q++) {
-    const int r = r0 + q;
-    if (r < k) {
-      P += d3s_fix40(d3s_expf(key_x(keys[r]) - lse));
-      if (r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > rp.top_p) cut_local = r;
+  /* prefix sums only grow: the cut lies at or before this thread's ranks
+   * only if their last prefix exceeds top_p */
+  if (d3s_fixsum_to_f32(P + loc) > rp.top_p) {
+#pragma unroll
+    for (int q = 0; q < EPT; q++) {
+      const int r = r0 + q;
+      P += term[q];
+      if (q < RPT && r < k && r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > rp.top_p) cut_local = r;
     }
   }
   const int cut = block_min_i32(cut_local, R);
@@ -224,22 +259,47 @@ __global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
 #pragma unroll
   for (int j = 0; j < EPT; j++) ks += rank[j] < cut ? d3s_fix40(e[j]) : 0ull;
   const float inv = 1.0f / d3s_fixsum_to_f32(block_sum_u64(ks, R));
+  /* Proven bounds of each score sc = max(p / noise, -1), noise = -log(1 - u):
+   * RN(1 - u) lies within a relative 2^-24 of 1 - u and d3s_logf within one
+   * ulp, so for u in [2^-24, 1)  u - 2^-24 <= noise <= (u / (1 - u) +
+   * 2^-24) (1 + 2^-23); the margins 2^-18 also cover the bounds' own
+   * rounding.  No score below the largest lower bound can be the first
+   * maximum: only the others take the exact logarithm and division. */
+  float p[EPT], ub[EPT];
+  float lbm = -1.0f;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    p[j] = rank[j] < cut ? e[j] * inv : 0.0f;
+    const float uu = uv[j];
+    float lb = -1.0f, hb = __builtin_inff();
+    if (uu >= 0x1p-24f && uu < 1.0f) {
+      /* v_rcp_f32 is within one ulp: inside the margins */
+      lb = p[j] * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * (1.0f - 0x1p-18f);
+      if (uu > 0x1p-24f) hb = p[j] * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * (1.0f + 0x1p-18f);
+    } else if (uu >= 1.0f) {
+      hb = 0.0f; /* noise +inf (score 0) or NaN (score -1) */
+    }
+    ub[j] = rank[j] < k ? hb : -__builtin_inff();
+    if (rank[j] < k) lbm = fmaxf(lbm, lb);
+  }
+  const float LB = block_max_f(lbm, R);
   float bs = -1.0f;
   int br = 0x7fffffff, bi = 0;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const int r = rank[j];
     if (r < k) {
-      const float p = r < cut ? e[j] * inv : 0.0f;
-      const float noise = -d3s_logf(1.0f - a.u[(size_t)row * k + r]);
-      const float score = p / noise;
-      const float sc = score > -1.0f ? score : -1.0f; /* NaN, -inf, <= -1 never beat -1 */
-      if (sc > bs || (sc == bs && r < br)) {
-        bs = sc;
-        br = r;
-        bi = j * TBLOCK + tid;
+      if (ub[j] >= LB) {
+        const float noise = -d3s_logf(1.0f - uv[j]);
+        const float score = p[j] / noise;
+        const float sc = score > -1.0f ? score : -1.0f; /* NaN, -inf, <= -1 never beat -1 */
+        if (sc > bs || (sc == bs && r < br)) {
+          bs = sc;
+          br = r;
+          bi = j * TBLOCK + tid;
+        }
       }
-      if (a.probs) a.probs[(size_t)row * k + r] = p;
+      if (a.probs) a.probs[(size_t)row * k + r] = p[j];
       if (a.cand) a.cand[(size_t)row * k + r] = j * TBLOCK + tid;
     }
   }
@@ -256,16 +316,15 @@ __global__ __launch_bounds__(TBLOCK) void k_topp(SampleArgs a) {
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    float b = sh_best[0];
-    int r = sh_bestr[0], id = sh_besti[0];
-    for (int w = 1; w < TNW; w++)
-      if (sh_best[w] > b || (sh_best[w] == b && sh_bestr[w] < r)) {
-        b = sh_best[w];
-        r = sh_bestr[w];
-        id = sh_besti[w];
-      }
-    a.ids[row] = id;
+  if (wid == 0) {
+    float ss = lane < TNW ? sh_best[lane] : -2.0f;
+    int rr = lane < TNW ? sh_bestr[lane] : 0x7fffffff;
+    const int ii = lane < TNW ? sh_besti[lane] : 0;
+    const float s_in = ss;
+    const int r_in = rr;
+    wave_argmax(ss, rr);
+    const int id = (int)readlane_u((uint32_t)ii, (int)__builtin_ctzll(__ballot(r_in == rr && s_in == ss)));
+    if (lane == 0) a.ids[row] = id;
   }
 }
 
