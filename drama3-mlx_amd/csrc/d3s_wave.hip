@@ -14,9 +14,9 @@
  *     at least k elements reach it.  tau_lo steps tau down past logits whose
  *     x ties with tau's x, so {logit >= tau_lo} holds every element whose x
  *     reaches the k-th largest x: the top k (src/sampling.c:90-121) lie in it.
- *  3. one pass over the registers: the fast row sum S' = sum 2^(logit*c - h)
- *     (c = log2(e)/T, v_exp_f32) and the candidates {logit >= tau_lo} into
- *     lane-private LDS lists.
+ *  3. passes over the registers: the candidates {logit >= tau_lo} as a bit
+ *     per element, then the fast row sum S' = sum 2^(logit*c - h)
+ *     (c = log2(e)/T, v_exp_f32) while the first candidates are read again.
  *  4. candidates take their exact x, rank by (x desc, index asc) and the top k
  *     run the reference kernel's tail (src/sampling.c:123-139) with
  *     lse' = m + ln S'.  lse only decides the top-p cut (the probabilities use
@@ -26,7 +26,8 @@
  *     d3s_expf(x - m), as the oracle) and redoes the cumulative.
  *  Exact fallbacks: more candidates than a wave holds -> 8-bit radix select
  *  over order-preserving keys of x; T not finite or |m| beyond 2^24 -> every
- *  quantity per element from x exactly (exact_row).
+ *  quantity per element from x exactly (slow_row).
+ * k_wide (below) runs the same passes on rows spread over a workgroup.
  */
 #include "d3s_generic.h"
 

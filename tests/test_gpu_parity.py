@@ -349,6 +349,41 @@ def test_ranked_nucleus_edge_rows(gpu, oracle):
         compare(oracle, gpu, x[3:], u[3:], T, 0.9, label=f"nucleus rows T={T}")
 
 
+def _u64_to_f32(v):
+    """round to nearest even of a non-negative integer, in fp32"""
+    v = int(v)
+    if v < (1 << 24):
+        return np.float32(v)
+    sh = v.bit_length() - 24
+    q, rem = v >> sh, v & ((1 << sh) - 1)
+    half = 1 << (sh - 1)
+    if rem > half or (rem == half and q & 1):
+        q += 1
+    return np.float32(q * 2.0 ** sh)
+
+
+def test_ranked_nucleus_top_p_on_a_prefix(gpu, oracle):
+    """k = V: top_p one ulp either side of a row's own exact prefix sum
+    (fixed point of d3s_expf(x_r - lse) over ranks, rounded once): the cut
+    depends on the last bit of that sum."""
+    w = W.make("C5", rows=16, seed=12, uniforms=False)
+    x, N, V = w["logits"], 16, 4097
+    u = oracle.uniform(12, 0, N, V)
+    top_p = np.empty(N, np.float32)
+    for r in range(N):
+        xr = x[r].copy()
+        if w["banned"][r] >= 0:
+            xr[w["banned"][r]] = -np.inf
+        lse = oracle.sample(x[r:r + 1], u[r:r + 1], 1.0, 2.0, banned=w["banned"][r:r + 1])["lse"][0]
+        order = np.lexsort((np.arange(V), -xr))
+        terms = oracle.fix40(oracle.expf((xr[order] - lse).astype(np.float32)))
+        j = 500 + 211 * r
+        P = int(np.sum(terms[:j + 1].astype(object)))
+        f = np.float32(_u64_to_f32(P) * np.float32(2.0 ** -40))
+        top_p[r] = np.nextafter(f, np.float32(0 if r % 2 else 2))
+    compare(oracle, gpu, x, u, 1.0, top_p, banned=w["banned"], label="nucleus top_p on a prefix")
+
+
 def test_strided_and_unaligned_rows(gpu, oracle):
     rng = np.random.default_rng(13)
     for stride, V in [(4099, 4097), (4097, 4000), (301, 300), (8195, 8190)]:
