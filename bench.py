@@ -14,8 +14,9 @@ the mean launch duration, timed with HIP events on the launching stream
 around the back-to-back launches.  cpu_baseline = the C oracle (the port of the
 reference semantics; the reference's own CPU path needs mlx-c, absent here)
 on a bounded sample of the same workload, all host cores.
-Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), and
-launch times of C2, C4 and C5 at their own shapes (`other_configs`).
+Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), launch
+times of C2, C4 and C5 at their own shapes, and the fused repetition-aware draw
+against its two separate launches (`other_configs`).
 """
 import argparse
 import json
@@ -261,6 +262,56 @@ def other_configs(reps):
     return out
 
 
+def ras_latency(reps):
+    """The main token's repetition-aware draw (src/tower.c:420-433) on the
+    backbone head's shape, bf16 [1, 4097]: one d3s_sample_ras launch (both
+    draws, the row read once from HBM) against the two d3s_sample launches it
+    replaces.  p50 of events around each, over `reps` rows."""
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    w = W.make("C1", rows=64, seed=9, uniforms=False)
+    xb = W.f32_to_bf16_bits(w["logits"])
+    lg = hiprt.to_device(xb)
+    u = hiprt.DeviceBuffer(4 * 64 * K)
+    u2 = hiprt.DeviceBuffer(4 * 64 * K)
+    assert d3s.lib().d3s_uniform_fill(u.ptr, 64 * K, 9, 0, None) == 0
+    assert d3s.lib().d3s_uniform_fill(u2.ptr, 64 * K, 9, 1, None) == 0
+    hist = hiprt.to_device(np.full(16, 151669, np.int32))
+    out = hiprt.DeviceBuffer(16)
+    P = d3s.ras_params(temperature=0.7, top_p=0.7, top_k=K, eos_id=151645, semantic_start=151669,
+                       semantic_end=151669 + 4095, code_vocab=4096)
+    s = hiprt.Stream()
+    a, b = hiprt.Event(), hiprt.Event()
+    fused, two = [], []
+    for i in range(reps + 20):
+        r = i % 64
+        row, ur, u2r = lg.ptr + r * V * 2, u.ptr + r * K * 4, u2.ptr + r * K * 4
+        a.record(s)
+        assert d3s.sample_ras_raw(row, d3s.DTYPE_BF16, 1, V, V, ur, u2r, hist.ptr, 16, P, out.ptr,
+                                  stream=s.ptr) == 0
+        b.record(s)
+        b.synchronize()
+        tf = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        assert d3s.sample_raw(row, d3s.DTYPE_BF16, 1, V, V, ur, K, 0.7, 0.7, None, out.ptr, stream=s.ptr) == 0
+        assert d3s.sample_raw(row, d3s.DTYPE_BF16, 1, V, V, u2r, K, 1.0, 0.95, None, out.ptr + 4,
+                              stream=s.ptr) == 0
+        b.record(s)
+        b.synchronize()
+        if i >= 20:
+            fused.append(tf)
+            two.append(a.elapsed_ms(b) * 1e3)
+    s.destroy()
+    res = {"shape": [1, V], "dtype": "bf16", "k": K, "retry": [1.0, 0.95, 30],
+           "fused_p50_us": float(np.median(fused)), "two_launches_p50_us": float(np.median(two)),
+           "hbm_bytes_fused": V * 2 + 2 * K * 4 + 16 * 4 + 8,
+           "hbm_bytes_two_launches": 2 * (V * 2 + K * 4 + 4)}
+    log(f"RAS main token, bf16 [1, {V}]: one fused launch p50 {res['fused_p50_us']:.2f} us, "
+        f"two launches p50 {res['two_launches_p50_us']:.2f} us")
+    return res
+
+
 def cpu_baseline(seconds):
     """The oracle on all host cores over a bounded sample of C3 rows."""
     import d3s_oracle
@@ -347,6 +398,7 @@ def main():
     others = None
     if not args.no_other:
         others = other_configs(200)
+        others["RAS"] = ras_latency(500)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_k_wave_C3.json")
     if os.path.exists(tpath):

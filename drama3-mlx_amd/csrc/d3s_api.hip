@@ -72,6 +72,55 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   return launched();
 }
 
+int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                   const float *u, const float *u_retry, const int32_t *history, int history_len,
+                   const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
+                   int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *stream) {
+  if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;
+  if (!params || n_rows < 0 || n_rows > 0x7fffffff || vocab < 1 || vocab > (1 << 26) ||
+      row_stride < vocab || params->top_k < 1 || params->retry_top_k < 1 || history_len < 0 ||
+      history_len > 64 || (history_len > 0 && !history) || params->code_vocab < 1)
+    return D3S_ERR_ARG;
+  if (n_rows == 0) return D3S_OK;
+  if (!logits || !u || !u_retry || !main_tok) return D3S_ERR_ARG;
+  if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
+  d3s::RasArgs r;
+  d3s::SampleArgs &a = r.first;
+  a.logits = logits;
+  a.row_stride = row_stride;
+  a.vocab = (int)vocab;
+  a.k = params->top_k < vocab ? params->top_k : (int)vocab; /* src/sampling.c:186,207 */
+  a.n_rows = (int)n_rows;
+  a.u = u;
+  a.temperature = nullptr;
+  a.top_p = nullptr;
+  a.temperature_scalar = params->temperature;
+  a.top_p_scalar = params->top_p;
+  a.banned = nullptr;
+  a.ids = first_idx;
+  a.probs = nullptr;
+  a.cand = nullptr;
+  a.counters = counters;
+  a.flags = 0u;
+  r.retry = a;
+  r.retry.k = params->retry_top_k < vocab ? params->retry_top_k : (int)vocab;
+  r.retry.u = u_retry;
+  r.retry.temperature_scalar = params->retry_temperature;
+  r.retry.top_p_scalar = params->retry_top_p;
+  r.retry.ids = retry_idx;
+  r.history = history;
+  r.history_len = history_len;
+  r.eos_id = params->eos_id;
+  r.semantic_start = params->semantic_start;
+  r.semantic_end = params->semantic_end;
+  r.code_vocab = params->code_vocab;
+  r.main_tok = main_tok;
+  r.code0 = code0;
+  const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
+  if (!d3s::launch_ras(r, dt, (hipStream_t)stream)) return D3S_ERR_UNSUPPORTED;
+  return launched();
+}
+
 int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream) {
   if (n < 0 || (n > 0 && !u)) return D3S_ERR_ARG;
   d3s::launch_uniform(u, n, seed, draw, (hipStream_t)stream);

@@ -29,6 +29,19 @@ struct SampleArgs {
   unsigned flags;
 };
 
+/* Repetition-aware sampling of the main token (src/tower.c:13-16,:405-433):
+ * two draws from each row, one with the caller's parameters and a retry; the
+ * retry's id replaces the first's when the first's token is a semantic token
+ * among the row's recent main tokens. */
+struct RasArgs {
+  SampleArgs first, retry;  /* the same logits and rows; their own u, k, T, top_p, ids */
+  const int32_t *history;   /* [n_rows, history_len] recent main tokens, or null */
+  int history_len;          /* 0 .. 64 */
+  int32_t eos_id, semantic_start, semantic_end, code_vocab;
+  int32_t *main_tok;        /* [n_rows] */
+  int32_t *code0;           /* [n_rows] or null: clip(main - semantic_start, 0, code_vocab - 1) */
+};
+
 /* counters[] slots (atomic increments per row) */
 enum {
   CNT_REFUSED = 0,      /* non-finite x: id -1 */
@@ -51,6 +64,9 @@ enum Dtype { DT_F32 = 0, DT_BF16 = 1 };
  * Returns false if no instantiation fits. */
 bool launch_wave(const SampleArgs &a, Dtype dt, hipStream_t s);
 int wave_max_vocab(Dtype dt);
+/* Launch the fused RAS kernel (both draws k <= 64, V within the wave kernel's
+ * reach).  Returns false if no instantiation fits. */
+bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
 /* Launch the wide kernel: one 1024-thread workgroup per row, the row in the

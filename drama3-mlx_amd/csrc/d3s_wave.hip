@@ -121,8 +121,8 @@ __device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float 
 /* The exclusive top-p cut over c_r, the probabilities and the race
  * (src/sampling.c:128-139); lane r < k holds rank r's index, c_r, ep_r =
  * exp(x_r - x_0), the prefix s_r of ep and noise -log(1 - u_r). */
-__device__ __forceinline__ void wave_race_prefix(const SampleArgs &a, int row, int idx, float c, float ep,
-                                                 float s, float noise, float top_p) {
+__device__ __forceinline__ int wave_race_prefix(const SampleArgs &a, int row, int idx, float c, float ep,
+                                                float s, float noise, float top_p) {
   const int lane = lane_id();
   const int k = a.k;
   const bool act = lane < k;
@@ -138,24 +138,27 @@ __device__ __forceinline__ void wave_race_prefix(const SampleArgs &a, int row, i
   int best = lane;
   wave_argmax(sc, best);
   const int id = (int)readlane_u((uint32_t)idx, best);
-  if (lane == 0) a.ids[row] = id;
+  if (lane == 0 && a.ids) a.ids[row] = id;
   if (act) {
     if (a.probs) a.probs[(size_t)row * k + lane] = p;
     if (a.cand) a.cand[(size_t)row * k + lane] = idx;
   }
+  return id;
 }
 
-/* A refused row (id -1) or an all -inf row (id 0, ranks 0..k-1); one wave. */
-__device__ __forceinline__ void wave_write_special(const SampleArgs &a, int row, bool masked) {
+/* A refused row (id -1) or an all -inf row (id 0, ranks 0..k-1); one wave.
+ * Returns the id. */
+__device__ __forceinline__ int wave_write_special(const SampleArgs &a, int row, bool masked) {
   const int lane = lane_id(), k = a.k;
   if (lane == 0) {
-    a.ids[row] = masked ? 0 : -1;
+    if (a.ids) a.ids[row] = masked ? 0 : -1;
     if (a.counters) atomicAdd(&a.counters[masked ? CNT_ALL_MASKED : CNT_REFUSED], 1u);
   }
   if (lane < k) {
     if (a.probs) a.probs[(size_t)row * k + lane] = __builtin_nanf("");
     if (a.cand) a.cand[(size_t)row * k + lane] = masked ? lane : -1;
   }
+  return masked ? 0 : -1;
 }
 
 /* A row in registers: CPT 16-byte chunks per lane (chunk j * 64 + lane, from
@@ -386,7 +389,7 @@ struct WaveRow {
 
   const SampleArgs a;
   WaveLds &S;
-  int row, V, k, lane, pos0, nchunks, banned;
+  int row, V, k, lane, pos0, off, nchunks, banned;
   const uint4 *src;
   const char *rowp;
   float T, y, uval, top_p;
@@ -402,7 +405,8 @@ struct WaveRow {
     return RowRef{a.counters, &S, src, nchunks, pos0, V, k, lane, banned, T, y, t_finite};
   }
 
-  __device__ __forceinline__ void load() {
+  /* the row's parameters and where its chunks lie */
+  __device__ __forceinline__ void setup() {
     const RowP rp = row_params(a, row);
     T = rp.T;
     top_p = rp.top_p;
@@ -413,10 +417,14 @@ struct WaveRow {
     /* a chunk never crosses a page, so the bytes outside the row it covers
      * are readable; they become -inf below */
     rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
-    const int off = (int)(((uintptr_t)rowp & 15u) / ES);
+    off = (int)(((uintptr_t)rowp & 15u) / ES);
     src = (const uint4 *)(rowp - off * ES);
     nchunks = (off + V + EPC - 1) / EPC;
     pos0 = lane * EPC - off;
+  }
+
+  __device__ __forceinline__ void load() {
+    setup();
     c.load(src, nchunks, lane);
     /* the partial chunk at the row start and every chunk row from the one
      * holding the row end on */
@@ -445,7 +453,7 @@ struct WaveRow {
    * 2^-24), eps_e bounding the relative change of a term exp(v - lse) between
    * the two lse values; the exact row sum is computed when a cut could fall
    * differently. */
-  __device__ __forceinline__ void finish(int n, float M, float lse, bool exact, float eps_s, float noise) {
+  __device__ __forceinline__ int finish(int n, float M, float lse, bool exact, float eps_s, float noise) {
     if (lane == 0) S.keys[n] = 0ull; /* pad for the pair reads; below every key */
     wave_lds_sync();
     const uint64_t my = lane < n ? S.keys[lane] : 0ull;
@@ -478,24 +486,21 @@ struct WaveRow {
         cc = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
       }
     }
-    wave_race_prefix(a, row, idx, cc, ep, sp, noise, top_p);
+    return wave_race_prefix(a, row, idx, cc, ep, sp, noise, top_p);
   }
 
   /* every quantity per element from x = L / T, as the oracle (T not finite,
    * or logits too large for the fast row sum) */
-  __device__ __forceinline__ void slow_row() {
+  __device__ __forceinline__ int slow_row() {
     const RowRef R = ref();
     const float M = slow_max<CPT, BF16>(R);
-    if (d3s_isnan(M) || M == -__builtin_inff()) {
-      wave_write_special(a, row, !d3s_isnan(M));
-      return;
-    }
+    if (d3s_isnan(M) || M == -__builtin_inff()) return wave_write_special(a, row, !d3s_isnan(M));
     const int n = exact_select<CPT, BF16>(R);
-    finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, -d3s_logf(1.0f - uval));
+    return finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, -d3s_logf(1.0f - uval));
   }
 
-  __device__ __forceinline__ void run() {
-    load();
+  /* the row, once loaded (and masked), to its id */
+  __device__ __forceinline__ int compute() {
     const float ninf = -__builtin_inff();
     const float noise = -d3s_logf(1.0f - uval); /* the race's noise needs only u */
     bool slow = !t_finite;
@@ -505,25 +510,16 @@ struct WaveRow {
 #pragma unroll
       for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
       const float Lmax = wave_maximum_f(lm);
-      if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
-        wave_write_special(a, row, false);
-        return;
-      }
+      if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) return wave_write_special(a, row, false);
       M = scale_logit(Lmax, T, y, true); /* = max x */
-      if (M == __builtin_inff() || M == ninf) {
-        wave_write_special(a, row, M == ninf);
-        return;
-      }
+      if (M == __builtin_inff() || M == ninf) return wave_write_special(a, row, M == ninf);
       cf = LOG2E_F / T;
       const float h = Lmax * cf;
       slow = !(fabsf(h) < 0x1p24f);
       b = -h;
       delta = __builtin_fmaf(Lmax, cf, b); /* Lmax * cf + b exactly */
     }
-    if (slow) {
-      slow_row();
-      return;
-    }
+    if (slow) return slow_row();
 
     /* ---- tau: the k-th largest lane max, to 20 bits of its order key (a
      * lower bound: at least k elements reach it), by ballot radix search */
@@ -635,7 +631,12 @@ struct WaveRow {
       }
       n = (int)tot;
     }
-    finish(n, M, lse, false, eps_s, noise);
+    return finish(n, M, lse, false, eps_s, noise);
+  }
+
+  __device__ __forceinline__ void run() {
+    load();
+    (void)compute();
   }
 };
 
@@ -934,6 +935,46 @@ constexpr int wave_occupancy() {
   return BF16 ? (CPT <= 8 ? 5 : 4) : (CPT <= 17 ? 5 : 3);
 }
 
+/* k_ras: the main token's two draws (src/tower.c:425-433) in one launch.  Two
+ * waves of a workgroup take one row: the first samples it with the caller's
+ * parameters, the second with the retry's, side by side (the second's loads
+ * of the row meet the first's in L2, so HBM reads it once).  Then the first
+ * wave picks: candidate index i -> token (0 -> eos, i -> semantic_start + i -
+ * 1, src/tower.c:405-409); the retry's token replaces the first's when the
+ * first is a semantic token found among the row's history (:429-432). */
+template <int CPT, bool BF16>
+__global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
+void k_ras(RasArgs ra) {
+  __shared__ WaveLds lds_all[WR];
+  __shared__ int drawn[WR];
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int row = (int)(blockIdx.x * (blockDim.x / WAVE / 2)) + wid / 2;
+  const bool retry = (wid & 1) != 0;
+  const int lane = lane_id();
+  if (row < ra.first.n_rows) {
+    const SampleArgs &a = retry ? ra.retry : ra.first;
+    WaveRow<CPT, BF16> r(a, lds_all[wid], row);
+    r.V = a.vocab;
+    r.k = a.k;
+    r.lane = lane;
+    r.load();
+    const int id = r.compute();
+    if (lane == 0) drawn[wid] = id;
+  }
+  __syncthreads();
+  if (retry || row >= ra.first.n_rows) return;
+  const int id1 = drawn[wid], id2 = drawn[wid + 1];
+  const int32_t first_tok = id1 == 0 ? ra.eos_id : id1 + ra.semantic_start - 1;
+  const int32_t retry_tok = id2 == 0 ? ra.eos_id : id2 + ra.semantic_start - 1;
+  const bool seen = lane < ra.history_len && ra.history[(size_t)row * ra.history_len + lane] == first_tok;
+  const bool repeated = __ballot(seen) != 0ull && first_tok >= ra.semantic_start && first_tok <= ra.semantic_end;
+  const int32_t tok = repeated ? retry_tok : first_tok;
+  if (lane == 0) {
+    ra.main_tok[row] = tok;
+    if (ra.code0) ra.code0[row] = min(max(tok - ra.semantic_start, 0), ra.code_vocab - 1);
+  }
+}
+
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
 void k_wave(SampleArgs a) {
@@ -991,6 +1032,29 @@ void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s)
   if (n <= 0) return;
   const int B = 256;
   hipLaunchKernelGGL(k_exp2, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, in, out, n);
+}
+
+template <int CPT, bool BF16>
+bool try_ras(const RasArgs &r, int max_off, hipStream_t s) {
+  if (r.first.vocab > wave_vmax<CPT, BF16>(max_off)) return false;
+  /* two waves per row: one row per workgroup for small launches, two otherwise */
+  const int n = r.first.n_rows;
+  const int rpw = n <= WR_SPREAD_ROWS ? 1 : WR / 2;
+  hipLaunchKernelGGL((k_ras<CPT, BF16>), dim3((unsigned)((n + rpw - 1) / rpw)), dim3(WAVE * 2 * rpw), 0, s, r);
+  return true;
+}
+
+bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s) {
+  if (r.first.k > KF || r.retry.k > KF) return false;
+  const SampleArgs &a = r.first;
+  const int es = dt == DT_F32 ? 4 : 2;
+  const bool aligned = ((uintptr_t)a.logits % 16u) == 0u && (a.row_stride * es) % 16 == 0;
+  const int max_off = aligned ? 0 : 16 / es - 1;
+  if (dt == DT_F32)
+    return try_ras<4, false>(r, max_off, s) || try_ras<8, false>(r, max_off, s) ||
+           try_ras<17, false>(r, max_off, s) || try_ras<24, false>(r, max_off, s);
+  return try_ras<4, true>(r, max_off, s) || try_ras<8, true>(r, max_off, s) ||
+         try_ras<10, true>(r, max_off, s) || try_ras<16, true>(r, max_off, s);
 }
 
 int wide_max_vocab(Dtype dt) { return dt == DT_F32 ? wide_vmax<19, false>() : wide_vmax<19, true>(); }

@@ -24,6 +24,23 @@ OK = 0
 _lib = None
 
 
+class RasParams(ctypes.Structure):
+    """d3s_ras_params (include/d3s_sampler.h)"""
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_int),
+                ("retry_temperature", ctypes.c_float), ("retry_top_p", ctypes.c_float),
+                ("retry_top_k", ctypes.c_int), ("eos_id", ctypes.c_int32),
+                ("semantic_start", ctypes.c_int32), ("semantic_end", ctypes.c_int32),
+                ("code_vocab", ctypes.c_int32)]
+
+
+def ras_params(**kw):
+    """RasParams from keyword fields; the retry defaults to the reference's
+    RAS_TEMPERATURE / RAS_TOP_P / RAS_TOP_K (src/tower.c:13-16)."""
+    d = dict(retry_temperature=1.0, retry_top_p=0.95, retry_top_k=30)
+    d.update(kw)
+    return RasParams(**d)
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -36,6 +53,9 @@ def lib():
         L.d3s_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
                                  vp, u32, vp]
         L.d3s_sample.restype = i32
+        L.d3s_sample_ras.argtypes = [vp, i32, i64, i64, i64, vp, vp, vp, i32,
+                                     ctypes.POINTER(RasParams), vp, vp, vp, vp, vp, vp]
+        L.d3s_sample_ras.restype = i32
         L.d3s_uniform_fill.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
         L.d3s_uniform_fill.restype = i32
         L.d3s_max_k.argtypes = []
@@ -171,4 +191,48 @@ def d3_sample_with_noise(logits, u, temperature, top_p):
     out = np.zeros(len(logits), np.int32)
     lib().d3_sample_with_noise(logits.ctypes.data, u.ctypes.data, logits.shape[0], logits.shape[1],
                                u.shape[1], temperature, top_p, out.ctypes.data)
+    return out
+
+
+def sample_ras_raw(logits, dtype, n_rows, vocab, row_stride, u, u_retry, history, history_len,
+                   params, main_tok, code0=None, first_idx=None, retry_idx=None, counters=None,
+                   stream=None):
+    """d3s_sample_ras on device pointers (ints); params: RasParams."""
+    return lib().d3s_sample_ras(logits, dtype, n_rows, vocab, row_stride, u, u_retry, history,
+                                history_len, ctypes.byref(params) if params is not None else None,
+                                main_tok, code0, first_idx, retry_idx, counters, stream)
+
+
+def sample_ras(logits, u, u_retry, params, history=None):
+    """Host arrays in and out: logits float32 or uint16 (bf16 bits) [N, V];
+    u [N, k], u_retry [N, k2]; history int32 [N, H] or None; params: dict of
+    d3s_ras_params' fields.  Returns dict(rc, main, code0, first, retry, counters)."""
+    import hiprt
+    logits = np.ascontiguousarray(logits)
+    dtype = DTYPE_F32 if logits.dtype == np.float32 else DTYPE_BF16
+    N, V = logits.shape
+    P = ras_params(**params)
+    bufs = dict(logits=hiprt.to_device(logits), u=hiprt.to_device(np.ascontiguousarray(u, np.float32)),
+                u2=hiprt.to_device(np.ascontiguousarray(u_retry, np.float32)),
+                main=hiprt.DeviceBuffer(4 * N), code0=hiprt.DeviceBuffer(4 * N),
+                first=hiprt.DeviceBuffer(4 * N), retry=hiprt.DeviceBuffer(4 * N),
+                counters=hiprt.DeviceBuffer(4 * NUM_COUNTERS).zero())
+    H = 0
+    hist = None
+    if history is not None and np.size(history):
+        history = np.ascontiguousarray(history, np.int32).reshape(N, -1)
+        H = history.shape[1]
+        bufs["hist"] = hiprt.to_device(history)
+        hist = bufs["hist"].ptr
+    rc = sample_ras_raw(bufs["logits"].ptr, dtype, N, V, V, bufs["u"].ptr, bufs["u2"].ptr, hist, H, P,
+                        bufs["main"].ptr, bufs["code0"].ptr, bufs["first"].ptr, bufs["retry"].ptr,
+                        bufs["counters"].ptr)
+    out = dict(rc=rc)
+    if rc == OK:
+        hiprt.synchronize()
+        for name in ("main", "code0", "first", "retry"):
+            out[name] = bufs[name].download((N,), np.int32)
+        out["counters"] = bufs["counters"].download((NUM_COUNTERS,), np.uint32)
+    for b in bufs.values():
+        b.free()
     return out

@@ -68,6 +68,40 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
                int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
                void *stream);
 
+/* Parameters of d3s_sample_ras: the first draw (SamplingParams, src/model.h:146-149),
+ * the retry (RAS_TEMPERATURE / RAS_TOP_K / RAS_TOP_P, src/tower.c:13-16: 1.0, 30,
+ * 0.95) and the candidate-to-token map of the backbone head (src/tower.c:405-409,
+ * :429-432: eos_id, semantic_start, semantic_end, code_vocab of the Config). */
+typedef struct {
+  float temperature, top_p;
+  int top_k;
+  float retry_temperature, retry_top_p;
+  int retry_top_k;
+  int32_t eos_id, semantic_start, semantic_end, code_vocab;
+} d3s_ras_params;
+
+/* Repetition-aware sampling of the main token, both draws in one launch that
+ * reads each row of logits once from HBM.  Per row (src/tower.c:425-433):
+ *   first = the sampled index with (temperature, top_p, top_k) and u [n_rows, k],
+ *   retry = the sampled index with the retry's parameters and u_retry [n_rows, k2]
+ *   (k = min(top_k, vocab), k2 = min(retry_top_k, vocab), as d3s_sample);
+ *   token(i) = i == 0 ? eos_id : semantic_start + i - 1;
+ *   main_tok = token(retry) if token(first) is in [semantic_start, semantic_end]
+ *              and equals one of the row's history [n_rows, history_len] (the last
+ *              RAS_WINDOW_FRAMES = 16 main tokens, src/generate.h:11,
+ *              src/generate.c:83-91), else token(first);
+ *   code0 = clip(main_tok - semantic_start, 0, code_vocab - 1).
+ * history may be NULL with history_len 0; history_len <= 64.  code0, first_idx,
+ * retry_idx (the two draws' indices) are optional.  counters count both draws.
+ * Rows the one-wave kernel does not hold (k or k2 above 64, or a vocab beyond
+ * its registers) return D3S_ERR_UNSUPPORTED.
+ * Replaces: the two sample_with_noise calls, candidate_token and the repeat test of
+ * tower_decode_step (src/tower.c:420-433). */
+int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                   const float *u, const float *u_retry, const int32_t *history, int history_len,
+                   const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
+                   int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *stream);
+
 /* u[i] = the i-th uniform of draw `draw` under `seed` (Philox4x32-10, counter
  * (i/4, draw), key seed, 24-bit values in [0, 1)), for i < n.
  * Replaces: m_uniform (src/mlxu.c:771-774) as used by sample_top_k_top_p

@@ -247,6 +247,24 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
   return failed ? -1 : 0;
 }
 
+void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n_rows,
+                           const int32_t *history, int history_len, int32_t eos_id,
+                           int32_t semantic_start, int32_t semantic_end, int32_t code_vocab,
+                           int32_t *main_tok, int32_t *code0) {
+  for (int64_t r = 0; r < n_rows; r++) {
+    const int32_t t1 = first[r] == 0 ? eos_id : first[r] + semantic_start - 1;
+    const int32_t t2 = retry[r] == 0 ? eos_id : retry[r] + semantic_start - 1;
+    int seen = 0;
+    for (int h = 0; h < history_len; h++) seen |= history[r * history_len + h] == t1;
+    const int32_t t = (seen && t1 >= semantic_start && t1 <= semantic_end) ? t2 : t1;
+    main_tok[r] = t;
+    if (code0) {
+      int32_t c = t - semantic_start;
+      code0[r] = c < 0 ? 0 : c > code_vocab - 1 ? code_vocab - 1 : c;
+    }
+  }
+}
+
 void d3s_oracle_expf(const float *in, float *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_expf(in[i]);
 }

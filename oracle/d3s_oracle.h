@@ -63,6 +63,18 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
                       float *lse, uint8_t *flags, double *gaps, int n_threads);
 
 /* elementwise d3s_expf / d3s_logf / true division, for the math tests */
+/* Repetition-aware selection of the main token (src/tower.c:405-409,:425-433),
+ * given the two draws' sampled indices per row (first: the caller's
+ * parameters, retry: RAS_TEMPERATURE / RAS_TOP_K / RAS_TOP_P, :13-16):
+ *   token(i) = i == 0 ? eos_id : semantic_start + i - 1            (:405-409)
+ *   main = token(retry) if semantic_start <= token(first) <= semantic_end
+ *          and token(first) is one of the row's history_len recent main
+ *          tokens (:429-431), else token(first)                     (:432)
+ *   code0 = clip(main - semantic_start, 0, code_vocab - 1)          (:433-434) */
+void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n_rows,
+                           const int32_t *history, int history_len, int32_t eos_id,
+                           int32_t semantic_start, int32_t semantic_end, int32_t code_vocab,
+                           int32_t *main_tok, int32_t *code0);
 void d3s_oracle_expf(const float *in, float *out, int64_t n);
 void d3s_oracle_logf(const float *in, float *out, int64_t n);
 void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n);

@@ -46,6 +46,8 @@ def lib():
         L.d3s_oracle_u64_to_f32.restype = f32
         L.d3s_oracle_philox.argtypes = [vp, vp, vp]
         L.d3s_oracle_philox.restype = None
+        L.d3s_oracle_ras_select.argtypes = [vp, vp, i64, vp, i32, i32, i32, i32, i32, vp, vp]
+        L.d3s_oracle_ras_select.restype = None
         L.d3s_oracle_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, i64, i64, vp]
         L.d3s_oracle_uniform.restype = None
         _lib = L
@@ -144,3 +146,31 @@ def uniform(seed, stream0, rows, k):
     u = np.empty((rows, k), np.float32)
     lib().d3s_oracle_uniform(seed, stream0, rows, k, _p(u))
     return u
+
+
+def ras_select(first, retry, history, eos_id, semantic_start, semantic_end, code_vocab):
+    """The RAS selection (src/tower.c:405-409,:425-433) over the two draws'
+    indices [N]; history int32 [N, H] (H may be 0).  Returns (main_tok, code0)."""
+    first = np.ascontiguousarray(first, np.int32)
+    retry = np.ascontiguousarray(retry, np.int32)
+    N = first.shape[0]
+    history = np.ascontiguousarray(history, np.int32).reshape(N, -1)
+    main, code0 = np.empty(N, np.int32), np.empty(N, np.int32)
+    lib().d3s_oracle_ras_select(_p(first), _p(retry), N, _p(history) if history.size else None,
+                                history.shape[1], eos_id, semantic_start, semantic_end, code_vocab,
+                                _p(main), _p(code0))
+    return main, code0
+
+
+def ras(logits, u, u_retry, params, history, n_threads=1):
+    """Both RAS draws of every row and the selection: the oracle of
+    d3s_sample_ras.  params: dict of d3s_ras_params' fields (the retry's
+    default to RAS_TEMPERATURE / RAS_TOP_P / RAS_TOP_K); the draws' k are
+    u's and u_retry's widths."""
+    p = dict(retry_temperature=1.0, retry_top_p=0.95, retry_top_k=30)  # src/tower.c:13-16
+    p.update(params)
+    first = sample(logits, u, p["temperature"], p["top_p"], n_threads=n_threads)["ids"]
+    retry = sample(logits, u_retry, p["retry_temperature"], p["retry_top_p"], n_threads=n_threads)["ids"]
+    main, code0 = ras_select(first, retry, history, p["eos_id"], p["semantic_start"],
+                             p["semantic_end"], p["code_vocab"])
+    return dict(first=first, retry=retry, main=main, code0=code0)

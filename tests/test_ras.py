@@ -1,0 +1,134 @@
+"""Repetition-aware sampling of the main token (src/tower.c:13-16,:405-433):
+the oracle's selection against known answers, the C-ABI's argument checks, and
+(on the GPU) the fused two-draw kernel against the oracle's two draws.
+
+The token map's ids are illustrative (the model's config files are not in the
+reference's sources); the band has the backbone head's shape: candidate index
+0 is eos and 1..4096 are the semantic codes (lm_head_audio [1 + code_vocab,
+hidden], src/model.h:71)."""
+import numpy as np
+import pytest
+
+import d3s_workloads as W
+
+EOS, START, CODES = 151645, 151669, 4096
+END = START + CODES - 1
+MAP = dict(eos_id=EOS, semantic_start=START, semantic_end=END, code_vocab=CODES)
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import d3s
+    import hiprt
+    d3s.lib()
+    if hiprt.device_count() < 1:
+        pytest.skip("no GPU")
+    return d3s
+
+
+def test_selection_known_answers(oracle):
+    """Each case follows from src/tower.c:405-409 and :425-433 by hand."""
+    first = np.array([0, 5, 5, 5, -1, 4096, 1, 3], np.int32)
+    retry = np.array([7, 9, 9, 0, 3, 2, 2, 8], np.int32)
+    hist = np.full((8, 3), -7, np.int32)
+    hist[0] = EOS                   # eos repeated: a stop is never redrawn
+    hist[1, 2] = START + 4          # token(5) seen: the retry's token
+    hist[3, 0] = START + 4          # seen, and the retry is eos
+    hist[4, :] = START - 2          # token(-1) = START - 2 is not semantic
+    hist[5, 1] = END                # the last code, seen
+    hist[6, 0] = START              # the first code, seen
+    main, code0 = oracle.ras_select(first, retry, hist, EOS, START, END, CODES)
+    assert main.tolist() == [EOS, START + 8, START + 4, EOS, START - 2, START + 1, START + 1, START + 2]
+    assert code0.tolist() == [0, 8, 4, 0, 0, 1, 1, 2]  # eos lies below the band: clipped to 0
+    # no history: the first draw always stands
+    main0, _ = oracle.ras_select(first, retry, np.zeros((8, 0), np.int32), EOS, START, END, CODES)
+    assert np.array_equal(main0, np.where(first == 0, EOS, first + START - 1))
+
+
+def test_ras_argument_validation_without_device():
+    import d3s
+    p = 16  # never dereferenced: every call below fails validation or launches nothing
+    P = d3s.ras_params(temperature=0.7, top_p=0.7, top_k=30, **MAP)
+    base = dict(logits=p, dtype=1, n_rows=1, vocab=4097, row_stride=4097, u=p, u_retry=p,
+                history=None, history_len=0, params=P, main_tok=p)
+    assert d3s.sample_ras_raw(**{**base, "params": None}) == -1
+    assert d3s.sample_ras_raw(**{**base, "dtype": 3}) == -4
+    assert d3s.sample_ras_raw(**{**base, "history_len": 65, "history": p}) == -1
+    assert d3s.sample_ras_raw(**{**base, "history_len": 4}) == -1  # history missing
+    assert d3s.sample_ras_raw(**{**base, "main_tok": None}) == -1
+    assert d3s.sample_ras_raw(**{**base, "row_stride": 4096}) == -1
+    bad_k = d3s.ras_params(temperature=0.7, top_p=0.7, top_k=0, **MAP)
+    assert d3s.sample_ras_raw(**{**base, "params": bad_k}) == -1
+    assert d3s.sample_ras_raw(**{**base, "n_rows": 0}) == 0
+
+
+def _case(oracle, name, rows, seed, top_k=30, temperature=0.7, top_p=0.7, H=16, repeat_every=2):
+    """Rows of config `name`, both draws' uniforms, and a history that holds
+    the first draw's token on every `repeat_every`-th row."""
+    w = W.make(name, rows=rows, seed=seed, uniforms=False)
+    x = w["logits"]
+    V = x.shape[1]
+    k, k2 = min(top_k, V), min(30, V)
+    u = oracle.uniform(seed, 0, rows, k)
+    u2 = oracle.uniform(seed, 1, rows, k2)
+    first = oracle.sample(x, u, temperature, top_p, n_threads=8)["ids"]
+    tok = np.where(first == 0, EOS, first + START - 1)
+    rng = np.random.default_rng(seed)
+    hist = rng.integers(START, END + 1, (rows, H)).astype(np.int32)
+    rep = np.arange(rows) % repeat_every == 0
+    if H:
+        hist[rep, rng.integers(0, H, rep.sum())] = tok[rep]
+    params = dict(temperature=temperature, top_p=top_p, top_k=top_k, **MAP)
+    return x, u, u2, hist, params
+
+
+def _check(oracle, gpu, x, u, u2, hist, params):
+    exp = oracle.ras(x, u, u2, params, hist, n_threads=8)
+    got = gpu.sample_ras(x, u, u2, params, hist)
+    assert got["rc"] == 0, got["rc"]
+    for name in ("first", "retry", "main", "code0"):
+        bad = np.nonzero(got[name] != exp[name])[0]
+        assert len(bad) == 0, (name, bad[:8], got[name][bad[:8]], exp[name][bad[:8]])
+    return got, exp
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,rows", [("C1", 1), ("C1", 300), ("C1", 2000), ("C2", 9), ("C3", 256)])
+def test_ras_fused_equals_two_draws(gpu, oracle, name, rows):
+    x, u, u2, hist, params = _case(oracle, name, rows, seed=21 + rows)
+    got, exp = _check(oracle, gpu, x, u, u2, hist, params)
+    # the case exercises both outcomes
+    if rows >= 256:
+        assert np.any(exp["main"] != np.where(exp["first"] == 0, EOS, exp["first"] + START - 1))
+        assert np.any(exp["main"] == np.where(exp["first"] == 0, EOS, exp["first"] + START - 1))
+
+
+@pytest.mark.gpu
+def test_ras_bf16_head_and_parameters(gpu, oracle):
+    """The tower's backbone head: bf16 [1, 4097] rows (src/tower.c:420-433), with
+    several first-draw parameters, no history and the longest history."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((64, 4097)) * 2.5).astype(np.float32)
+    x[np.arange(64), rng.integers(0, 4097, 64)] += 6.0
+    xb = W.f32_to_bf16_bits(x)
+    for top_k, T, top_p, H in [(30, 0.7, 0.7, 16), (5, 1.3, 0.9, 0), (64, 0.3, 1.0, 64), (1, 0.7, 0.7, 16)]:
+        k = top_k
+        u = oracle.uniform(7, 0, 64, k)
+        u2 = oracle.uniform(7, 1, 64, 30)
+        first = oracle.sample(xb, u, T, top_p)["ids"]
+        hist = np.full((64, H), START, np.int32)
+        if H:
+            hist[::2, -1] = np.where(first[::2] == 0, EOS, first[::2] + START - 1)
+        _check(oracle, gpu, xb, u, u2, hist, dict(temperature=T, top_p=top_p, top_k=top_k, **MAP))
+
+
+@pytest.mark.gpu
+def test_ras_rows_beyond_the_wave_kernel(gpu, oracle):
+    """k above 64 or a row wider than one wave's registers: unsupported, nothing launched."""
+    x = np.zeros((2, 4097), np.float32)
+    u = np.full((2, 100), 0.5, np.float32)
+    got = gpu.sample_ras(x, u, u[:, :30], dict(temperature=1.0, top_p=0.9, top_k=100, **MAP))
+    assert got["rc"] == -2
+    wide = np.zeros((1, 20000), np.float32)
+    got = gpu.sample_ras(wide, u[:1, :30], u[:1, :30], dict(temperature=1.0, top_p=0.9, top_k=30, **MAP))
+    assert got["rc"] == -2
