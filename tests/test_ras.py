@@ -132,3 +132,36 @@ def test_ras_rows_beyond_the_wave_kernel(gpu, oracle):
     wide = np.zeros((1, 20000), np.float32)
     got = gpu.sample_ras(wide, u[:1, :30], u[:1, :30], dict(temperature=1.0, top_p=0.9, top_k=30, **MAP))
     assert got["rc"] == -2
+
+
+@pytest.mark.gpu
+def test_frame_assembled_in_place(gpu, oracle):
+    """A decode step's frame [main, code0, code_1 .. code_9] (src/tower.c:420-451)
+    written in place on the device: d3s_sample_ras into frame[0..1], then each
+    codebook head's d3s_sample into frame[2 + j]."""
+    import hiprt
+    rng = np.random.default_rng(17)
+    head = W.f32_to_bf16_bits((rng.standard_normal((1, 4097)) * 2.5).astype(np.float32))
+    books = [W.make("C2", rows=9, seed=17, uniforms=False)["logits"][j:j + 1] for j in range(9)]
+    u0, u1 = oracle.uniform(17, 0, 1, 30), oracle.uniform(17, 1, 1, 30)
+    uj = [oracle.uniform(17, 2 + j, 1, 30) for j in range(9)]
+    first = oracle.sample(head, u0, 0.7, 0.7)["ids"]
+    hist = np.array([[first[0] + START - 1 if first[0] else EOS] * 4 + [START] * 12], np.int32)
+    params = dict(temperature=0.7, top_p=0.7, top_k=30, **MAP)
+    exp = oracle.ras(head, u0, u1, params, hist)
+    expected = [exp["main"][0], exp["code0"][0]] + [oracle.sample(books[j], uj[j], 0.7, 0.7)["ids"][0]
+                                                    for j in range(9)]
+    frame = hiprt.DeviceBuffer(4 * 11)
+    dh, d0, d1, dhist = (hiprt.to_device(head), hiprt.to_device(u0), hiprt.to_device(u1),
+                         hiprt.to_device(hist))
+    rc = gpu.sample_ras_raw(dh.ptr, gpu.DTYPE_BF16, 1, 4097, 4097, d0.ptr, d1.ptr, dhist.ptr, 16,
+                            gpu.ras_params(**params), frame.ptr, frame.ptr + 4)
+    assert rc == 0
+    keep = []
+    for j in range(9):
+        db, du = hiprt.to_device(books[j]), hiprt.to_device(uj[j])
+        keep += [db, du]
+        assert gpu.sample_raw(db.ptr, gpu.DTYPE_BF16, 1, 4096, 4096, du.ptr, 30, 0.7, 0.7, None,
+                              frame.ptr + 4 * (2 + j)) == 0
+    hiprt.synchronize()
+    assert frame.download((11,), np.int32).tolist() == [int(v) for v in expected]
