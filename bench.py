@@ -15,8 +15,9 @@ around the back-to-back launches.  cpu_baseline = the C oracle (the port of the
 reference semantics; the reference's own CPU path needs mlx-c, absent here)
 on a bounded sample of the same workload, all host cores.
 Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), launch
-times of C2, C4 and C5 at their own shapes, and the fused repetition-aware draw
-against its two separate launches (`other_configs`).
+times of C2, C4 and C5 at their own shapes, the fused repetition-aware draw
+against its two separate launches, and the backbone head's gemv and its sample
+as two launches and as one HIP graph (`other_configs`).
 """
 import argparse
 import json
@@ -34,6 +35,7 @@ for p in (os.path.join(ROOT, "drama3-mlx_amd"), os.path.join(ROOT, "oracle")):
 METRIC = "sampled rows/sec at B=256×4097 (% HBM roofline); p50 µs per single-row sample"
 HBM_PEAK_GBS = 8000.0
 ROWS, V, K = 256, 4097, 30
+K_SAMPLE = K
 BYTES_PER_ROW = V * 4 + K * 4 + 4 + 12  # logits, uniforms, id, (T, top_p, k)
 
 
@@ -312,6 +314,77 @@ def ras_latency(reps):
     return res
 
 
+def head_latency(reps):
+    """The backbone head (src/backbone.c:1213-1215) and its sample: bf16 hidden
+    [1, 2048] x lm_head [4097, 2048]^T (d3s_linear_bf16), then one draw
+    (d3s_sample).  p50 of events around the two launches, and around one replay
+    of a HIP graph holding both (one weight copy for both, as a graph fixes its
+    pointers).  The gemv alone rotates over 32 weight copies (537 MB, over twice
+    the Infinity Cache) so each call reads them from HBM."""
+    import ctypes
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    H = hiprt.hip()
+    K, Vh, copies = 2048, 4097, 32
+    rng = np.random.default_rng(11)
+    x = W.f32_to_bf16_bits(rng.standard_normal((1, K)).astype(np.float32))
+    w = W.f32_to_bf16_bits((rng.standard_normal((Vh, K)) * 0.06).astype(np.float32))
+    bx = hiprt.to_device(x)
+    bw = hiprt.DeviceBuffer(copies * w.nbytes)
+    for c in range(copies):
+        bw.upload(w, offset=c * w.nbytes)
+    y = hiprt.DeviceBuffer(2 * Vh)
+    u = hiprt.DeviceBuffer(4 * K_SAMPLE)
+    assert d3s.lib().d3s_uniform_fill(u.ptr, K_SAMPLE, 11, 0, None) == 0
+    ids = hiprt.DeviceBuffer(16)
+    hiprt.synchronize()
+    s = hiprt.Stream()
+    L = d3s.lib()
+
+    def both(wp):
+        assert L.d3s_linear_bf16(bx.ptr, wp, 1, K, Vh, y.ptr, s.ptr) == 0
+        assert d3s.sample_raw(y.ptr, d3s.DTYPE_BF16, 1, Vh, Vh, u.ptr, K_SAMPLE, 0.7, 0.7, None, ids.ptr,
+                              stream=s.ptr) == 0
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    hiprt.check(H.hipStreamBeginCapture(s.ptr, 0), "begin capture")
+    both(bw.ptr)
+    hiprt.check(H.hipStreamEndCapture(s.ptr, ctypes.byref(graph)), "end capture")
+    hiprt.check(H.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "instantiate")
+    a, b = hiprt.Event(), hiprt.Event()
+    two, replay, gemv = [], [], []
+    for i in range(reps + 20):
+        a.record(s)
+        both(bw.ptr)
+        b.record(s)
+        b.synchronize()
+        t2 = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        hiprt.check(H.hipGraphLaunch(exe, s.ptr), "graph launch")
+        b.record(s)
+        b.synchronize()
+        tg = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        assert L.d3s_linear_bf16(bx.ptr, bw.ptr + (i % copies) * w.nbytes, 1, K, Vh, y.ptr, s.ptr) == 0
+        b.record(s)
+        b.synchronize()
+        if i >= 20:
+            two.append(t2)
+            replay.append(tg)
+            gemv.append(a.elapsed_ms(b) * 1e3)
+    H.hipGraphExecDestroy(exe)
+    H.hipGraphDestroy(graph)
+    s.destroy()
+    g = float(np.median(gemv))
+    res = {"shape": [[1, K], [Vh, K]], "dtype": "bf16", "k": K_SAMPLE,
+           "two_launches_p50_us": float(np.median(two)), "graph_replay_p50_us": float(np.median(replay)),
+           "gemv_p50_us": g, "gemv_weight_GBs": w.nbytes / (g * 1e-6) / 1e9}
+    log(f"head gemv + sample, [1, {K}] x [{Vh}, {K}] bf16: two launches p50 {res['two_launches_p50_us']:.2f} us, "
+        f"one graph replay p50 {res['graph_replay_p50_us']:.2f} us; gemv alone (HBM) {g:.2f} us "
+        f"({res['gemv_weight_GBs']:.0f} GB/s of weights)")
+    return res
+
+
 def cpu_baseline(seconds):
     """The oracle on all host cores over a bounded sample of C3 rows."""
     import d3s_oracle
@@ -399,6 +472,7 @@ def main():
     if not args.no_other:
         others = other_configs(200)
         others["RAS"] = ras_latency(500)
+        others["head"] = head_latency(300)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_k_wave_C3.json")
     if os.path.exists(tpath):

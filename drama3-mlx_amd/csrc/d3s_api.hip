@@ -121,6 +121,24 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
   return launched();
 }
 
+int d3s_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
+                    uint16_t *y, void *stream) {
+  if (n_rows < 0 || n_rows > 65535 || K < 128 || K % 128 != 0 || K > (1 << 20) || V < 1 || V > (1 << 24))
+    return D3S_ERR_ARG;
+  if (n_rows == 0) return D3S_OK;
+  if (!x || !w || !y) return D3S_ERR_ARG;
+  if ((uintptr_t)x % 8u != 0u || (uintptr_t)w % 8u != 0u || (uintptr_t)y % 2u != 0u) return D3S_ERR_ARG;
+  d3s::LinearArgs la;
+  la.x = x;
+  la.w = w;
+  la.K = (int)K;
+  la.V = (int)V;
+  la.n_rows = (int)n_rows;
+  la.y = y;
+  d3s::launch_linear(la, (hipStream_t)stream);
+  return launched();
+}
+
 int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream) {
   if (n < 0 || (n > 0 && !u)) return D3S_ERR_ARG;
   d3s::launch_uniform(u, n, seed, draw, (hipStream_t)stream);

@@ -42,6 +42,14 @@ struct RasArgs {
   int32_t *code0;           /* [n_rows] or null: clip(main - semantic_start, 0, code_vocab - 1) */
 };
 
+/* The backbone head's logits (src/backbone.c:1213-1215; src/mlxu.c:365-400,:492-495). */
+struct LinearArgs {
+  const uint16_t *x; /* [n_rows, K] bf16 */
+  const uint16_t *w; /* [V, K] bf16 */
+  int K, V, n_rows;
+  uint16_t *y;       /* [n_rows, V] bf16 logits */
+};
+
 /* counters[] slots (atomic increments per row) */
 enum {
   CNT_REFUSED = 0,      /* non-finite x: id -1 */
@@ -67,6 +75,8 @@ int wave_max_vocab(Dtype dt);
 /* Launch the fused RAS kernel (both draws k <= 64, V within the wave kernel's
  * reach).  Returns false if no instantiation fits. */
 bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s);
+/* Launch the head's gemv. */
+void launch_linear(const LinearArgs &la, hipStream_t s);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
 /* Launch the wide kernel: one 1024-thread workgroup per row, the row in the

@@ -70,6 +70,14 @@ D3S_HD float d3s_u2f(uint32_t u) {
 /* bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 bits. */
 D3S_HD float d3s_bf16_to_f32(uint16_t b) { return d3s_u2f((uint32_t)b << 16); }
 
+/* fp32 -> bf16, rounded to nearest even; NaN -> a quiet NaN of the same sign
+ * (MLX's bfloat16 conversion, used when the reference's gemv stores its result) */
+D3S_HD uint16_t d3s_f32_to_bf16_rn(float f) {
+  const uint32_t b = d3s_f2u(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x0040u);
+  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
 /* Order-preserving key: a > b (as floats, NaN excluded) iff key(a) > key(b).
  * -0 and +0 compare equal, so -0 is mapped to the key of +0. */
 D3S_HD uint32_t d3s_ordkey(float f) {

@@ -56,6 +56,8 @@ def lib():
         L.d3s_sample_ras.argtypes = [vp, i32, i64, i64, i64, vp, vp, vp, i32,
                                      ctypes.POINTER(RasParams), vp, vp, vp, vp, vp, vp]
         L.d3s_sample_ras.restype = i32
+        L.d3s_linear_bf16.argtypes = [vp, vp, i64, i64, i64, vp, vp]
+        L.d3s_linear_bf16.restype = i32
         L.d3s_uniform_fill.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
         L.d3s_uniform_fill.restype = i32
         L.d3s_max_k.argtypes = []
@@ -236,3 +238,22 @@ def sample_ras(logits, u, u_retry, params, history=None):
     for b in bufs.values():
         b.free()
     return out
+
+
+def linear_bf16(x, w):
+    """Host helper: x uint16 [N, K], w uint16 [V, K] (bf16 bits) -> uint16 [N, V]."""
+    import hiprt
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    N, K = x.shape
+    V = w.shape[0]
+    bx, bw, by = hiprt.to_device(x), hiprt.to_device(w), hiprt.DeviceBuffer(2 * N * V)
+    rc = lib().d3s_linear_bf16(bx.ptr, bw.ptr, N, K, V, by.ptr, None)
+    out = None
+    if rc == OK:
+        hiprt.synchronize()
+        out = by.download((N, V), np.uint16)
+    for b in (bx, bw, by):
+        b.free()
+    return rc, out
+

@@ -102,6 +102,21 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
                    const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
                    int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *stream);
 
+/* The backbone head's logits (src/backbone.c:1213-1215: m_linear of the last
+ * hidden row with lm_head_audio): y[n, r] = bf16 of x[n, :] . w[r, :], in the
+ * order of the reference's single-row gemv (src/mlxu.c:365-400,:492-495): 32
+ * lanes, lane l accumulating in fp32 the products of elements c*128 + 4l + t
+ * (blocks c in order), fused; a shuffle-down tree over 16, 8, 4, 2, 1 lanes;
+ * the sum rounded to nearest-even bf16.  x [n_rows, K], w [V, K], y [n_rows, V]
+ * bf16 device arrays (8-byte aligned), K a multiple of 128.  (The reference
+ * takes this arithmetic for one row; for more rows MLX's matmul order is not
+ * reproduced.)  The head's sample is a d3s_sample on y: the two launches can be
+ * captured together in a HIP graph.
+ * Replaces: backbone_audio_logits (src/backbone.c:1213-1215) through m_linear's
+ * gemv_row (src/mlxu.c:454-496). */
+int d3s_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
+                    uint16_t *y, void *stream);
+
 /* u[i] = the i-th uniform of draw `draw` under `seed` (Philox4x32-10, counter
  * (i/4, draw), key seed, 24-bit values in [0, 1)), for i < n.
  * Replaces: m_uniform (src/mlxu.c:771-774) as used by sample_top_k_top_p

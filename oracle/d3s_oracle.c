@@ -265,6 +265,26 @@ void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n
   }
 }
 
+void d3s_oracle_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K,
+                            int64_t V, uint16_t *y) {
+  for (int64_t n = 0; n < n_rows; n++)
+#pragma omp parallel for
+    for (int64_t r = 0; r < V; r++) {
+      float acc[32];
+      for (int l = 0; l < 32; l++) {
+        acc[l] = 0.0f;
+        for (int64_t c = 0; c < K / 128; c++)
+          for (int t = 0; t < 4; t++) {
+            const int64_t i = c * 128 + 4 * l + t;
+            acc[l] = fmaf(d3s_bf16_to_f32(w[r * K + i]), d3s_bf16_to_f32(x[n * K + i]), acc[l]);
+          }
+      }
+      for (int sn = 16; sn >= 1; sn >>= 1)
+        for (int l = 0; l < sn; l++) acc[l] = acc[l] + acc[l + sn];
+      y[n * V + r] = d3s_f32_to_bf16_rn(acc[0]);
+    }
+}
+
 void d3s_oracle_expf(const float *in, float *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_expf(in[i]);
 }

@@ -75,6 +75,15 @@ void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n
                            const int32_t *history, int history_len, int32_t eos_id,
                            int32_t semantic_start, int32_t semantic_end, int32_t code_vocab,
                            int32_t *main_tok, int32_t *code0);
+/* The backbone head's logits (src/backbone.c:1213-1215, m_linear of one row,
+ * src/mlxu.c:365-400,:492-495): y[n, r] = bf16 of x[n, :] . w[r, :] in the
+ * order of the reference's gemv: 32 lanes, lane l accumulating in fp32 the
+ * products of elements c*128 + 4l + t (blocks c in order, t = 0..3), then a
+ * shuffle-down tree over 16, 8, 4, 2, 1 lanes; lane 0's sum rounded to bf16.
+ * The products are fused into the accumulation (fma): the Metal compiler's
+ * fast-math contraction, which the reference does not pin.  K % 128 == 0. */
+void d3s_oracle_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K,
+                            int64_t V, uint16_t *y);
 void d3s_oracle_expf(const float *in, float *out, int64_t n);
 void d3s_oracle_logf(const float *in, float *out, int64_t n);
 void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n);

@@ -48,6 +48,8 @@ def lib():
         L.d3s_oracle_philox.restype = None
         L.d3s_oracle_ras_select.argtypes = [vp, vp, i64, vp, i32, i32, i32, i32, i32, vp, vp]
         L.d3s_oracle_ras_select.restype = None
+        L.d3s_oracle_linear_bf16.argtypes = [vp, vp, i64, i64, i64, vp]
+        L.d3s_oracle_linear_bf16.restype = None
         L.d3s_oracle_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, i64, i64, vp]
         L.d3s_oracle_uniform.restype = None
         _lib = L
@@ -174,3 +176,16 @@ def ras(logits, u, u_retry, params, history, n_threads=1):
     main, code0 = ras_select(first, retry, history, p["eos_id"], p["semantic_start"],
                              p["semantic_end"], p["code_vocab"])
     return dict(first=first, retry=retry, main=main, code0=code0)
+
+
+def linear_bf16(x, w):
+    """The reference's single-row gemv (bf16 bits in and out): x uint16 [N, K],
+    w uint16 [V, K] -> uint16 [N, V]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    N, K = x.shape
+    V = w.shape[0]
+    assert w.shape[1] == K and K % 128 == 0
+    y = np.empty((N, V), np.uint16)
+    lib().d3s_oracle_linear_bf16(_p(x), _p(w), N, K, V, _p(y))
+    return y
