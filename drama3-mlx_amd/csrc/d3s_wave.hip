@@ -304,23 +304,9 @@ __device__ __forceinline__ int exact_select(const RowRef &R) {
       base += (uint32_t)__popcll(m);
     });
   if (!done) {
-    uint32_t ord0 = 0u, cnt = 0u, ord = 0u;
-    /* chunk row by chunk row: the lane's tie count, an exclusive scan, then
-     * each tie's ordinal in index order */
-#pragma unroll 1
-    for (int j0 = 0; j0 < CPT; j0 += GROUP)
-      for_group<CPT, BF16>(R, j0, [&](int i, float x, bool in) {
-        const int e = i % EPC;
-        if (e == 0) cnt = 0u;
-        cnt += (in && d3s_ordkey(x) == prefix) ? 1u : 0u;
-        if (e == EPC - 1) {
-          const uint32_t incl = wave_scan_add_u32(cnt);
-          ord = ord0 + incl - cnt;
-          ord0 += readlane_u(incl, 63);
-        }
-      });
-    /* second sweep: the same order, now writing the first `need` ties */
-    ord0 = 0u;
+    /* chunk row by chunk row: each lane's tie count, an exclusive scan for
+     * the ties' ordinals in index order, and the first `need` ties written */
+    uint32_t ord0 = 0u;
 #pragma unroll 1
     for (int j0 = 0; j0 < CPT; j0 += GROUP) {
       uint32_t cnts[GROUP * EPC];
