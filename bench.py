@@ -129,6 +129,48 @@ def traffic_probe(pool, g, n):
     log(f"traffic probe: 1 copy of {nbytes} B, {n} launches of {g} C3 batches")
 
 
+def counter_probe(name, pool):
+    """For rocprofv3 --pmc runs: launches of one workload only, each followed by
+    a synchronisation, so every dispatch in the profile is that workload's.
+    c1: 200 single C1 rows; c3one: 50 one-batch C3 launches; c3: 20 headline
+    launches; c4 / c5: 20 launches of C4 / C5."""
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    if name in ("c3", "c3one"):
+        g = 128 if name == "c3" else 1
+        ids = hiprt.DeviceBuffer(4 * ROWS * g)
+        for i in range(20 if name == "c3" else 50):
+            assert pool.launch((i % (pool.n // g)) * g, g, ids, None) == 0
+            hiprt.synchronize()
+        log(f"counter probe {name}: done")
+        return
+    cfg = {"c1": "C1", "c4": "C4", "c5": "C5"}[name]
+    w = W.make(cfg, rows=256 if name == "c1" else None, seed=5, uniforms=False)
+    x = w["logits"]
+    N, Vc = x.shape
+    k = w["k"]
+    dt = d3s.DTYPE_F32 if x.dtype == np.float32 else d3s.DTYPE_BF16
+    lg = hiprt.to_device(x)
+    u = hiprt.DeviceBuffer(4 * N * k)
+    assert d3s.lib().d3s_uniform_fill(u.ptr, N * k, 42, 0, None) == 0
+    ban = hiprt.to_device(w["banned"]) if w["banned"] is not None else None
+    ids = hiprt.DeviceBuffer(4 * N)
+    T, P = w["temperature"], w["top_p"]
+    T = float(T) if np.ndim(T) == 0 else float(T[0])
+    P = float(P) if np.ndim(P) == 0 else float(P[0])
+    for i in range(200 if name == "c1" else 20):
+        if name == "c1":
+            r = i % N
+            rc = d3s.sample_raw(lg.ptr + r * Vc * x.itemsize, dt, 1, Vc, Vc, u.ptr + r * k * 4, k, T, P,
+                                None, ids.ptr)
+        else:
+            rc = d3s.sample_raw(lg.ptr, dt, N, Vc, Vc, u.ptr, k, T, P, ban.ptr if ban else None, ids.ptr)
+        assert rc == 0
+        hiprt.synchronize()
+    log(f"counter probe {name}: done")
+
+
 def launch_floor(n):
     """Events around a near-empty launch (the uniform fill of 64 values): the
     part of any event-timed launch that is dispatch, not work."""
@@ -420,6 +462,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the C2 / C4 / C5 figures")
+    ap.add_argument("--counter-probe", choices=["c1", "c3one", "c3", "c4", "c5"], default=None,
+                    help="only run one workload's launches (for --pmc runs)")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="N",
                     help="only run the copy calibration and N headline launches (for --pmc runs)")
     args = ap.parse_args()
@@ -444,6 +488,9 @@ def main():
     log(f"pool: {args.pool_batches} batches, {pool_mb:.0f} MB")
     if args.traffic_probe:
         traffic_probe(pool, G, args.traffic_probe)
+        return
+    if args.counter_probe:
+        counter_probe(args.counter_probe, pool)
         return
     # headline: G batches per launch, back to back on one stream
     ms, wall, launches = time_batches(pool, args.steps, args.warmup, G, 1)
