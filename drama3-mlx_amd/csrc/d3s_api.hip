@@ -165,6 +165,12 @@ int d3s_exp2_selftest(const float *in, float *out, int64_t n, void *stream) {
   return n > 0 ? launched() : D3S_OK;
 }
 
+int d3s_log2_selftest(const float *in, float *out, int64_t n, void *stream) {
+  if (n < 0 || (n > 0 && (!in || !out))) return D3S_ERR_ARG;
+  d3s::launch_log2_selftest(in, out, n, (hipStream_t)stream);
+  return n > 0 ? launched() : D3S_OK;
+}
+
 const char *d3s_version(void) { return "d3sampler 0.2 gfx950"; }
 
 }  // extern "C"

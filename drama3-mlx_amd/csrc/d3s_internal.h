@@ -79,6 +79,8 @@ bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s);
 void launch_linear(const LinearArgs &la, hipStream_t s);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
+/* out[i] = the hardware log2(in[i]) (v_log_f32) the fast row sum's log uses */
+void launch_log2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
 /* Launch the wide kernel: one 1024-thread workgroup per row, the row in the
  * registers of its 16 waves (k <= 64, V <= wide_max_vocab(dt)). */
 bool launch_wide(const SampleArgs &a, Dtype dt, hipStream_t s);

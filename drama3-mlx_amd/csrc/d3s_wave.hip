@@ -457,12 +457,18 @@ struct WaveRow {
     const float v = key_x(key);
     const int idx = key_idx(key);
     const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    /* the cumulative's terms: exact with the exact lse; with the fast lse only
+     * the cut depends on them, so the hardware 2^x, inside the margin below */
+    const float ec = exact ? d3s_expf(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
     float cc, sp;
-    wave_seq_prefix2(act ? d3s_expf(v - lse) : 0.0f, ep, k, S.buf, S.buf2, cc, sp);
+    wave_seq_prefix2(act ? ec : 0.0f, ep, k, S.buf, S.buf2, cc, sp);
     if (!exact) {
       const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
       const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
-      const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
+      /* a term's relative change: lse's, the rounding of v - lse on either
+       * side, of its product with log2(e) and of log2(e) itself (|v - lse| <=
+       * D), v_exp_f32's error and d3s_expf's */
+      const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f;
       const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
       exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
               (a.flags & FLAG_EXACT_LSE) != 0;
@@ -593,13 +599,17 @@ struct WaveRow {
 #pragma unroll
       for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
     const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
-    const float lse = M + (d3s_logf(sp) - delta * LN2_F);
-    /* relative error bound of 2^-delta S' against the exact row sum: the
-     * rounding of x, m, x - m and log2(e)/T, the fast exponent's error,
-     * d3s_expf's, the terms below e^-40, the fixed-point truncation, and the
-     * accumulation (CPT + 3 + 6 roundings) and the final rounding */
+    /* the hardware log2, within 2^-23 |log2 sp| + 2^-24 (checked by the tests) */
+    const float l2 = __builtin_amdgcn_logf(sp);
+    const float lse = M + (l2 * LN2_F - delta * LN2_F);
+    /* bound on |lse' - lse|, less the final roundings: the relative error of
+     * 2^-delta S' against the exact row sum (the rounding of x, m, x - m and
+     * log2(e)/T, the fast exponent's error, d3s_expf's, the terms below e^-40,
+     * the fixed-point truncation, the accumulation's CPT + 3 + 6 roundings and
+     * the final one), then the log: twice its bound, times ln 2, with the
+     * product's rounding */
     const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
-                        (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f;
+                        (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f + 0x1p-22f * fabsf(l2) + 0x1p-23f;
 
     int n;
     if (need_sel) {
@@ -904,11 +914,11 @@ void k_wide(SampleArgs a) {
     generic_row<BF16>(a, row, kpow, glist);
     return;
   }
-  const float lse = M + (d3s_logf(sp) - delta * LN2_F);
-  /* relative error bound of 2^-delta S' against the exact row sum: the wave
-   * kernel's, with NW - 1 more roundings for the sum over the waves */
+  const float l2 = __builtin_amdgcn_logf(sp); /* within 2^-23 |log2 sp| + 2^-24 */
+  const float lse = M + (l2 * LN2_F - delta * LN2_F);
+  /* the wave kernel's bound, with NW - 1 more roundings for the sum over the waves */
   const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
-                      (float)(CPT + 11 + NW) * 0x1p-24f + (float)V * 0x1p-40f;
+                      (float)(CPT + 11 + NW) * 0x1p-24f + (float)V * 0x1p-40f + 0x1p-22f * fabsf(l2) + 0x1p-23f;
 
   /* ---- file the keys: this wave's slots from base on, lane by lane */
   {
@@ -949,10 +959,10 @@ void k_wide(SampleArgs a) {
     const int idx = key_idx(key);
     const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
     float cc, spp;
-    wave_seq_prefix2(act ? d3s_expf(v - lse) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
+    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
     const float D = lse - readlane_f(v, k - 1);
     const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
-    const float eps_e = dl + 0x1p-23f * (D + 1.0f) + 0x1p-22f;
+    const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f; /* as the wave kernel's */
     const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
     const bool exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
                        (a.flags & FLAG_EXACT_LSE) != 0;
@@ -1025,6 +1035,11 @@ void k_wave(SampleArgs a) {
   r.run();
 }
 
+__global__ void k_log2(const float *in, float *out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __builtin_amdgcn_logf(in[i]);
+}
+
 __global__ void k_exp2(const float *in, float *out, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = __builtin_amdgcn_exp2f(in[i]);
@@ -1062,6 +1077,12 @@ bool try_wide(const SampleArgs &a, hipStream_t s) {
 }
 
 }  // namespace
+
+void launch_log2_selftest(const float *in, float *out, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  const int B = 256;
+  hipLaunchKernelGGL(k_log2, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, in, out, n);
+}
 
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s) {
   if (n <= 0) return;

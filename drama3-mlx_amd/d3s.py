@@ -68,6 +68,8 @@ def lib():
         L.d3s_math_selftest.restype = i32
         L.d3s_exp2_selftest.argtypes = [vp, vp, i64, vp]
         L.d3s_exp2_selftest.restype = i32
+        L.d3s_log2_selftest.argtypes = [vp, vp, i64, vp]
+        L.d3s_log2_selftest.restype = i32
         L.d3s_version.argtypes = []
         L.d3s_version.restype = ctypes.c_char_p
         L.d3_sample.argtypes = [vp, i32, i32, f32, i32, f32, ctypes.c_ulonglong, vp]
@@ -173,6 +175,18 @@ def exp2_selftest(x):
     rc = lib().d3s_exp2_selftest(bi.ptr, bo.ptr, x.size, None)
     if rc != OK:
         raise RuntimeError(f"d3s_exp2_selftest: {rc}")
+    hiprt.synchronize()
+    return bo.download((x.size,), np.float32)
+
+
+def log2_selftest(x):
+    """The hardware log2 x (v_log_f32) behind the wave kernel's fast row sum's log."""
+    import hiprt
+    x = np.ascontiguousarray(x, np.float32)
+    bi, bo = hiprt.to_device(x), hiprt.DeviceBuffer(4 * x.size)
+    rc = lib().d3s_log2_selftest(bi.ptr, bo.ptr, x.size, None)
+    if rc != OK:
+        raise RuntimeError(f"d3s_log2_selftest: {rc}")
     hiprt.synchronize()
     return bo.download((x.size,), np.float32)
 

@@ -139,6 +139,11 @@ int d3s_math_selftest(const float *in, float *out_exp, float *out_log, float *ou
  * margin relies on (checked by the tests). */
 int d3s_exp2_selftest(const float *in, float *out, int64_t n, void *stream);
 
+/* Diagnostic, no counterpart in the reference: out[i] = the hardware log2(in[i])
+ * (v_log_f32) behind the fast row sum's log-sum-exp, whose error bound the
+ * kernel's top-p margin relies on (checked by the tests). */
+int d3s_log2_selftest(const float *in, float *out, int64_t n, void *stream);
+
 /* "d3sampler <version> gfx950" */
 const char *d3s_version(void);
 

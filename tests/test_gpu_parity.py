@@ -92,6 +92,26 @@ def test_hardware_exp2_error_bound(gpu):
     assert gpu.exp2_selftest(np.array([-np.inf], np.float32))[0] == 0.0
 
 
+def test_hardware_log2_error_bound(gpu):
+    """The wave kernel's fast log-sum-exp takes the hardware log2 of its row sum
+    (at least about 1, at most V); its margin assumes an error below one ulp of
+    the result, bounded as 2^-23 |log2 x| + 2^-24, over dense and random samples
+    of [2^-1, 2^24] and every float in [1 - 2^-8, 1 + 2^-8]."""
+    rng = np.random.default_rng(22)
+    one = np.float32(1.0).view(np.uint32)
+    near1 = np.arange(one - (1 << 16), one + (1 << 15), dtype=np.uint32).view(np.float32)
+    x = np.concatenate([np.exp2(np.linspace(-1, 24, 1 << 22)).astype(np.float32),
+                        np.exp2(rng.uniform(-1, 24, 1 << 22)).astype(np.float32), near1,
+                        np.array([0.5, 1.0, 2.0, 4097.0, 2.0 ** 24], np.float32)])
+    got = gpu.log2_selftest(x).astype(np.float64)
+    ref = np.log2(x.astype(np.float64))
+    err = np.abs(got - ref)
+    bound = 2.0 ** -23 * np.abs(ref) + 2.0 ** -24
+    banner(f"v_log_f32: max absolute error {err.max():.3e}, max error / bound {(err / bound).max():.3f} "
+           f"over {x.size} inputs")
+    assert np.all(err < bound)
+
+
 def test_uniform_fill_matches_host(gpu, oracle):
     u = gpu.uniform_fill(100_003, 42, 7)
     assert np.array_equal(u, oracle.uniform(42, 7, 1, 100_003)[0])
