@@ -262,6 +262,22 @@ D3S_HD float d3s_u64_to_f32(uint64_t v) {
 /* fixed-point sum (scale 2^40) -> fp32, round to nearest */
 D3S_HD float d3s_fixsum_to_f32(uint64_t s) { return d3s_u64_to_f32(s) * 0x1.0p-40f; }
 
+/* The smallest s with d3s_fixsum_to_f32(s) > c (UINT64_MAX when none, c NaN
+ * or at least 2^23), so that the test is one integer comparison.  With
+ * t = c * 2^40 (exact): below 2^24 every integer converts exactly, so s =
+ * floor(t) + 1; from 2^24 on t is an integer with half-ulp h = 2^(e - 24),
+ * s = t + h rounds to the even neighbour, which is above t when t's last
+ * mantissa bit is 1, and to t otherwise (then s = t + h + 1). */
+D3S_HD uint64_t d3s_fixsum_gt_threshold(float c) {
+  const float t = c * 0x1.0p+40f;
+  if (!(t >= 0.0f)) return t < 0.0f ? 0ull : ~0ull;
+  if (t >= 0x1.0p+63f) return ~0ull;
+  if (t < 0x1.0p+24f) return (uint64_t)t + 1ull;
+  const uint32_t b = d3s_f2u(t);
+  const int e = (int)((b >> 23) & 0xffu) - 127;
+  return (uint64_t)t + (1ull << (e - 24)) + ((b & 1u) ? 0ull : 1ull);
+}
+
 /* ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ---- */
 typedef struct {
   uint32_t v[4];

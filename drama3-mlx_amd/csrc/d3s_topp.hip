@@ -7,18 +7,20 @@
  * the race draws u[rank] for every kept rank (src/sampling.c:45-47).
  *
  *  1. x = L / T exactly, classification, max m and the smallest finite x.
- *  2. e = d3s_expf(x - m) per element: its 2^-40 fixed-point sum is the exact
- *     row sum (lse = m + log S, src/sampling.c:37-38); with x_0 = m the same
- *     e is each element's term of the renormalised softmax (:43-44).
+ *  2. The exact row sum: 2^-40 fixed-point images of d3s_expf(x - m)
+ *     (lse = m + log S, src/sampling.c:37-38).
  *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 4096
  *     buckets of m - x, scaled to the row's range (a non-decreasing function
  *     of -x, so buckets are ordered), then each element counts the larger
- *     keys of its own bucket.  The keys end in LDS in rank order.
+ *     keys of its own bucket.  The keys end in LDS in rank order, and from
+ *     here on each thread owns consecutive ranks.
  *  4. The cut: exact fixed-point prefix sums of d3s_expf(x_r - lse) over
  *     ranks (the op graph's cumsum, :39-42, rounded once), first r > 0 whose
  *     prefix exceeds top_p.
- *  5. The kept sum of e (exact, fixed point), the probabilities e * inv and
- *     the race p / -log(1 - u[rank]), first maximum (:45-48).
+ *  5. Only the kept ranks (x_0 = m): the exact sum of e_r = d3s_expf(x_r -
+ *     m), the probabilities e_r * inv and the race p / -log(1 - u[rank]),
+ *     first maximum (:43-48).  Dropped ranks race only when no kept score
+ *     is positive.
  * The definition is the generic kernel's for k > 64, bit for bit.  A row
  * whose x fall in few buckets (heavy ties) is still exact, only slower. */
 #include "d3s_generic.h"
@@ -98,6 +100,37 @@ __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
   return m;
 }
 
+/* the race's score of one rank, clamped: NaN, -inf and scores <= -1 never
+ * beat the initial -1 (src/sampling.c:45-48) */
+__device__ __forceinline__ float topp_score(float p, float u) {
+  const float score = p / -d3s_logf(1.0f - u);
+  return score > -1.0f ? score : -1.0f;
+}
+
+/* the first maximum over the workgroup: the greatest score, ties to the
+ * lower rank; every thread gets it */
+__device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
+  wave_argmax(s, r);
+  const int wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) {
+    R.f[wid] = s;
+    R.r[wid] = r;
+  }
+  __syncthreads();
+  s = R.f[0];
+  r = R.r[0];
+#pragma unroll
+  for (int w = 1; w < TNW; w++) {
+    const float os = R.f[w];
+    const int orr = R.r[w];
+    if (os > s || (os == s && orr < r)) {
+      s = os;
+      r = orr;
+    }
+  }
+}
+
 template <int EPT, bool BF16>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_topp(SampleArgs a) {
   __shared__ uint64_t keys[EPT * TBLOCK]; /* by bucket, then by rank */
@@ -105,8 +138,6 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   __shared__ uint32_t bfill[NBK + 1];
   __shared__ uint32_t scan_sh[TNW];
   __shared__ TRed R;
-  __shared__ float sh_best[TNW];
-  __shared__ int sh_bestr[TNW], sh_besti[TNW];
 
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
@@ -147,14 +178,10 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   }
   const float xmin = -nxl;
 
-  /* ---- 2. e = exp(x - m), the exact row sum and lse */
-  float e[EPT];
+  /* ---- 2. the exact row sum and lse (x = -inf, and i >= V, add 0) */
   uint64_t acc = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    e[j] = d3s_expf(x[j] - m); /* 0 for -inf (and for i >= V, x = -inf) */
-    acc += d3s_fix40(e[j]);
-  }
+  for (int j = 0; j < EPT; j++) acc += d3s_fix40_exp(x[j] - m); /* fix40(expf(x - m)) */
   const uint64_t S = block_sum_u64(acc, R);
   const float lse = m + d3s_logf(d3s_fixsum_to_f32(S));
 
@@ -219,45 +246,58 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
     for (int j = 0; j < EPT; j++)
       if (q < bn[j]) rank[j] += keys[b0[j] + q] > key[j] ? 1 : 0;
   }
-  /* this element's uniform, read now: the race needs it last */
+  /* From here on thread t owns the ranks [t RPT, t RPT + RPT): the uniforms
+   * are read in rank order (the race needs them last) and the keys land in
+   * LDS in rank order. */
+  const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
+  const int r0 = tid * RPT;
   float uv[EPT];
 #pragma unroll
-  for (int j = 0; j < EPT; j++) uv[j] = rank[j] < k ? a.u[(size_t)row * k + rank[j]] : 0.0f;
+  for (int q = 0; q < EPT; q++) uv[q] = (q < RPT && r0 + q < k) ? a.u[(size_t)row * k + r0 + q] : 0.0f;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < EPT; j++)
     if (rank[j] < V) keys[rank[j]] = key[j];
   __syncthreads();
 
-  /* ---- 4. the cut: exact prefix sums of exp(x_r - lse) over ranks r < k */
-  const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
-  const int r0 = tid * RPT;
+  /* ---- 4. the cut: exact prefix sums of exp(x_r - lse) over ranks r < k;
+   * fixsum_to_f32(P) > top_p is P >= Tq */
+  const uint64_t Tq = d3s_fixsum_gt_threshold(rp.top_p);
   uint64_t term[EPT];
   uint64_t loc = 0;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
     const int r = r0 + q;
-    term[q] = (q < RPT && r < k) ? d3s_fix40(d3s_expf(key_x(keys[r]) - lse)) : 0ull;
+    term[q] = (q < RPT && r < k) ? d3s_fix40_exp(key_x(keys[r]) - lse) : 0ull; /* x_r <= m <= lse */
     loc += term[q];
   }
   uint64_t P = block_excl_scan_u64(loc, R.lo, R.hi);
   int cut_local = k;
-  /* prefix sums only grow: the cut lies at or before this thread's ranks
-   * only if their last prefix exceeds top_p */
-  if (d3s_fixsum_to_f32(P + loc) > rp.top_p) {
+  /* prefix sums only grow: the cut lies among this thread's ranks only if
+   * their last prefix passes the threshold */
+  if (P + loc >= Tq) {
 #pragma unroll
     for (int q = 0; q < EPT; q++) {
       const int r = r0 + q;
       P += term[q];
-      if (q < RPT && r < k && r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > rp.top_p) cut_local = r;
+      if (q < RPT && r < k && r > 0 && cut_local == k && P >= Tq) cut_local = r;
     }
   }
   const int cut = block_min_i32(cut_local, R);
 
-  /* ---- 5. kept sum, probabilities and the race */
+  /* ---- 5. the kept ranks r < cut (x_0 = m): their exact sum, probabilities
+   * and the race.  Threads whose ranks all lie at or past the cut skip. */
+  float e[EPT];
   uint64_t ks = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) ks += rank[j] < cut ? d3s_fix40(e[j]) : 0ull;
+  for (int q = 0; q < EPT; q++) {
+    const int r = r0 + q;
+    e[q] = 0.0f;
+    if (q < RPT && r < cut) {
+      e[q] = d3s_expf(key_x(keys[r]) - m);
+      ks += d3s_fix40(e[q]);
+    }
+  }
   const float inv = 1.0f / d3s_fixsum_to_f32(block_sum_u64(ks, R));
   /* Proven bounds of each score sc = max(p / noise, -1), noise = -log(1 - u):
    * RN(1 - u) lies within a relative 2^-24 of 1 - u and d3s_logf within one
@@ -265,66 +305,71 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
    * 2^-24) (1 + 2^-23); the margins 2^-18 also cover the bounds' own
    * rounding.  No score below the largest lower bound can be the first
    * maximum: only the others take the exact logarithm and division. */
-  float p[EPT], ub[EPT];
+  float ub[EPT];
   float lbm = -1.0f;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    p[j] = rank[j] < cut ? e[j] * inv : 0.0f;
-    const float uu = uv[j];
-    float lb = -1.0f, hb = __builtin_inff();
-    if (uu >= 0x1p-24f && uu < 1.0f) {
-      /* v_rcp_f32 is within one ulp: inside the margins */
-      lb = p[j] * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * (1.0f - 0x1p-18f);
-      if (uu > 0x1p-24f) hb = p[j] * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * (1.0f + 0x1p-18f);
-    } else if (uu >= 1.0f) {
-      hb = 0.0f; /* noise +inf (score 0) or NaN (score -1) */
+  for (int q = 0; q < EPT; q++) {
+    const int r = r0 + q;
+    ub[q] = -__builtin_inff();
+    if (q < RPT && r < cut) {
+      const float p = e[q] * inv;
+      const float uu = uv[q];
+      float lb = -1.0f, hb = __builtin_inff();
+      if (uu >= 0x1p-24f && uu < 1.0f) {
+        /* v_rcp_f32 is within one ulp: inside the margins */
+        lb = p * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * (1.0f - 0x1p-18f);
+        if (uu > 0x1p-24f) hb = p * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * (1.0f + 0x1p-18f);
+      } else if (uu >= 1.0f) {
+        hb = 0.0f; /* noise +inf (score 0) or NaN (score -1) */
+      }
+      ub[q] = hb;
+      lbm = fmaxf(lbm, lb);
     }
-    ub[j] = rank[j] < k ? hb : -__builtin_inff();
-    if (rank[j] < k) lbm = fmaxf(lbm, lb);
   }
   const float LB = block_max_f(lbm, R);
   float bs = -1.0f;
-  int br = 0x7fffffff, bi = 0;
+  int br = 0x7fffffff;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int r = rank[j];
-    if (r < k) {
-      if (ub[j] >= LB) {
-        const float noise = -d3s_logf(1.0f - uv[j]);
-        const float score = p[j] / noise;
-        const float sc = score > -1.0f ? score : -1.0f; /* NaN, -inf, <= -1 never beat -1 */
+  for (int q = 0; q < EPT; q++) {
+    const int r = r0 + q;
+    if (ub[q] >= LB) { /* only kept ranks: the others hold -inf */
+      const float sc = topp_score(e[q] * inv, uv[q]);
+      if (sc > bs || (sc == bs && r < br)) {
+        bs = sc;
+        br = r;
+      }
+    }
+  }
+  /* A dropped rank has p = 0: its score is 0 or NaN.  With a positive kept
+   * maximum it cannot win; otherwise (u at or near 0 or 1 on every kept
+   * rank) every rank below k races, as in the reference. */
+  block_argmax(bs, br, R);
+  if (!(bs > 0.0f)) {
+    bs = -1.0f;
+    br = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < EPT; q++) {
+      const int r = r0 + q;
+      if (q < RPT && r < k) {
+        const float sc = topp_score(r < cut ? e[q] * inv : 0.0f, uv[q]);
         if (sc > bs || (sc == bs && r < br)) {
           bs = sc;
           br = r;
-          bi = j * TBLOCK + tid;
         }
       }
-      if (a.probs) a.probs[(size_t)row * k + r] = p[j];
-      if (a.cand) a.cand[(size_t)row * k + r] = j * TBLOCK + tid;
     }
+    block_argmax(bs, br, R);
   }
-  /* the first maximum over ranks: the greatest score, ties to the lower rank */
-  {
-    int rr = br;
-    float ss = bs;
-    wave_argmax(ss, rr);
-    const int ii = (int)readlane_u((uint32_t)bi, (int)__builtin_ctzll(__ballot(br == rr && bs == ss)));
-    if (lane == 0) {
-      sh_best[wid] = ss;
-      sh_bestr[wid] = rr;
-      sh_besti[wid] = ii;
+  if (tid == 0) a.ids[row] = key_idx(keys[br]);
+  if (a.probs || a.cand) {
+#pragma unroll
+    for (int q = 0; q < EPT; q++) {
+      const int r = r0 + q;
+      if (q < RPT && r < k) {
+        if (a.probs) a.probs[(size_t)row * k + r] = r < cut ? e[q] * inv : 0.0f;
+        if (a.cand) a.cand[(size_t)row * k + r] = key_idx(keys[r]);
+      }
     }
-  }
-  __syncthreads();
-  if (wid == 0) {
-    float ss = lane < TNW ? sh_best[lane] : -2.0f;
-    int rr = lane < TNW ? sh_bestr[lane] : 0x7fffffff;
-    const int ii = lane < TNW ? sh_besti[lane] : 0;
-    const float s_in = ss;
-    const int r_in = rr;
-    wave_argmax(ss, rr);
-    const int id = (int)readlane_u((uint32_t)ii, (int)__builtin_ctzll(__ballot(r_in == rr && s_in == ss)));
-    if (lane == 0) a.ids[row] = id;
   }
 }
 

@@ -25,6 +25,7 @@ def hip():
         H.hipStreamCreate.argtypes = [ctypes.POINTER(vp)]
         H.hipStreamDestroy.argtypes = [vp]
         H.hipStreamSynchronize.argtypes = [vp]
+        H.hipStreamWaitEvent.argtypes = [vp, vp, ctypes.c_uint]
         H.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
         H.hipEventDestroy.argtypes = [vp]
         H.hipEventRecord.argtypes = [vp, vp]
@@ -40,7 +41,7 @@ def hip():
         H.hipGraphDestroy.argtypes = [vp]
         for f in ("hipMalloc", "hipFree", "hipMemcpy", "hipMemcpyAsync", "hipMemset",
                   "hipDeviceSynchronize", "hipGetDeviceCount", "hipStreamCreate",
-                  "hipStreamDestroy", "hipStreamSynchronize", "hipEventCreate", "hipEventDestroy",
+                  "hipStreamDestroy", "hipStreamSynchronize", "hipStreamWaitEvent", "hipEventCreate", "hipEventDestroy",
                   "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
                   "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate",
                   "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy"):
@@ -117,6 +118,10 @@ class Stream:
 
     def synchronize(self):
         check(hip().hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
+
+    def wait(self, event):
+        """later work on this stream waits for `event` (no host wait)"""
+        check(hip().hipStreamWaitEvent(self.ptr, event.ptr, 0), "hipStreamWaitEvent")
 
     def destroy(self):
         if self.ptr:

@@ -297,6 +297,14 @@ void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40(in[i]);
 }
 
+void d3s_oracle_fix40_exp(const float *z, uint64_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40_exp(z[i]);
+}
+
+void d3s_oracle_fixsum_gt_threshold(const float *c, uint64_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_fixsum_gt_threshold(c[i]);
+}
+
 void d3s_oracle_div_rn(const float *a, float b, float *out, int64_t n) {
   const float y = 1.0f / b;
   for (int64_t i = 0; i < n; i++) out[i] = d3s_div_rn(a[i], b, y);

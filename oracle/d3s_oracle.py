@@ -37,7 +37,8 @@ def lib():
         L.d3s_oracle_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp,
                                         vp, vp, vp, vp, vp, i32]
         L.d3s_oracle_sample.restype = i32
-        for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40"):
+        for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40", "d3s_oracle_fix40_exp",
+                     "d3s_oracle_fixsum_gt_threshold"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         L.d3s_oracle_div_rn.argtypes = [vp, f32, vp, i64]
@@ -121,6 +122,20 @@ def fix40(x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.shape, np.uint64)
     lib().d3s_oracle_fix40(_p(x), _p(out), x.size)
+    return out
+
+
+def fix40_exp(z):
+    z = np.ascontiguousarray(z, np.float32)
+    out = np.empty(z.shape, np.uint64)
+    lib().d3s_oracle_fix40_exp(_p(z), _p(out), z.size)
+    return out
+
+
+def fixsum_gt_threshold(c):
+    c = np.ascontiguousarray(c, np.float32)
+    out = np.empty(c.shape, np.uint64)
+    lib().d3s_oracle_fixsum_gt_threshold(_p(c), _p(out), c.size)
     return out
 
 

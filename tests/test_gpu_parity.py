@@ -369,6 +369,28 @@ def test_ranked_nucleus_edge_rows(gpu, oracle):
         compare(oracle, gpu, x[3:], u[3:], T, 0.9, label=f"nucleus rows T={T}")
 
 
+def test_ranked_nucleus_no_positive_kept_score(gpu, oracle):
+    """k = V with uniforms that leave no kept rank a positive score (u = 0:
+    noise -0, score -inf; u = 1: noise +inf, score 0; u NaN or above 1): the
+    dropped ranks (p = 0, score 0 or NaN) race too, and the first maximum may
+    be a dropped rank."""
+    rng = np.random.default_rng(35)
+    V, N = 4097, 8
+    x = (rng.standard_normal((N, V)) * 3.0).astype(np.float32)
+    u = oracle.uniform(35, 0, N, V)
+    u[0, :3000] = 0.0          # kept ranks -inf: a dropped rank wins
+    u[1, :3000] = 1.0          # kept scores 0: rank 0 wins the tie
+    u[2, :] = np.nan           # every score -1: rank 0
+    u[3, :3000] = 1.5          # kept scores NaN: a dropped rank wins
+    u[4, :3000] = 1e-30        # 1 - u rounds to 1: noise -0
+    u[5, 0] = 0.0              # rank 0 alone scores -inf (p / -0): another kept rank wins
+    got, exp = compare(oracle, gpu, x, u, 1.0, 0.3, label="nucleus no positive kept score")
+    won = lambda r: int(np.nonzero(exp["cand"][r] == exp["ids"][r])[0][0])
+    for r in (0, 3, 4):
+        assert exp["probs"][r, won(r)] == 0.0  # a dropped rank won
+    assert won(1) == 0 and won(2) == 0
+
+
 def _u64_to_f32(v):
     """round to nearest even of a non-negative integer, in fp32"""
     v = int(v)

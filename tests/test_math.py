@@ -76,6 +76,30 @@ def test_fix40_is_floor_of_scaled_value(oracle):
     assert int(oracle.fix40(np.array([3.0], np.float32))[0]) == 1 << 40
 
 
+def test_fused_fix40_exp_equals_two_steps(oracle):
+    """fix40(expf(z)) formed from exp's polynomial value (the kernels' row sums)
+    against the two-step form, on every 61st float of [-110, 0] and the ends."""
+    b = np.arange(0x80000000, 0xC2DC0000, 61, dtype=np.uint64).astype(np.uint32)
+    z = np.concatenate([b.view(np.float32), np.array([0.0, -0.0, -np.inf, -104.0, -103.97], np.float32)])
+    assert np.array_equal(oracle.fix40_exp(z), oracle.fix40(oracle.expf(z)))
+
+
+def test_fixsum_threshold_is_the_least_sum_above(oracle):
+    """The cut's integer test: s = threshold(c) is the least fixed-point sum with
+    fixsum_to_f32(s) > c.  Conversions here are exact (s < 2^53 in float64, then
+    one rounding to float32)."""
+    b = np.arange(0, 0x45800000, 389, dtype=np.uint64).astype(np.uint32)  # [0, 2^12)
+    c = np.concatenate([b.view(np.float32), np.float32([0.95, 0.7, 0.9, 1.0, 2.0 ** -16, 2.0 ** -17])])
+    s = oracle.fixsum_gt_threshold(c)
+    f = lambda v: v.astype(np.float64).astype(np.float32) * np.float32(2.0 ** -40)
+    assert np.all(f(s) > c)
+    pos = s > 0
+    assert np.all(f(s[pos] - np.uint64(1)) <= c[pos])
+    top = np.uint64(2 ** 64 - 1)
+    sp = oracle.fixsum_gt_threshold(np.float32([-1.0, -0.0, np.nan, np.inf, 2.0 ** 23, -np.inf]))
+    assert sp.tolist() == [0, 1, int(top), int(top), int(top), 0]
+
+
 def test_u64_to_f32_round_to_nearest_even(oracle):
     rng = np.random.default_rng(3)
     vals = [0, 1, 2 ** 24, 2 ** 24 + 1, 2 ** 24 + 3, 2 ** 25 + 2, 2 ** 25 + 6, 2 ** 63 + 2 ** 39,
