@@ -32,14 +32,63 @@ namespace {
 
 constexpr int TBLOCK = 1024;
 constexpr int TNW = TBLOCK / WAVE;
-constexpr int NBK = 4096; /* buckets of finite x; bucket NBK holds -inf */
+/* buckets of finite x (bucket NBK holds -inf): 8192 for rows of up to 5120
+ * elements, whose LDS (keys and bucket bounds) then still fits twice per CU */
+constexpr int topp_buckets(int ept) { return ept <= 5 ? 8192 : 4096; }
 
-/* workgroup reductions through LDS; every thread gets the result */
+/* Workgroup reductions.  Each wave reduces on DPP and files its value in
+ * LDS; after the barrier every lane reads entry lane % 16 and the sixteen
+ * entries combine by a butterfly inside each DPP row of 16 lanes (quad_perm
+ * 1,0,3,2; quad_perm 2,3,0,1; row_half_mirror; row_mirror), so every lane
+ * holds the result.  Each call opens with a barrier: the previous call's
+ * entries may still be being read. */
+static_assert(TNW == 16, "one LDS entry per lane of a DPP row");
+constexpr int DPP_X1 = 0xb1, DPP_X2 = 0x4e, DPP_HMIR = 0x141, DPP_MIR = 0x140;
+
 struct TRed {
-  float f[TNW], g[TNW];
-  uint32_t lo[TNW], hi[TNW];
+  float f[TNW], g[TNW], h[TNW];
+  uint64_t s[TNW];
+  uint32_t a[TNW];
   int r[TNW];
 };
+
+template <int C>
+__device__ __forceinline__ float xch_f(float v) {
+  return dpp_f<C, 0xf>(v, v);
+}
+template <int C>
+__device__ __forceinline__ uint32_t xch_u(uint32_t v) {
+  return dpp_u<C, 0xf>(v, v);
+}
+template <int C>
+__device__ __forceinline__ uint64_t xch_u64(uint64_t v) {
+  return ((uint64_t)xch_u<C>((uint32_t)(v >> 32)) << 32) | xch_u<C>((uint32_t)v);
+}
+
+__device__ __forceinline__ float row16_max_f(float v) {
+  v = fmaxf(v, xch_f<DPP_X1>(v));
+  v = fmaxf(v, xch_f<DPP_X2>(v));
+  v = fmaxf(v, xch_f<DPP_HMIR>(v));
+  return fmaxf(v, xch_f<DPP_MIR>(v));
+}
+__device__ __forceinline__ int row16_min_i32(int v) {
+  v = min(v, (int)xch_u<DPP_X1>((uint32_t)v));
+  v = min(v, (int)xch_u<DPP_X2>((uint32_t)v));
+  v = min(v, (int)xch_u<DPP_HMIR>((uint32_t)v));
+  return min(v, (int)xch_u<DPP_MIR>((uint32_t)v));
+}
+__device__ __forceinline__ uint32_t row16_sum_u32(uint32_t v) {
+  v += xch_u<DPP_X1>(v);
+  v += xch_u<DPP_X2>(v);
+  v += xch_u<DPP_HMIR>(v);
+  return v + xch_u<DPP_MIR>(v);
+}
+__device__ __forceinline__ uint64_t row16_sum_u64(uint64_t v) {
+  v += xch_u64<DPP_X1>(v);
+  v += xch_u64<DPP_X2>(v);
+  v += xch_u64<DPP_HMIR>(v);
+  return v + xch_u64<DPP_MIR>(v);
+}
 
 __device__ __forceinline__ float block_max_f(float v, TRed &R) {
   v = wave_max_f(v);
@@ -47,45 +96,34 @@ __device__ __forceinline__ float block_max_f(float v, TRed &R) {
   __syncthreads();
   if (lane_id() == 0) R.f[wid] = v;
   __syncthreads();
-  float m = R.f[0];
-#pragma unroll
-  for (int w = 1; w < TNW; w++) m = fmaxf(m, R.f[w]);
-  return m;
+  return row16_max_f(R.f[lane_id() & 15]);
 }
 
-/* the maxima of two values in one round */
-__device__ __forceinline__ void block_max2_f(float &v, float &w, TRed &R) {
+/* the maxima of three values in one round */
+__device__ __forceinline__ void block_max3_f(float &u, float &v, float &w, TRed &R) {
+  u = wave_max_f(u);
   v = wave_max_f(v);
   w = wave_max_f(w);
-  const int wid = threadIdx.x / WAVE;
+  const int wid = threadIdx.x / WAVE, l16 = lane_id() & 15;
   __syncthreads();
   if (lane_id() == 0) {
-    R.f[wid] = v;
-    R.g[wid] = w;
+    R.f[wid] = u;
+    R.g[wid] = v;
+    R.h[wid] = w;
   }
   __syncthreads();
-  v = R.f[0];
-  w = R.g[0];
-#pragma unroll
-  for (int q = 1; q < TNW; q++) {
-    v = fmaxf(v, R.f[q]);
-    w = fmaxf(w, R.g[q]);
-  }
+  u = row16_max_f(R.f[l16]);
+  v = row16_max_f(R.g[l16]);
+  w = row16_max_f(R.h[l16]);
 }
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
   const uint64_t w = wave_sum_u64(v);
   const int wid = threadIdx.x / WAVE;
   __syncthreads();
-  if (lane_id() == 0) {
-    R.lo[wid] = (uint32_t)w;
-    R.hi[wid] = (uint32_t)(w >> 32);
-  }
+  if (lane_id() == 0) R.s[wid] = w;
   __syncthreads();
-  uint64_t s = 0;
-#pragma unroll
-  for (int w2 = 0; w2 < TNW; w2++) s += ((uint64_t)R.hi[w2] << 32) | R.lo[w2];
-  return s;
+  return row16_sum_u64(R.s[lane_id() & 15]);
 }
 
 __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
@@ -94,10 +132,33 @@ __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
   __syncthreads();
   if (lane_id() == 0) R.r[wid] = v;
   __syncthreads();
-  int m = R.r[0];
-#pragma unroll
-  for (int w = 1; w < TNW; w++) m = min(m, R.r[w]);
-  return m;
+  return row16_min_i32(R.r[lane_id() & 15]);
+}
+
+/* exclusive scan of per-thread counts in thread order; `tot` = the total */
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, TRed &R, uint32_t &tot) {
+  const int lane = lane_id(), wid = threadIdx.x / WAVE;
+  const uint32_t incl = wave_scan_add_u32(v);
+  __syncthreads();
+  if (lane == WAVE - 1) R.a[wid] = incl;
+  __syncthreads();
+  const uint32_t x = R.a[lane & 15];
+  tot = row16_sum_u32(x);
+  return row16_sum_u32((lane & 15) < wid ? x : 0u) + incl - v;
+}
+
+/* the same for per-thread fixed-point sums below 2^45 (the wave scan in
+ * 24-bit parts) */
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, TRed &R) {
+  const int lane = lane_id(), wid = threadIdx.x / WAVE;
+  const uint32_t lo = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t hi = wave_scan_add_u32((uint32_t)(v >> 24));
+  const uint64_t incl = ((uint64_t)hi << 24) + lo;
+  __syncthreads();
+  if (lane == WAVE - 1) R.s[wid] = incl;
+  __syncthreads();
+  const uint64_t x = R.s[lane & 15];
+  return row16_sum_u64((lane & 15) < wid ? x : 0ull) + incl - v;
 }
 
 /* the race's score of one rank, clamped: NaN, -inf and scores <= -1 never
@@ -111,32 +172,37 @@ __device__ __forceinline__ float topp_score(float p, float u) {
  * lower rank; every thread gets it */
 __device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
   wave_argmax(s, r);
-  const int wid = threadIdx.x / WAVE;
+  const int wid = threadIdx.x / WAVE, l16 = lane_id() & 15;
   __syncthreads();
   if (lane_id() == 0) {
     R.f[wid] = s;
     R.r[wid] = r;
   }
   __syncthreads();
-  s = R.f[0];
-  r = R.r[0];
-#pragma unroll
-  for (int w = 1; w < TNW; w++) {
-    const float os = R.f[w];
-    const int orr = R.r[w];
-    if (os > s || (os == s && orr < r)) {
-      s = os;
-      r = orr;
-    }
+  s = R.f[l16];
+  r = R.r[l16];
+#define D3S_ROW16_ARGMAX_STEP(C)                          \
+  {                                                       \
+    const float os = xch_f<C>(s);                         \
+    const int orr = (int)xch_u<C>((uint32_t)r);           \
+    if (os > s || (os == s && orr < r)) {                 \
+      s = os;                                             \
+      r = orr;                                            \
+    }                                                     \
   }
+  D3S_ROW16_ARGMAX_STEP(DPP_X1)
+  D3S_ROW16_ARGMAX_STEP(DPP_X2)
+  D3S_ROW16_ARGMAX_STEP(DPP_HMIR)
+  D3S_ROW16_ARGMAX_STEP(DPP_MIR)
+#undef D3S_ROW16_ARGMAX_STEP
 }
 
 template <int EPT, bool BF16>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_topp(SampleArgs a) {
-  __shared__ uint64_t keys[EPT * TBLOCK]; /* by bucket, then by rank */
-  __shared__ uint32_t bstart[NBK + 2];    /* bucket counts, then first slots */
-  __shared__ uint32_t bfill[NBK + 1];
-  __shared__ uint32_t scan_sh[TNW];
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_topp(
+    SampleArgs a) {
+  constexpr int NBK = topp_buckets(EPT);
+  extern __shared__ uint64_t keys[]; /* V slots: by bucket, then by rank */
+  __shared__ uint32_t bstart[NBK + 1]; /* bucket counts, first slots, then ends */
   __shared__ TRed R;
 
   const int row = (int)blockIdx.x;
@@ -150,28 +216,31 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
 
   /* ---- 1. x, classification, max and smallest finite x */
   float x[EPT];
-  uint32_t fl = 0u;
   float xm = -__builtin_inff(), xl = __builtin_inff();
+  /* every load in flight before the first use (past the row's end, the last
+   * element is read again and ignored) */
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const int i = j * TBLOCK + tid;
-    x[j] = -__builtin_inff();
-    if (i < V) {
-      const float xi = scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite);
-      x[j] = xi;
-      const uint32_t c = classify(xi);
-      fl |= c;
-      if (!(c & 1u)) xm = fmaxf(xm, xi);
-      if (!c) xl = fminf(xl, xi); /* finite */
-    }
+    x[j] = load_logit<BF16>(rowp, i < V ? i : V - 1, rp.banned);
   }
-  const bool bad = __syncthreads_or((int)(fl & 1u)) != 0;
-  if (bad) {
+  /* xm: the maximum with NaN propagated, so NaN or +inf anywhere shows in it;
+   * xl: the least x above -inf */
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    const float xi = i < V ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
+    x[j] = xi;
+    xm = __builtin_elementwise_maximum(xm, xi);
+    xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
+  }
+  const bool refused = !(xm < __builtin_inff()); /* NaN or +inf */
+  float m = refused ? 0.0f : xm, nxl = -xl, bad = refused ? 1.0f : 0.0f;
+  block_max3_f(m, nxl, bad, R);
+  if (bad > 0.0f) {
     write_special(a, row, false);
     return;
   }
-  float m = xm, nxl = -xl;
-  block_max2_f(m, nxl, R);
   if (m == -__builtin_inff()) {
     write_special(a, row, true);
     return;
@@ -188,8 +257,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
   const float dmax = m - xmin;
   const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
-  for (int b = tid; b < NBK + 2; b += TBLOCK) bstart[b] = 0u;
-  for (int b = tid; b < NBK + 1; b += TBLOCK) bfill[b] = 0u;
+  for (int b = tid; b < NBK + 1; b += TBLOCK) bstart[b] = 0u;
   __syncthreads();
   int bk[EPT];
 #pragma unroll
@@ -202,7 +270,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   }
   __syncthreads();
   {
-    /* exclusive scan of the NBK + 1 counts: thread t owns 4 or 5 buckets */
+    /* exclusive scan of the NBK + 1 counts: thread t owns PER of them */
     constexpr int PER = (NBK + 1 + TBLOCK - 1) / TBLOCK;
     uint32_t c[PER], loc = 0u;
 #pragma unroll
@@ -212,14 +280,13 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
       loc += c[q];
     }
     uint32_t tot;
-    uint32_t run = block_excl_scan_u32(loc, scan_sh, tot);
+    uint32_t run = block_excl_scan_u32(loc, R, tot);
 #pragma unroll
     for (int q = 0; q < PER; q++) {
       const int b = tid * PER + q;
       if (b <= NBK) bstart[b] = run;
       run += c[q];
     }
-    if (tid == 0) bstart[NBK + 1] = tot;
   }
   __syncthreads();
   uint64_t key[EPT];
@@ -227,17 +294,18 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   for (int j = 0; j < EPT; j++) {
     const int i = j * TBLOCK + tid;
     key[j] = composite_key(x[j], i);
-    if (i < V) keys[bstart[bk[j]] + atomicAdd(&bfill[bk[j]], 1u)] = key[j];
+    if (i < V) keys[atomicAdd(&bstart[bk[j]], 1u)] = key[j];
   }
   __syncthreads();
+  /* now bstart[b] is the end of bucket b, the start of bucket b + 1 */
   /* the elements' buckets side by side, one member of each per step */
   int rank[EPT];
   uint32_t b0[EPT], bn[EPT], most = 0u;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const bool in = j * TBLOCK + tid < V;
-    b0[j] = in ? bstart[bk[j]] : 0u;
-    bn[j] = in ? bstart[bk[j] + 1] - b0[j] : 0u;
+    b0[j] = in && bk[j] > 0 ? bstart[bk[j] - 1] : 0u;
+    bn[j] = in ? bstart[bk[j]] - b0[j] : 0u;
     rank[j] = in ? (int)b0[j] : 0x7fffffff;
     most = max(most, bn[j]);
   }
@@ -271,7 +339,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
     term[q] = (q < RPT && r < k) ? d3s_fix40_exp(key_x(keys[r]) - lse) : 0ull; /* x_r <= m <= lse */
     loc += term[q];
   }
-  uint64_t P = block_excl_scan_u64(loc, R.lo, R.hi);
+  uint64_t P = block_excl_scan_u64(loc, R);
   int cut_local = k;
   /* prefix sums only grow: the cut lies among this thread's ranks only if
    * their last prefix passes the threshold */
@@ -376,7 +444,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
 template <int EPT, bool BF16>
 bool try_topp(const SampleArgs &a, hipStream_t s) {
   if (a.vocab > EPT * TBLOCK) return false;
-  hipLaunchKernelGGL((k_topp<EPT, BF16>), dim3(a.n_rows), dim3(TBLOCK), 0, s, a);
+  hipLaunchKernelGGL((k_topp<EPT, BF16>), dim3(a.n_rows), dim3(TBLOCK), (size_t)a.vocab * sizeof(uint64_t), s, a);
   return true;
 }
 
