@@ -92,16 +92,15 @@ D3S_HD float d3s_from_ordkey(uint32_t k) {
 
 D3S_HD int d3s_isnan(float f) { return (d3s_f2u(f) & 0x7fffffffu) > 0x7f800000u; }
 
-/* e^a, correctly handling NaN, +-inf, overflow and subnormal results.
- * Branch-free: the main path runs on a clamped argument and the special cases
- * are selected at the end (divergent branches are costly on a GPU wave). */
-D3S_HD float d3s_expf(float a) {
+/* The shared core of the exponentials below: for ac in [-104, 89], n =
+ * round(ac log2 e) (ties to even, exact for |t| < 2^22) and exp's polynomial
+ * value p in [2^-1/2, 2^1/2] at r = ac - n ln 2 (Cody-Waite, ln 2 in two
+ * parts, the first product exact); e^ac = p 2^n. */
+D3S_HD float d3s_exp_core(float ac, float *n_out) {
 #if defined(__clang__)
 #pragma clang fp contract(off)
 #endif
-  const float ac = fminf(fmaxf(a, -0x1.a0p+6f), 0x1.64p+6f); /* [-104, 89]; NaN -> -104 */
   const float t = ac * 0x1.715476p+0f;                        /* a * log2(e) */
-  /* round to nearest even: exact for |t| < 2^22 */
   const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
   float r = D3S_FMAF(n, -0x1.62e400p-1f, ac); /* a - n*ln2_hi (exact) */
   r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);       /* - n*ln2_lo */
@@ -113,6 +112,20 @@ D3S_HD float d3s_expf(float a) {
   p = D3S_FMAF(p, r, 0x1.0p-1f);              /* 1/2! */
   p = D3S_FMAF(p, r, 1.0f);
   p = D3S_FMAF(p, r, 1.0f);
+  *n_out = n;
+  return p;
+}
+
+/* e^a, correctly handling NaN, +-inf, overflow and subnormal results.
+ * Branch-free: the main path runs on a clamped argument and the special cases
+ * are selected at the end (divergent branches are costly on a GPU wave). */
+D3S_HD float d3s_expf(float a) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  const float ac = fminf(fmaxf(a, -0x1.a0p+6f), 0x1.64p+6f); /* [-104, 89]; NaN -> -104 */
+  float n;
+  const float p = d3s_exp_core(ac, &n);
   const int ni = (int)n; /* -150 <= ni <= 128 */
   /* p * 2^ni with one rounding: the first product is exact, the second rounds
    * into the subnormal range (or overflows) when it has to. */
@@ -123,6 +136,22 @@ D3S_HD float d3s_expf(float a) {
   res = a > 0x1.62e430p+6f ? D3S_INF : res; /* > 88.7228394: overflows */
   res = a < -0x1.a0p+6f ? 0.0f : res;       /* < -104: below half the least subnormal */
   return d3s_isnan(a) ? a : res;
+}
+
+/* d3s_expf(a) for a <= 88 or -inf (not NaN): the same bits without the
+ * overflow and NaN cases (up to 88, n <= 127). */
+D3S_HD float d3s_expf_nonpos(float a) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  const float ac = fmaxf(a, -0x1.a0p+6f); /* [-104, 88] */
+  float n;
+  const float p = d3s_exp_core(ac, &n);
+  const int ni = (int)n; /* -150 <= ni <= 127 */
+  const int lo = ni < -126;
+  const float s2 = lo ? 0x1.0p-127f : 1.0f;
+  const float res = (p * d3s_u2f((uint32_t)((lo ? ni + 127 : ni) + 127) << 23)) * s2;
+  return a < -0x1.a0p+6f ? 0.0f : res;
 }
 
 /* natural log, correctly handling NaN, negative, zero, subnormal and +inf;
@@ -200,28 +229,29 @@ D3S_HD uint64_t d3s_fix40(float e) {
   return e > 0.0f ? r : 0; /* 0, -0, negative, NaN */
 }
 
+/* d3s_fix40(e) for e in [0, 1] (not NaN), in float operations: F = e 2^40 is
+ * exact and below 2^40 + 1; its integer part is hi 2^32 + lo with hi =
+ * trunc(F 2^-32) and lo = trunc(F - hi 2^32), the subtraction exact (both
+ * terms are multiples of F's ulp and the difference is below 2^32). */
+D3S_HD uint64_t d3s_fix40_unit(float e) {
+#if defined(__clang__)
+#pragma clang fp contract(off)
+#endif
+  const float F = e * 0x1.0p+40f;
+  const uint32_t hi = (uint32_t)(F * 0x1.0p-32f);
+  const uint32_t lo = (uint32_t)(F - (float)hi * 0x1.0p+32f);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 /* d3s_fix40(d3s_expf(z)) for z <= 0 (or -0, or -inf), without forming the
  * fp32 result: exp's polynomial value p lies in [2^-1/2, 2^1/2], so p * 2^24
  * is an integer below 2^25 and floor(p * 2^n * 2^40) is that integer shifted
  * by n + 16 (results below 2^-126 give 0 either way).  Same bits as the
  * two-step form; fewer instructions for the per-element row sum. */
 D3S_HD uint64_t d3s_fix40_exp(float z) {
-#if defined(__clang__)
-#pragma clang fp contract(off)
-#endif
   const float zc = fmaxf(z, -0x1.a0p+6f); /* [-104, 0]; -inf -> -104 */
-  const float t = zc * 0x1.715476p+0f;
-  const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
-  float r = D3S_FMAF(n, -0x1.62e400p-1f, zc);
-  r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);
-  float p = 0x1.a01a02p-13f;
-  p = D3S_FMAF(p, r, 0x1.6c16c2p-10f);
-  p = D3S_FMAF(p, r, 0x1.111112p-7f);
-  p = D3S_FMAF(p, r, 0x1.555556p-5f);
-  p = D3S_FMAF(p, r, 0x1.555556p-3f);
-  p = D3S_FMAF(p, r, 0x1.0p-1f);
-  p = D3S_FMAF(p, r, 1.0f);
-  p = D3S_FMAF(p, r, 1.0f);
+  float n;
+  const float p = d3s_exp_core(zc, &n);
   const uint64_t P = (uint64_t)(uint32_t)(p * 0x1.0p+24f);
   const int sh = (int)n + 16; /* <= 16 */
   const uint64_t left = P << (sh > 0 ? sh : 0);

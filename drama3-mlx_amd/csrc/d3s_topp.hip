@@ -362,8 +362,8 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
     const int r = r0 + q;
     e[q] = 0.0f;
     if (q < RPT && r < cut) {
-      e[q] = d3s_expf(key_x(keys[r]) - m);
-      ks += d3s_fix40(e[q]);
+      e[q] = d3s_expf_nonpos(key_x(keys[r]) - m); /* in [0, 1] */
+      ks += d3s_fix40_unit(e[q]);
     }
   }
   const float inv = 1.0f / d3s_fixsum_to_f32(block_sum_u64(ks, R));

@@ -344,7 +344,7 @@ __device__ __forceinline__ float exact_lse(const RowRef &R, float M) {
   uint64_t acc = 0;
 #pragma unroll 1
   for (int j0 = 0; j0 < CPT; j0 += GROUP)
-    for_group<CPT, BF16>(R, j0, [&](int, float x, bool in) { acc += in ? d3s_fix40(d3s_expf(x - M)) : 0ull; });
+    for_group<CPT, BF16>(R, j0, [&](int, float x, bool in) { acc += in ? d3s_fix40_exp(x - M) : 0ull; });
   return M + d3s_logf(d3s_fixsum_to_f32(wave_sum_u64(acc)));
 }
 
@@ -456,10 +456,10 @@ struct WaveRow {
     const uint64_t key = act ? S.ranked[lane] : 0ull;
     const float v = key_x(key);
     const int idx = key_idx(key);
-    const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
     /* the cumulative's terms: exact with the exact lse; with the fast lse only
      * the cut depends on them, so the hardware 2^x, inside the margin below */
-    const float ec = exact ? d3s_expf(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
+    const float ec = exact ? d3s_expf_nonpos(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
     float cc, sp;
     wave_seq_prefix2(act ? ec : 0.0f, ep, k, S.buf, S.buf2, cc, sp);
     if (!exact) {
@@ -475,7 +475,7 @@ struct WaveRow {
       if (exact && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
       if (exact) {
         const float lx = exact_lse<CPT, BF16>(ref(), M);
-        cc = wave_seq_cumsum(act ? d3s_expf(v - lx) : 0.0f, k, S.buf);
+        cc = wave_seq_cumsum(act ? d3s_expf_nonpos(v - lx) : 0.0f, k, S.buf);
       }
     }
     return wave_race_prefix(a, row, idx, cc, ep, sp, noise, top_p);
@@ -957,7 +957,7 @@ void k_wide(SampleArgs a) {
     const uint64_t key = act ? S.ranked[lane] : 0ull;
     const float v = key_x(key);
     const int idx = key_idx(key);
-    const float ep = act ? d3s_expf(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
     float cc, spp;
     wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
     const float D = lse - readlane_f(v, k - 1);

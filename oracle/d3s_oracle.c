@@ -297,6 +297,14 @@ void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40(in[i]);
 }
 
+void d3s_oracle_fix40_unit(const float *e, uint64_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40_unit(e[i]);
+}
+
+void d3s_oracle_expf_nonpos(const float *a, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = d3s_expf_nonpos(a[i]);
+}
+
 void d3s_oracle_fix40_exp(const float *z, uint64_t *out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = d3s_fix40_exp(z[i]);
 }

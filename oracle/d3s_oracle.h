@@ -87,6 +87,10 @@ void d3s_oracle_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows
 void d3s_oracle_expf(const float *in, float *out, int64_t n);
 void d3s_oracle_logf(const float *in, float *out, int64_t n);
 void d3s_oracle_fix40(const float *in, uint64_t *out, int64_t n);
+/* out[i] = d3s_fix40_unit(e[i]), the kernels' fix40 for e in [0, 1] */
+void d3s_oracle_fix40_unit(const float *e, uint64_t *out, int64_t n);
+/* out[i] = d3s_expf_nonpos(a[i]), the kernels' expf for a <= 0 */
+void d3s_oracle_expf_nonpos(const float *a, float *out, int64_t n);
 /* out[i] = d3s_fix40_exp(z[i]), the kernels' fused form of fix40(expf(z)), z <= 0 */
 void d3s_oracle_fix40_exp(const float *z, uint64_t *out, int64_t n);
 /* out[i] = the smallest s with fixsum_to_f32(s) > c[i] (the kernels' cut test) */

@@ -38,7 +38,7 @@ def lib():
                                         vp, vp, vp, vp, vp, i32]
         L.d3s_oracle_sample.restype = i32
         for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40", "d3s_oracle_fix40_exp",
-                     "d3s_oracle_fixsum_gt_threshold"):
+                     "d3s_oracle_fixsum_gt_threshold", "d3s_oracle_fix40_unit", "d3s_oracle_expf_nonpos"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         L.d3s_oracle_div_rn.argtypes = [vp, f32, vp, i64]
@@ -122,6 +122,20 @@ def fix40(x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.shape, np.uint64)
     lib().d3s_oracle_fix40(_p(x), _p(out), x.size)
+    return out
+
+
+def fix40_unit(e):
+    e = np.ascontiguousarray(e, np.float32)
+    out = np.empty(e.shape, np.uint64)
+    lib().d3s_oracle_fix40_unit(_p(e), _p(out), e.size)
+    return out
+
+
+def expf_nonpos(a):
+    a = np.ascontiguousarray(a, np.float32)
+    out = np.empty(a.shape, np.float32)
+    lib().d3s_oracle_expf_nonpos(_p(a), _p(out), a.size)
     return out
 
 

@@ -84,6 +84,20 @@ def test_fused_fix40_exp_equals_two_steps(oracle):
     assert np.array_equal(oracle.fix40_exp(z), oracle.fix40(oracle.expf(z)))
 
 
+def test_nonpositive_expf_and_unit_fix40_equal_the_general_forms(oracle):
+    """The kernels' shortcuts for arguments they know the range of: expf up
+    to 88 (every 61st float of [-110, 0], a grid of [0, 88], -inf) and fix40 on [0, 1]
+    (every 101st float, the ends), bit for bit against the general forms."""
+    b = np.arange(0x80000000, 0xC2DC0000, 61, dtype=np.uint64).astype(np.uint32)
+    a = np.concatenate([b.view(np.float32), np.linspace(0, 88, 100_001, dtype=np.float32),
+                        np.float32([0.0, -0.0, -np.inf, -104.0, -103.97, -87.3, -88.0, 88.0, 1e-30])])
+    assert np.array_equal(oracle.expf_nonpos(a).view(np.uint32), oracle.expf(a).view(np.uint32))
+    b = np.arange(0, 0x3F800001, 101, dtype=np.uint64).astype(np.uint32)
+    e = np.concatenate([b.view(np.float32), np.float32([0.0, -0.0, 1.0, 0.5, 2.0 ** -40, 2.0 ** -41, 1e-45,
+                                                       np.nextafter(np.float32(1), np.float32(0))])])
+    assert np.array_equal(oracle.fix40_unit(e), oracle.fix40(e))
+
+
 def test_fixsum_threshold_is_the_least_sum_above(oracle):
     """The cut's integer test: s = threshold(c) is the least fixed-point sum with
     fixsum_to_f32(s) > c.  Conversions here are exact (s < 2^53 in float64, then
