@@ -714,6 +714,64 @@ struct __align__(16) WideLds {
   uint32_t exact;
 };
 
+/* The workgroup's tail once its `tot` candidates (every key that can rank
+ * below k) are in S.keys: ranks by counting (thread t < tot counts the keys
+ * above its own), then wave 0 runs the wave kernel's cumulative, margin test
+ * and race; a cut within the fast sum's margin samples the row again by the
+ * generic procedure.  Every thread of the 1024 calls it. */
+template <bool BF16>
+__device__ __forceinline__ void wide_finish(const SampleArgs &a, int row, WideLds &S, uint64_t *glist,
+                                            uint32_t tot, float M, float lse, float eps_s, float noise,
+                                            float top_p, int kpow) {
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int lane = lane_id();
+  const int k = a.k;
+  if (threadIdx.x == 0) {
+    S.keys[tot] = 0ull; /* pads below every key */
+    S.keys[tot + 1] = 0ull;
+  }
+  __syncthreads();
+  /* ---- ranks: candidate t counts the keys above its own */
+  if (threadIdx.x < tot) {
+    const uint64_t my = S.keys[threadIdx.x];
+    const ulonglong2 *k2 = (const ulonglong2 *)S.keys;
+    int rank = 0;
+#pragma unroll 4
+    for (int j2 = 0; j2 < (int)(tot + 1) / 2; j2++) {
+      const ulonglong2 q = k2[j2];
+      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
+    }
+    if (rank < k) S.ranked[rank] = my;
+  }
+  __syncthreads();
+  /* ---- the tail on wave 0 (the wave kernel's, with its margin test) */
+  if (wid == 0) {
+    const bool act = lane < k;
+    const uint64_t key = act ? S.ranked[lane] : 0ull;
+    const float v = key_x(key);
+    const int idx = key_idx(key);
+    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+    float cc, spp;
+    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
+    const float D = lse - readlane_f(v, k - 1);
+    const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
+    const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f; /* as the wave kernel's */
+    const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+    const bool exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
+                       (a.flags & FLAG_EXACT_LSE) != 0;
+    if (exact) {
+      if (lane == 0) {
+        S.exact = 1u;
+        if (a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+      }
+    } else {
+      wave_race_prefix(a, row, idx, cc, ep, spp, noise, top_p);
+    }
+  }
+  __syncthreads();
+  if (S.exact) generic_row<BF16>(a, row, kpow, glist);
+}
+
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WIDE_NW) __attribute__((amdgpu_waves_per_eu(4)))
 void k_wide(SampleArgs a) {
@@ -933,50 +991,7 @@ void k_wide(SampleArgs a) {
       if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(read_logit(p), T, y, true), p);
     }
   }
-  if (threadIdx.x == 0) {
-    S.keys[tot] = 0ull; /* pads below every key */
-    S.keys[tot + 1] = 0ull;
-  }
-  __syncthreads();
-  /* ---- ranks: candidate t counts the keys above its own */
-  if (threadIdx.x < tot) {
-    const uint64_t my = S.keys[threadIdx.x];
-    const ulonglong2 *k2 = (const ulonglong2 *)S.keys;
-    int rank = 0;
-#pragma unroll 4
-    for (int j2 = 0; j2 < (int)(tot + 1) / 2; j2++) {
-      const ulonglong2 q = k2[j2];
-      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
-    }
-    if (rank < k) S.ranked[rank] = my;
-  }
-  __syncthreads();
-  /* ---- the tail on wave 0 (the wave kernel's, with its margin test) */
-  if (wid == 0) {
-    const bool act = lane < k;
-    const uint64_t key = act ? S.ranked[lane] : 0ull;
-    const float v = key_x(key);
-    const int idx = key_idx(key);
-    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
-    float cc, spp;
-    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
-    const float D = lse - readlane_f(v, k - 1);
-    const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
-    const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f; /* as the wave kernel's */
-    const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-    const bool exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
-                       (a.flags & FLAG_EXACT_LSE) != 0;
-    if (exact) {
-      if (lane == 0) {
-        S.exact = 1u;
-        if (a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-      }
-    } else {
-      wave_race_prefix(a, row, idx, cc, ep, spp, noise, top_p);
-    }
-  }
-  __syncthreads();
-  if (S.exact) generic_row<BF16>(a, row, kpow, glist);
+  wide_finish<BF16>(a, row, S, glist, tot, M, lse, eps_s, noise, top_p, kpow);
 }
 
 

@@ -305,6 +305,56 @@ def test_wide_unaligned_banned_and_edge_rows(gpu, oracle):
                 label=f"wide rows T={T}")
 
 
+@pytest.mark.parametrize("bf16,V", [(True, 200003), (False, 100000), (True, 151936)])
+def test_wide_rows_with_structure_across_the_row(gpu, oracle, bf16, V):
+    """Wide rows (the one-workgroup kernel's, and past it the generic
+    kernel's) with structure spread over the row: the top k at the bounds of
+    32 KB stretches, a refusal near the end, masked halves, ties everywhere,
+    the banned index, the top k inside one stretch, a wide value range and
+    fewer finite elements than k; against the oracle and the generic kernel."""
+    rng = np.random.default_rng([V, 7])
+    N = 12
+    seg = 8192  # a 32 KB (bf16: 16 KB) stretch
+    nseg = -(-V // seg)
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    bounds = np.arange(1, nseg) * seg
+    x[1, np.clip(np.concatenate([bounds - 1, bounds, bounds + 1]), 0, V - 1)] += 9.0  # top k at stretch bounds
+    x[2, V - 3] = np.nan                   # refused, in the last segment
+    x[3, : V // 2] = -np.inf               # half the row masked
+    x[5] = np.round(x[5])                  # ties across the row
+    x[6, seg + 10: seg + 60] += 20.0       # the top k inside one stretch
+    x[7] *= 40.0                           # most of the row far below its max
+    x[8, :] = -np.inf
+    x[8, [3, V // 2, V - 1]] = 0.5         # three finite elements: fewer than k
+    ban = np.full(N, -1, np.int32)
+    ban[4] = int(np.argmax(x[4]))
+    ban[9] = int(bounds[0])
+    x[9, bounds[0]] = 30.0                 # the banned index would be the max
+    T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    u = oracle.uniform(41, 0, N, 30)
+    xs = W.f32_to_bf16_bits(x) if bf16 else x
+    got, _ = compare(oracle, gpu, xs, u, T, top_p, banned=ban, label=f"wide structured V={V} bf16={bf16}")
+    assert got["ids"][2] == -1
+    gen, _ = compare(oracle, gpu, xs, u, T, top_p, banned=ban, flags=gpu.FLAG_GENERIC,
+                     label="wide structured rows, generic kernel")
+    assert np.array_equal(got["ids"], gen["ids"])
+    for T1 in (np.inf, 1e-5):
+        compare(oracle, gpu, xs[:6], u[:6], T1, 0.9, label=f"wide structured rows T={T1}")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_wide_kernel_on_many_rows(gpu, oracle, bf16):
+    """A launch of many rows too wide for one wave (one workgroup each)."""
+    rng = np.random.default_rng(44 + bf16)
+    N, V = 130, 70000
+    x = (rng.standard_normal((N, V)) * 3).astype(np.float32)
+    x[np.arange(N), rng.integers(0, V, N)] += 7.0
+    u = oracle.uniform(44, 0, N, 30)
+    xs = W.f32_to_bf16_bits(x) if bf16 else x
+    compare(oracle, gpu, xs, u, 0.8, 0.9, label=f"wide kernel, {N} rows bf16={bf16}")
+
+
 def test_wide_top_p_on_a_cumulative_boundary(gpu, oracle):
     """top_p one ulp either side of a row's own cumulative value: every row is
     within the fast sum's margin and takes the exact fallback."""
