@@ -428,24 +428,34 @@ def head_latency(reps):
 
 
 def cpu_baseline(seconds):
-    """The oracle on all host cores over a bounded sample of C3 rows."""
+    """The oracle (ids only: no probabilities or float64 boundary shadow) on
+    all host cores over a bounded sample of C3 rows, and its per-row time on
+    one thread for C1 rows (a 2000-row call, so the per-call cost is spread)."""
     import d3s_oracle
     import d3s_workloads as W
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     w = W.make("C3", rows=ROWS, seed=7, uniforms=False)
     u = d3s_oracle.uniform(42, 0, ROWS, K)
+    run = lambda: d3s_oracle.sample(w["logits"], u, w["temperature"], w["top_p"], n_threads=threads,
+                                    detail=False)
     # calibrate, then run about `seconds` of work
     t0 = time.perf_counter()
-    d3s_oracle.sample(w["logits"], u, w["temperature"], w["top_p"], n_threads=threads)
+    run()
     per_batch = time.perf_counter() - t0
     n = max(1, int(seconds / max(per_batch, 1e-6)))
     t0 = time.perf_counter()
     for _ in range(n):
-        d3s_oracle.sample(w["logits"], u, w["temperature"], w["top_p"], n_threads=threads)
+        run()
     dt = time.perf_counter() - t0
+    c1 = W.make("C1", rows=2000, seed=7, uniforms=False)
+    u1 = d3s_oracle.uniform(42, 1, 2000, K)
+    t0 = time.perf_counter()
+    d3s_oracle.sample(c1["logits"], u1, 0.7, 0.7, n_threads=1, detail=False)
+    c1_us = (time.perf_counter() - t0) / 2000 * 1e6
     return dict(value=n * ROWS / dt, unit="rows/s", cores=int(threads), kind="port",
                 sample=f"{n} batches x {ROWS} rows of C3 (fp32 [256,4097], k=30), C oracle "
-                       f"(-O2, OpenMP over rows) on {threads} threads, {dt:.1f} s")
+                       f"(-O2 -march=x86-64-v3, OpenMP over rows, ids only) on {threads} threads, {dt:.1f} s",
+                c1_row_us_1_thread=c1_us)
 
 
 def main():
@@ -539,7 +549,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline")
         cpu = cpu_baseline(args.cpu_seconds)
-        log(f"cpu: {cpu['value']:.3e} rows/s on {cpu['cores']} threads")
+        log(f"cpu: {cpu['value']:.3e} rows/s on {cpu['cores']} threads; C1 row on one thread "
+            f"{cpu['c1_row_us_1_thread']:.1f} us")
     out = {
         "metric": METRIC,
         "value": value,

@@ -163,6 +163,7 @@ static void sample_row(const float *L, int64_t V, int k, const float *u, float T
   *id_out = top[choice].i;
   if (lse_out) *lse_out = lse;
 
+  if (!flags_out && !gaps) return; /* no classification asked for */
   /* float64 shadow, for classifying rows where accumulation order could matter */
   double s64 = 0.0;
   for (int64_t i = 0; i < V; i++) s64 += exp((double)x[i] - (double)m);

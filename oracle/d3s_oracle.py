@@ -61,10 +61,12 @@ def _p(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
-def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=None, vocab=None):
+def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=None, vocab=None,
+           detail=True):
     """Oracle sampling.  logits: float32 [N, >=V] or uint16 (bf16 bits) [N, >=V];
     u: float32 [N, k]; temperature / top_p: scalars or float32 [N] arrays.
-    Returns dict(ids, probs, cand, lse, flags, gaps)."""
+    Returns dict(ids, probs, cand, lse, flags, gaps); with detail=False only
+    ids (no probabilities, candidates, lse or float64 boundary shadow)."""
     logits = np.ascontiguousarray(logits)
     if logits.dtype == np.float32:
         dtype = DTYPE_F32
@@ -91,11 +93,11 @@ def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=N
         p_s = float(top_p)
     ban = None if banned is None else np.ascontiguousarray(banned, np.int32)
     ids = np.empty(N, np.int32)
-    probs = np.empty((N, k), np.float32)
-    cand = np.empty((N, k), np.int32)
-    lse = np.empty(N, np.float32)
-    flags = np.empty(N, np.uint8)
-    gaps = np.empty((N, 2), np.float64)
+    probs = np.empty((N, k), np.float32) if detail else None
+    cand = np.empty((N, k), np.int32) if detail else None
+    lse = np.empty(N, np.float32) if detail else None
+    flags = np.empty(N, np.uint8) if detail else None
+    gaps = np.empty((N, 2), np.float64) if detail else None
     rc = lib().d3s_oracle_sample(_p(logits), dtype, N, V, stride, _p(u), k, _p(t_arr), _p(p_arr), t_s,
                                  p_s, _p(ban), _p(ids), _p(probs), _p(cand), _p(lse), _p(flags),
                                  _p(gaps), n_threads)
