@@ -247,12 +247,18 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   }
   const float xmin = -nxl;
 
-  /* ---- 2. the exact row sum and lse (x = -inf, and i >= V, add 0) */
+  /* ---- 2. e = exp(x - m) and the exact row sum and lse (x = -inf, and
+   * i >= V, add 0); e is also each element's softmax term (x_0 = m) */
+  float ev[EPT];
   uint64_t acc = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) acc += d3s_fix40_exp(x[j] - m); /* fix40(expf(x - m)) */
+  for (int j = 0; j < EPT; j++) {
+    ev[j] = d3s_expf_nonpos(x[j] - m); /* in [0, 1] */
+    acc += d3s_fix40_unit(ev[j]);
+  }
   const uint64_t S = block_sum_u64(acc, R);
-  const float lse = m + d3s_logf(d3s_fixsum_to_f32(S));
+  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
+  const float lse = m + lnS;
 
   /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
   const float dmax = m - xmin;
@@ -315,8 +321,8 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
       if (q < bn[j]) rank[j] += keys[b0[j] + q] > key[j] ? 1 : 0;
   }
   /* From here on thread t owns the ranks [t RPT, t RPT + RPT): the uniforms
-   * are read in rank order (the race needs them last) and the keys land in
-   * LDS in rank order. */
+   * are read in rank order (the race needs them last), and LDS holds by rank
+   * each element's e (high word) and ~index (low word). */
   const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
   const int r0 = tid * RPT;
   float uv[EPT];
@@ -325,33 +331,110 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < EPT; j++)
-    if (rank[j] < V) keys[rank[j]] = key[j];
+    if (rank[j] < k) keys[rank[j]] = ((uint64_t)d3s_f2u(ev[j]) << 32) | (uint32_t)key[j];
   __syncthreads();
 
-  /* ---- 4. the cut: exact prefix sums of exp(x_r - lse) over ranks r < k;
-   * fixsum_to_f32(P) > top_p is P >= Tq */
+  /* ---- 4. the cut: the first r > 0 whose exact prefix P_r of the terms
+   * fix40(expf(x_r - lse)) passes top_p (fixsum_to_f32(P) > top_p is P >=
+   * Tq).  First from the prefixes Q_r of fix40(e_r): with G = exp(m - lse)
+   * and G' = 2^40 / S, |P_r - Q_r G'| <= eps' (Q_r + k) G' + k.  eps' is
+   * each term's relative error, its two argument roundings (2^-24 z on
+   * either side, z = lse - x_r <= min(lse - xmin, 30): terms with larger z
+   * are below one unit on both sides) and two expf ulps, plus G's against
+   * G' (the roundings of S 2^-40, of m + log S, and the log's ulp).  Ranks
+   * with Q_r >= Tdrop certainly drop, those with Q_r < Tkeep certainly stay;
+   * if the rank before the first certain drop does not certainly stay, the
+   * exact prefixes decide. */
   const uint64_t Tq = d3s_fixsum_gt_threshold(rp.top_p);
-  uint64_t term[EPT];
-  uint64_t loc = 0;
+  uint64_t qt[EPT];
+  uint64_t qloc = 0;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
     const int r = r0 + q;
-    term[q] = (q < RPT && r < k) ? d3s_fix40_exp(key_x(keys[r]) - lse) : 0ull; /* x_r <= m <= lse */
-    loc += term[q];
+    qt[q] = (q < RPT && r < k) ? d3s_fix40_unit(d3s_u2f((uint32_t)(keys[r] >> 32))) : 0ull;
+    qloc += qt[q];
   }
-  uint64_t P = block_excl_scan_u64(loc, R);
-  int cut_local = k;
-  /* prefix sums only grow: the cut lies among this thread's ranks only if
-   * their last prefix passes the threshold */
-  if (P + loc >= Tq) {
+  uint64_t Qp = block_excl_scan_u64(qloc, R);
+  int cut;
+  bool exact_cut = false;
+  if (Tq == 0ull) {
+    cut = 1; /* every prefix passes; rank 0 never drops */
+  } else if (Tq > ((uint64_t)k << 41)) {
+    cut = k; /* no prefix of at most k terms below 1 reaches it */
+  } else {
+    /* in fp32: S' = RN(S 2^-40) = 1 / G' within 2^-24; every product and
+     * conversion below is within a relative 2^-23, inside the extra 2^-20 */
+    const float Sf = d3s_fixsum_to_f32(S);
+    const float zf = lse - xmin;
+    const float z = zf < 30.0f ? zf : 30.0f; /* NaN and inf too */
+    const float et = 0x1p-24f * 1.01f * 2.0f * z + 0x1p-22f;
+    const float ulp_ln = lnS > 0x1p-126f ? ldexpf(1.0f, ilogbf(lnS) - 23) : 0x1p-126f;
+    const float eg = 0x1p-24f * 1.01f * (fabsf(lse) + 1.0f) + 1.01f * ulp_ln;
+    const float ep = (et * 1.0001f + 1.01f * eg) * (1.0f + 1.01f * eg);
+    const float slack = ep * (float)k / Sf + (float)k;
+    const float Tqf = (float)Tq;
+    /* 1 / (1 - ep) <= 1 + 1.13 ep and 1 / (1 + ep) >= 1 - ep for ep < 1/16 */
+    const float dd = (Tqf + slack) * Sf * (1.0f + 1.13f * ep + 0x1p-20f);
+    const float dk = (Tqf - slack) * Sf * (1.0f - ep - 0x1p-20f);
+    /* (an lse so large that the band is wide leaves every rank to the exact
+     * prefixes: no rank certainly drops, none certainly stays) */
+    const bool wide = !(ep < 0x1p-4f);
+    const uint64_t Tdrop = wide || !(dd < 0x1p62f) ? ~0ull : (uint64_t)dd + 2ull;
+    const uint64_t Tkeep = wide || !(dk > 2.0f) ? 0ull : (dk < 0x1p62f ? (uint64_t)dk - 1ull : (1ull << 62));
+    int drop = k;
+    uint64_t Q = Qp;
 #pragma unroll
     for (int q = 0; q < EPT; q++) {
       const int r = r0 + q;
-      P += term[q];
-      if (q < RPT && r < k && r > 0 && cut_local == k && P >= Tq) cut_local = r;
+      Q += qt[q];
+      if (q < RPT && r < k && r > 0 && drop == k && Q >= Tdrop) drop = r;
     }
+    cut = block_min_i32(drop, R);
+    /* the rank before it (or the last rank) must certainly stay */
+    const int last = cut - 1;
+    if (threadIdx.x == 0) R.a[0] = 0u;
+    __syncthreads();
+    if (last > 0 && last >= r0 && last < r0 + RPT) {
+      Q = Qp;
+#pragma unroll
+      for (int q = 0; q < EPT; q++)
+        if (r0 + q <= last) Q += qt[q];
+      if (!(Q < Tkeep)) R.a[0] = 1u;
+    }
+    __syncthreads();
+    exact_cut = R.a[0] != 0u || (a.flags & FLAG_EXACT_LSE) != 0;
   }
-  const int cut = block_min_i32(cut_local, R);
+  if (exact_cut) {
+    if (threadIdx.x == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+    /* x_r again from the row (the banned index stays -inf), then the exact
+     * prefixes */
+    uint64_t term[EPT];
+    uint64_t loc = 0;
+#pragma unroll
+    for (int q = 0; q < EPT; q++) {
+      const int r = r0 + q;
+      term[q] = 0ull;
+      if (q < RPT && r < k) {
+        const int idx = key_idx(keys[r]);
+        const float xr = scale_logit(load_logit<BF16>(rowp, idx, rp.banned), T, y, t_finite);
+        term[q] = d3s_fix40_exp(xr - lse); /* x_r <= m <= lse */
+      }
+      loc += term[q];
+    }
+    uint64_t P = block_excl_scan_u64(loc, R);
+    int cut_local = k;
+    /* prefix sums only grow: the cut lies among this thread's ranks only if
+     * their last prefix passes the threshold */
+    if (P + loc >= Tq) {
+#pragma unroll
+      for (int q = 0; q < EPT; q++) {
+        const int r = r0 + q;
+        P += term[q];
+        if (q < RPT && r < k && r > 0 && cut_local == k && P >= Tq) cut_local = r;
+      }
+    }
+    cut = block_min_i32(cut_local, R);
+  }
 
   /* ---- 5. the kept ranks r < cut (x_0 = m): their exact sum, probabilities
    * and the race.  Threads whose ranks all lie at or past the cut skip. */
@@ -362,7 +445,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
     const int r = r0 + q;
     e[q] = 0.0f;
     if (q < RPT && r < cut) {
-      e[q] = d3s_expf_nonpos(key_x(keys[r]) - m); /* in [0, 1] */
+      e[q] = d3s_u2f((uint32_t)(keys[r] >> 32)); /* exp(x_r - m), in [0, 1] */
       ks += d3s_fix40_unit(e[q]);
     }
   }
