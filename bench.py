@@ -2,12 +2,12 @@
 
 Headline (`value`): sampled rows/s on C3, the batched backbone head
 (fp32 [256, 4097], per-row T/top_p, k = 30) in steady state: multi-batch
-launches, `--batches-per-launch` batches of 256 rows per d3s_sample call,
-taken in turn by `--headline-streams` streams (default 3), so that one
-launch's last waves overlap the next one's first, over a pool of
-`--pool-batches` batches in device memory (default 256 batches, 1.08 GB, over
-four times the 256 MB Infinity Cache, so every launch reads HBM; 16 distinct
-generated contents, every batch with its own uniforms).  Beside it: one batch
+launches, `--batches-per-launch` batches of 256 rows per d3s_sample call
+(default 512: 131 072 rows), taken in turn by `--headline-streams` streams
+(default 3), so that one launch's last waves overlap the next one's first, over
+a pool of `--pool-batches` batches in device memory (default 512 batches,
+2.2 GB, over eight times the 256 MB Infinity Cache, so every launch reads HBM;
+16 distinct generated contents, every batch with its own uniforms).  Beside it: one batch
 per launch on one stream and on `--streams` streams.
 
 roofline.achieved = algorithmic bytes per launch (16 524 B per row) divided by
@@ -129,16 +129,16 @@ def traffic_probe(pool, g, n):
     log(f"traffic probe: 1 copy of {nbytes} B, {n} launches of {g} C3 batches")
 
 
-def counter_probe(name, pool):
+def counter_probe(name, pool, g_head):
     """For rocprofv3 --pmc runs: launches of one workload only, each followed by
     a synchronisation, so every dispatch in the profile is that workload's.
     c1: 200 single C1 rows; c3one: 50 one-batch C3 launches; c3: 20 headline
-    launches; c4 / c5: 20 launches of C4 / C5."""
+    launches (g_head batches each); c4 / c5: 20 launches of C4 / C5."""
     import d3s
     import d3s_workloads as W
     import hiprt
     if name in ("c3", "c3one"):
-        g = 128 if name == "c3" else 1
+        g = g_head if name == "c3" else 1
         ids = hiprt.DeviceBuffer(4 * ROWS * g)
         for i in range(20 if name == "c3" else 50):
             assert pool.launch((i % (pool.n // g)) * g, g, ids, None) == 0
@@ -463,13 +463,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20480, help="C3 batches timed")
     ap.add_argument("--warmup", type=int, default=8192, help="C3 batches before timing (clocks settle)")
-    ap.add_argument("--batches-per-launch", type=int, default=128,
+    ap.add_argument("--batches-per-launch", type=int, default=512,
                     help="C3 batches one d3s_sample call carries in the headline figure")
     ap.add_argument("--headline-streams", type=int, default=3,
                     help="streams the headline's launches take in turn (launches overlap)")
     ap.add_argument("--streams", type=int, default=4,
                     help="streams for the one-batch-per-launch figure beside the headline")
-    ap.add_argument("--pool-batches", type=int, default=256)
+    ap.add_argument("--pool-batches", type=int, default=512)
     ap.add_argument("--single-rows", type=int, default=10000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -502,7 +502,7 @@ def main():
         traffic_probe(pool, G, args.traffic_probe)
         return
     if args.counter_probe:
-        counter_probe(args.counter_probe, pool)
+        counter_probe(args.counter_probe, pool, G)
         return
     # the dominant kernel alone: G batches per launch, back to back on one
     # stream, HIP events on that stream (the roofline's launch duration)

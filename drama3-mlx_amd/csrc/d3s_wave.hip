@@ -87,18 +87,23 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
  * and s_r = f_0 + ... + f_r (the reference kernel's sequential cumulative,
  * src/sampling.c:126-127, and its kept sum, :129-131, whose value at the cut
  * is s_{cut-1}).  One lane runs both chains side by side over the terms in
- * LDS and writes each prefix back in place; every lane then reads its own. */
+ * LDS, four at a time, and writes each prefix back in place; every lane then
+ * reads its own.  The chains stop after the group in which c passes `stop`:
+ * every later rank has c_r > stop too (the terms are non-negative), so those
+ * lanes get c = +inf (and s = 0, never read: the cut lies before them). */
 __device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float *be, float *bf, float &c,
-                                                 float &s) {
+                                                 float &s, float stop = __builtin_inff()) {
   const int lane = lane_id();
   be[lane] = lane < k ? e : 0.0f;
   bf[lane] = lane < k ? f : 0.0f;
   wave_lds_sync();
+  int done = 0;
   if (lane == 0) {
     float4 *e4 = (float4 *)be;
     float4 *f4 = (float4 *)bf;
     float ce = 0.0f, cf = 0.0f;
-    for (int r4 = 0; r4 < (k + 3) / 4; r4++) {
+    int r4 = 0;
+    while (r4 < (k + 3) / 4) {
       float4 qe = e4[r4], qf = f4[r4];
       qe.x = ce = ce + qe.x;
       qf.x = cf = cf + qf.x;
@@ -110,11 +115,15 @@ __device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float 
       qf.w = cf = cf + qf.w;
       e4[r4] = qe;
       f4[r4] = qf;
+      r4++;
+      if (ce > stop) break;
     }
+    done = 4 * r4;
   }
+  done = (int)readlane_u((uint32_t)done, 0);
   wave_lds_sync();
-  c = be[lane];
-  s = bf[lane];
+  c = lane < done ? be[lane] : __builtin_inff();
+  s = lane < done ? bf[lane] : 0.0f;
   wave_lds_sync();
 }
 
@@ -460,8 +469,8 @@ struct WaveRow {
     /* the cumulative's terms: exact with the exact lse; with the fast lse only
      * the cut depends on them, so the hardware 2^x, inside the margin below */
     const float ec = exact ? d3s_expf_nonpos(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
-    float cc, sp;
-    wave_seq_prefix2(act ? ec : 0.0f, ep, k, S.buf, S.buf2, cc, sp);
+    /* the margin: |c'_r - c_r| <= B c'_r (0 with the exact lse) */
+    float B = 0.0f;
     if (!exact) {
       const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
       const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
@@ -469,8 +478,16 @@ struct WaveRow {
        * side, of its product with log2(e) and of log2(e) itself (|v - lse| <=
        * D), v_exp_f32's error and d3s_expf's */
       const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f;
-      const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-      exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
+      B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+    }
+    /* past stop, c - top_p > B c + 2^-60: certainly dropped, also with the
+     * exact lse, and never within the margin (for B < 1/2) */
+    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
+    float cc, sp;
+    wave_seq_prefix2(act ? ec : 0.0f, ep, k, S.buf, S.buf2, cc, sp, stop);
+    if (!exact) {
+      exact = __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) !=
+                  0ull ||
               (a.flags & FLAG_EXACT_LSE) != 0;
       if (exact && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
       if (exact) {
@@ -751,14 +768,17 @@ __device__ __forceinline__ void wide_finish(const SampleArgs &a, int row, WideLd
     const float v = key_x(key);
     const int idx = key_idx(key);
     const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
-    float cc, spp;
-    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp);
     const float D = lse - readlane_f(v, k - 1);
     const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
     const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f; /* as the wave kernel's */
     const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-    const bool exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
-                       (a.flags & FLAG_EXACT_LSE) != 0;
+    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
+    float cc, spp;
+    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp,
+                     stop);
+    const bool exact =
+        __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
+        (a.flags & FLAG_EXACT_LSE) != 0;
     if (exact) {
       if (lane == 0) {
         S.exact = 1u;
