@@ -9,8 +9,8 @@
  *  1. x = L / T exactly, classification, max m and the smallest finite x.
  *  2. The exact row sum: 2^-40 fixed-point images of d3s_expf(x - m)
  *     (lse = m + log S, src/sampling.c:37-38).
- *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 4096
- *     buckets of m - x, scaled to the row's range (a non-decreasing function
+ *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 8192
+ *     (rows above 5120 elements: 4096) buckets of m - x, scaled to the row's range (a non-decreasing function
  *     of -x, so buckets are ordered), then each element counts the larger
  *     keys of its own bucket.  The keys end in LDS in rank order, and from
  *     here on each thread owns consecutive ranks.
@@ -90,13 +90,24 @@ __device__ __forceinline__ uint64_t row16_sum_u64(uint64_t v) {
   return v + xch_u64<DPP_MIR>(v);
 }
 
+/* A workgroup reduction leaves the same value in every lane: taken from the
+ * first lane it is known to be wave-uniform, so the arithmetic that follows
+ * on it (the same in all 16 waves) runs on the scalar unit where it can. */
+__device__ __forceinline__ float uni_f(float v) {
+  return d3s_u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)d3s_f2u(v)));
+}
+__device__ __forceinline__ uint32_t uni_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ uint64_t uni_u64(uint64_t v) {
+  return ((uint64_t)uni_u32((uint32_t)(v >> 32)) << 32) | uni_u32((uint32_t)v);
+}
+
 __device__ __forceinline__ float block_max_f(float v, TRed &R) {
   v = wave_max_f(v);
   const int wid = threadIdx.x / WAVE;
   __syncthreads();
   if (lane_id() == 0) R.f[wid] = v;
   __syncthreads();
-  return row16_max_f(R.f[lane_id() & 15]);
+  return uni_f(row16_max_f(R.f[lane_id() & 15]));
 }
 
 /* the maxima of three values in one round */
@@ -112,9 +123,9 @@ __device__ __forceinline__ void block_max3_f(float &u, float &v, float &w, TRed 
     R.h[wid] = w;
   }
   __syncthreads();
-  u = row16_max_f(R.f[l16]);
-  v = row16_max_f(R.g[l16]);
-  w = row16_max_f(R.h[l16]);
+  u = uni_f(row16_max_f(R.f[l16]));
+  v = uni_f(row16_max_f(R.g[l16]));
+  w = uni_f(row16_max_f(R.h[l16]));
 }
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
@@ -123,7 +134,7 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
   __syncthreads();
   if (lane_id() == 0) R.s[wid] = w;
   __syncthreads();
-  return row16_sum_u64(R.s[lane_id() & 15]);
+  return uni_u64(row16_sum_u64(R.s[lane_id() & 15]));
 }
 
 __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
@@ -132,7 +143,7 @@ __device__ __forceinline__ int block_min_i32(int v, TRed &R) {
   __syncthreads();
   if (lane_id() == 0) R.r[wid] = v;
   __syncthreads();
-  return row16_min_i32(R.r[lane_id() & 15]);
+  return (int)uni_u32((uint32_t)row16_min_i32(R.r[lane_id() & 15]));
 }
 
 /* exclusive scan of per-thread counts in thread order; `tot` = the total */
@@ -143,7 +154,7 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, TRed &R, uin
   if (lane == WAVE - 1) R.a[wid] = incl;
   __syncthreads();
   const uint32_t x = R.a[lane & 15];
-  tot = row16_sum_u32(x);
+  tot = uni_u32(row16_sum_u32(x));
   return row16_sum_u32((lane & 15) < wid ? x : 0u) + incl - v;
 }
 
@@ -195,6 +206,8 @@ __device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
   D3S_ROW16_ARGMAX_STEP(DPP_HMIR)
   D3S_ROW16_ARGMAX_STEP(DPP_MIR)
 #undef D3S_ROW16_ARGMAX_STEP
+  s = uni_f(s);
+  r = (int)uni_u32((uint32_t)r);
 }
 
 template <int EPT, bool BF16>
