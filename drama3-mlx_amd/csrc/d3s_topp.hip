@@ -48,6 +48,7 @@ constexpr int DPP_X1 = 0xb1, DPP_X2 = 0x4e, DPP_HMIR = 0x141, DPP_MIR = 0x140;
 struct TRed {
   float f[TNW], g[TNW], h[TNW];
   uint64_t s[TNW];
+  uint64_t kept; /* the kept ranks' fixed-point sum */
   uint32_t a[TNW];
   int r[TNW];
 };
@@ -215,7 +216,8 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
     SampleArgs a) {
   constexpr int NBK = topp_buckets(EPT);
   extern __shared__ uint64_t keys[]; /* V slots: by bucket, then by rank */
-  __shared__ uint32_t bstart[NBK + 1]; /* bucket counts, first slots, then ends */
+  static_assert(NBK % (4 * TBLOCK) == 0, "whole 16-byte groups of buckets per thread");
+  __shared__ __align__(16) uint32_t bstart[NBK + 4]; /* bucket counts, first slots, then ends */
   __shared__ TRed R;
 
   const int row = (int)blockIdx.x;
@@ -276,7 +278,9 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
   const float dmax = m - xmin;
   const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
-  for (int b = tid; b < NBK + 1; b += TBLOCK) bstart[b] = 0u;
+#pragma unroll
+  for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
+  if (tid == 0) bstart[NBK] = 0u;
   __syncthreads();
   int bk[EPT];
 #pragma unroll
@@ -289,23 +293,30 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   }
   __syncthreads();
   {
-    /* exclusive scan of the NBK + 1 counts: thread t owns PER of them */
-    constexpr int PER = (NBK + 1 + TBLOCK - 1) / TBLOCK;
-    uint32_t c[PER], loc = 0u;
+    /* exclusive scan of the counts of the NBK finite buckets: thread t owns
+     * PER consecutive ones, read and written 4 at a time; the -inf bucket
+     * starts after them all */
+    constexpr int PER = NBK / TBLOCK;
+    uint4 c[PER / 4];
+    uint32_t loc = 0u;
 #pragma unroll
-    for (int q = 0; q < PER; q++) {
-      const int b = tid * PER + q;
-      c[q] = b <= NBK ? bstart[b] : 0u;
-      loc += c[q];
+    for (int q = 0; q < PER / 4; q++) {
+      c[q] = *(const uint4 *)&bstart[tid * PER + 4 * q];
+      loc += c[q].x + c[q].y + c[q].z + c[q].w;
     }
     uint32_t tot;
     uint32_t run = block_excl_scan_u32(loc, R, tot);
 #pragma unroll
-    for (int q = 0; q < PER; q++) {
-      const int b = tid * PER + q;
-      if (b <= NBK) bstart[b] = run;
-      run += c[q];
+    for (int q = 0; q < PER / 4; q++) {
+      uint4 o;
+      o.x = run;
+      o.y = o.x + c[q].x;
+      o.z = o.y + c[q].y;
+      o.w = o.z + c[q].z;
+      run = o.w + c[q].w;
+      *(uint4 *)&bstart[tid * PER + 4 * q] = o;
     }
+    if (tid == 0) bstart[NBK] = tot;
   }
   __syncthreads();
   uint64_t key[EPT];
@@ -451,18 +462,27 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
 
   /* ---- 5. the kept ranks r < cut (x_0 = m): their exact sum, probabilities
    * and the race.  Threads whose ranks all lie at or past the cut skip. */
+  /* Their exact sum is the prefix at the cut of the terms fix40(e_r) that
+   * the cut started from: the thread holding rank cut - 1 files it. */
+  {
+    const int last = cut - 1;
+    if (last >= r0 && last < r0 + RPT) {
+      uint64_t Q = Qp;
+#pragma unroll
+      for (int q = 0; q < EPT; q++)
+        if (r0 + q <= last) Q += d3s_fix40_unit(d3s_u2f((uint32_t)(keys[r0 + q] >> 32)));
+      R.kept = Q;
+    }
+  }
   float e[EPT];
-  uint64_t ks = 0;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
     const int r = r0 + q;
     e[q] = 0.0f;
-    if (q < RPT && r < cut) {
-      e[q] = d3s_u2f((uint32_t)(keys[r] >> 32)); /* exp(x_r - m), in [0, 1] */
-      ks += d3s_fix40_unit(e[q]);
-    }
+    if (q < RPT && r < cut) e[q] = d3s_u2f((uint32_t)(keys[r] >> 32)); /* exp(x_r - m), in [0, 1] */
   }
-  const float inv = 1.0f / d3s_fixsum_to_f32(block_sum_u64(ks, R));
+  __syncthreads();
+  const float inv = 1.0f / d3s_fixsum_to_f32(uni_u64(R.kept));
   /* Proven bounds of each score sc = max(p / noise, -1), noise = -log(1 - u):
    * RN(1 - u) lies within a relative 2^-24 of 1 - u and d3s_logf within one
    * ulp, so for u in [2^-24, 1)  u - 2^-24 <= noise <= (u / (1 - u) +
