@@ -56,14 +56,18 @@ __device__ __forceinline__ uint32_t wave_scan_add_u32(uint32_t v) {
 /* wave-uniform results (lane 63's scan value, read into a scalar) */
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return readlane_u(wave_scan_add_u32(v), 63); }
 
+/* the maximum over the wave of values that are never NaN (callers screen
+ * NaN first).  v_maximum3_f32 (IEEE maximum) needs no quieting of its
+ * operands, where fmaxf's minNum semantics make the compiler canonicalise
+ * both at every step. */
 __device__ __forceinline__ float wave_max_f(float v) {
   const float ninf = -__builtin_inff();
-  v = fmaxf(v, dpp_f<DPP_SHR1, 0xf>(ninf, v));
-  v = fmaxf(v, dpp_f<DPP_SHR2, 0xf>(ninf, v));
-  v = fmaxf(v, dpp_f<DPP_SHR4, 0xf>(ninf, v));
-  v = fmaxf(v, dpp_f<DPP_SHR8, 0xf>(ninf, v));
-  v = fmaxf(v, dpp_f<DPP_BCAST15, 0xa>(ninf, v));
-  v = fmaxf(v, dpp_f<DPP_BCAST31, 0xc>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_SHR1, 0xf>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_SHR2, 0xf>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_SHR4, 0xf>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_SHR8, 0xf>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_BCAST15, 0xa>(ninf, v));
+  v = __builtin_elementwise_maximum(v, dpp_f<DPP_BCAST31, 0xc>(ninf, v));
   return readlane_f(v, 63);
 }
 

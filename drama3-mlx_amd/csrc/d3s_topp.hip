@@ -66,11 +66,12 @@ __device__ __forceinline__ uint64_t xch_u64(uint64_t v) {
   return ((uint64_t)xch_u<C>((uint32_t)(v >> 32)) << 32) | xch_u<C>((uint32_t)v);
 }
 
+/* (never NaN, as in wave_max_f) */
 __device__ __forceinline__ float row16_max_f(float v) {
-  v = fmaxf(v, xch_f<DPP_X1>(v));
-  v = fmaxf(v, xch_f<DPP_X2>(v));
-  v = fmaxf(v, xch_f<DPP_HMIR>(v));
-  return fmaxf(v, xch_f<DPP_MIR>(v));
+  v = __builtin_elementwise_maximum(v, xch_f<DPP_X1>(v));
+  v = __builtin_elementwise_maximum(v, xch_f<DPP_X2>(v));
+  v = __builtin_elementwise_maximum(v, xch_f<DPP_HMIR>(v));
+  return __builtin_elementwise_maximum(v, xch_f<DPP_MIR>(v));
 }
 __device__ __forceinline__ int row16_min_i32(int v) {
   v = min(v, (int)xch_u<DPP_X1>((uint32_t)v));
