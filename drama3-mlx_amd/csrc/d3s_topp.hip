@@ -2,16 +2,17 @@
  * k_topp, for k > 64 (the reference's op-graph case, src/sampling.c:22-49,
  * with k up to V: "top-k disabled") on rows of at most 1024 * EPT elements.
  *
- * One 1024-thread workgroup per row, EPT elements per thread in registers
- * (element j * 1024 + t of thread t).  Every element needs its exact rank:
+ * One workgroup per row (512 threads for rows up to 4608 elements, 1024
+ * above), EPT elements per thread in registers (element j * TBLOCK + t of
+ * thread t).  Every element needs its exact rank:
  * the race draws u[rank] for every kept rank (src/sampling.c:45-47).
  *
  *  1. x = L / T exactly, classification, max m and the smallest finite x.
  *  2. The exact row sum: 2^-40 fixed-point images of d3s_expf(x - m)
  *     (lse = m + log S, src/sampling.c:37-38).
- *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 8192
- *     (rows above 5120 elements: 4096) buckets of m - x, scaled to the row's range (a non-decreasing function
- *     of -x, so buckets are ordered), then each element counts the larger
+ *  3. Ranks by (x desc, index asc) (:27-36): a counting sort over 4096 or
+ *     8192 buckets of m - x, scaled to the row's range (a non-decreasing
+ *     function of -x, so buckets are ordered), then each element counts the larger
  *     keys of its own bucket.  The keys end in LDS in rank order, and from
  *     here on each thread owns consecutive ranks.
  *  4. The cut: exact fixed-point prefix sums of d3s_expf(x_r - lse) over
@@ -30,11 +31,14 @@
 namespace d3s {
 namespace {
 
-constexpr int TBLOCK = 1024;
-constexpr int TNW = TBLOCK / WAVE;
-/* buckets of finite x (bucket NBK holds -inf): 8192 for rows of up to 5120
- * elements, whose LDS (keys and bucket bounds) then still fits twice per CU */
-constexpr int topp_buckets(int ept) { return ept <= 5 ? 8192 : 4096; }
+/* workgroups of 512 or 1024 threads; the reductions' LDS rows hold one
+ * entry per wave, 16 at most */
+constexpr int TNW = 16;
+/* buckets of finite x (bucket NBK holds -inf): 8192 for 1024-thread rows of
+ * up to 5120 elements, whose LDS (keys and bucket bounds) then still fits
+ * twice per CU; 4096 otherwise (512-thread rows of up to 4608 elements fit
+ * three times) */
+constexpr int topp_buckets(int max_v, int tb) { return max_v <= 5120 && tb == 1024 ? 8192 : 4096; }
 
 /* Workgroup reductions.  Each wave reduces on DPP and files its value in
  * LDS; after the barrier every lane reads entry lane % 16 and the sixteen
@@ -43,6 +47,8 @@ constexpr int topp_buckets(int ept) { return ept <= 5 ? 8192 : 4096; }
  * holds the result.  Each call opens with a barrier: the previous call's
  * entries may still be being read. */
 static_assert(TNW == 16, "one LDS entry per lane of a DPP row");
+/* (a workgroup of fewer than 16 waves fills the other entries with each
+ * reduction's identity once, at its start) */
 constexpr int DPP_X1 = 0xb1, DPP_X2 = 0x4e, DPP_HMIR = 0x141, DPP_MIR = 0x140;
 
 struct TRed {
@@ -94,7 +100,7 @@ __device__ __forceinline__ uint64_t row16_sum_u64(uint64_t v) {
 
 /* A workgroup reduction leaves the same value in every lane: taken from the
  * first lane it is known to be wave-uniform, so the arithmetic that follows
- * on it (the same in all 16 waves) runs on the scalar unit where it can. */
+ * on it (the same in every wave) runs on the scalar unit where it can. */
 __device__ __forceinline__ float uni_f(float v) {
   return d3s_u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)d3s_f2u(v)));
 }
@@ -212,10 +218,12 @@ __device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
   r = (int)uni_u32((uint32_t)r);
 }
 
-template <int EPT, bool BF16>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_topp(
+template <int EPT, bool BF16, int TBLOCK>
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(TBLOCK == 1024 ? 8 : 6))) void k_topp(
     SampleArgs a) {
-  constexpr int NBK = topp_buckets(EPT);
+  constexpr int NBK = topp_buckets(EPT * TBLOCK, TBLOCK);
+  constexpr int NW = TBLOCK / WAVE;
+  static_assert(NW <= TNW, "one reduction entry per wave");
   extern __shared__ uint64_t keys[]; /* V slots: by bucket, then by rank */
   static_assert(NBK % (4 * TBLOCK) == 0, "whole 16-byte groups of buckets per thread");
   __shared__ __align__(16) uint32_t bstart[NBK + 4]; /* bucket counts, first slots, then ends */
@@ -223,6 +231,13 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
 
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  if (NW < TNW && tid >= NW && tid < TNW) {
+    /* the reduction entries of absent waves: identities, never overwritten */
+    R.f[tid] = R.g[tid] = R.h[tid] = -__builtin_inff();
+    R.s[tid] = 0ull;
+    R.a[tid] = 0u;
+    R.r[tid] = 0x7fffffff;
+  }
   const int V = a.vocab, k = a.k;
   const RowP rp = row_params(a, row);
   const float T = rp.T;
@@ -558,21 +573,26 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(8))) voi
   }
 }
 
-template <int EPT, bool BF16>
+template <int EPT, bool BF16, int TBLOCK>
 bool try_topp(const SampleArgs &a, hipStream_t s) {
   if (a.vocab > EPT * TBLOCK) return false;
-  hipLaunchKernelGGL((k_topp<EPT, BF16>), dim3(a.n_rows), dim3(TBLOCK), (size_t)a.vocab * sizeof(uint64_t), s, a);
+  hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), (size_t)a.vocab * sizeof(uint64_t), s,
+                     a);
   return true;
 }
 
 }  // namespace
 
-int topp_max_vocab() { return 8 * TBLOCK; }
+int topp_max_vocab() { return 8 * 1024; }
 
 bool launch_topp(const SampleArgs &a, Dtype dt, hipStream_t s) {
   if (a.k <= KF) return false;
-  if (dt == DT_F32) return try_topp<5, false>(a, s) || try_topp<8, false>(a, s);
-  return try_topp<5, true>(a, s) || try_topp<8, true>(a, s);
+  /* rows up to 4608 elements: 512 threads, three workgroups per CU (the
+   * per-wave share of the reductions and the row's scalar arithmetic is
+   * paid by 8 waves instead of 16); longer rows: 1024 threads */
+  if (dt == DT_F32)
+    return try_topp<9, false, 512>(a, s) || try_topp<5, false, 1024>(a, s) || try_topp<8, false, 1024>(a, s);
+  return try_topp<9, true, 512>(a, s) || try_topp<5, true, 1024>(a, s) || try_topp<8, true, 1024>(a, s);
 }
 
 }  // namespace d3s
