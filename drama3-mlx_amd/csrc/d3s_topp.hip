@@ -39,6 +39,10 @@ constexpr int TNW = 16;
  * twice per CU; 4096 otherwise (512-thread rows of up to 4608 elements fit
  * three times) */
 constexpr int topp_buckets(int max_v, int tb) { return max_v <= 5120 && tb == 1024 ? 8192 : 4096; }
+/* waves per SIMD that the LDS allows, which sets the register budget:
+ * three 512-thread rows of up to 4608 elements per CU (6), two 1024-thread
+ * rows of up to 5120 (8), one of up to 8192 (4) */
+constexpr int topp_waves(int ept, int tb) { return tb == 512 ? 6 : (ept * tb <= 5120 ? 8 : 4); }
 
 /* Workgroup reductions.  Each wave reduces on DPP and files its value in
  * LDS; after the barrier every lane reads entry lane % 16 and the sixteen
@@ -219,7 +223,7 @@ __device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
 }
 
 template <int EPT, bool BF16, int TBLOCK>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(TBLOCK == 1024 ? 8 : 6))) void k_topp(
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
     SampleArgs a) {
   constexpr int NBK = topp_buckets(EPT * TBLOCK, TBLOCK);
   constexpr int NW = TBLOCK / WAVE;
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(TBLOCK =
   }
   __syncthreads();
   /* now bstart[b] is the end of bucket b, the start of bucket b + 1 */
-  /* the elements' buckets side by side, one member of each per step */
+  /* the elements' buckets side by side, two members of each per step */
   int rank[EPT];
   uint32_t b0[EPT], bn[EPT], most = 0u;
 #pragma unroll
@@ -355,10 +359,14 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(TBLOCK =
     rank[j] = in ? (int)b0[j] : 0x7fffffff;
     most = max(most, bn[j]);
   }
-  for (uint32_t q = 0; q < most; q++) {
+  for (uint32_t q = 0; q < most; q += 2u) {
 #pragma unroll
     for (int j = 0; j < EPT; j++)
-      if (q < bn[j]) rank[j] += keys[b0[j] + q] > key[j] ? 1 : 0;
+      if (q < bn[j]) {
+        const uint64_t k0 = keys[b0[j] + q];
+        const uint64_t k1 = keys[min(b0[j] + q + 1u, (uint32_t)V - 1u)];
+        rank[j] += (k0 > key[j] ? 1 : 0) + (q + 1u < bn[j] && k1 > key[j] ? 1 : 0);
+      }
   }
   /* From here on thread t owns the ranks [t RPT, t RPT + RPT): the uniforms
    * are read in rank order (the race needs them last), and LDS holds by rank
