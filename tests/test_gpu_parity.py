@@ -378,8 +378,8 @@ def test_wide_top_p_on_a_cumulative_boundary(gpu, oracle):
     assert got["counters"][gpu.COUNTER_EXACT_LSE] == 8
 
 
-@pytest.mark.parametrize("V,k", [(4097, 4097), (4608, 4608), (4609, 2000), (5120, 5120), (5121, 700),
-                                 (8192, 8192), (8193, 300), (300, 200)])
+@pytest.mark.parametrize("V,k", [(4097, 4097), (4097, 700), (1000, 65), (4608, 4608), (4609, 2000),
+                                 (5120, 5120), (5121, 700), (8192, 8192), (8193, 300), (300, 200)])
 def test_ranked_nucleus_rows(gpu, oracle, V, k):
     """k > 64 (the op graph's semantics: every rank exact, prefix sums exact):
     near-flat rows, per-row T and top_p, and the same bits as the generic
