@@ -234,7 +234,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   __shared__ TRed R;
 
   const int row = (int)blockIdx.x;
-  const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int tid = (int)threadIdx.x;
   if (NW < TNW && tid >= NW && tid < TNW) {
     /* the reduction entries of absent waves: identities, never overwritten */
     R.f[tid] = R.g[tid] = R.h[tid] = -__builtin_inff();
