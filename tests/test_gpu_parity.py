@@ -496,6 +496,50 @@ def test_banned_rows(gpu, oracle):
     compare(oracle, gpu, w3["logits"], u3, 0.7, 0.7, banned=ban, label="C3 banned argmax")
 
 
+# every route's register forms start and end at these lengths (and some
+# between): one wave, a workgroup, the nucleus kernel's three forms, generic
+ROUTE_EDGES = [1, 2, 17, 63, 64, 65, 300, 1000, 2047, 3841, 4096, 4097, 4352, 4353, 4608, 4609, 5120,
+               5121, 6141, 6142, 8185, 8186, 8192, 8193, 16381, 16382, 32761, 32762, 40000]
+
+
+@pytest.mark.parametrize("case", range(48))
+def test_random_configurations_across_routes(gpu, oracle, case):
+    """Seeded random configurations: a length at or near a route's edge, k up
+    to 64 or above, either dtype, per-row T and top_p (including T = 0 and
+    top_p >= 1), a padded row stride, banned indices, ties, masked stretches,
+    one all -inf row, peaks; every id, candidate and probability equal to the
+    oracle's."""
+    rng = np.random.default_rng([7919, case])
+    V = int(rng.choice(ROUTE_EDGES))
+    bf16 = bool(rng.integers(0, 2))
+    if V > 64 and rng.random() < 0.4:
+        k = int(rng.integers(65, min(V, 2000) + 1))
+    else:
+        k = int(rng.integers(1, min(V, 64) + 1))
+    N = int(rng.integers(1, 7))
+    stride = V + int(rng.integers(0, 8))
+    sigma = float(rng.choice([0.3, 2.5, 6.0]))
+    x = (rng.standard_normal((N, stride)) * sigma).astype(np.float32)
+    for r in range(N):
+        kind = rng.integers(0, 6)
+        if kind == 0:
+            x[r, rng.integers(0, V, 5)] += 8.0                  # peaks
+        elif kind == 1:
+            x[r] = np.round(x[r] * 2) / 2                        # many ties
+        elif kind == 2:
+            a = int(rng.integers(0, V))
+            x[r, a:a + V // 3] = -np.inf                         # a masked stretch
+        elif kind == 3 and N > 1:
+            x[r, :V] = -np.inf                                   # all masked
+    T = rng.choice(np.float32([0.0, 0.3, 0.7, 1.0, 2.5]), N).astype(np.float32)
+    top_p = rng.choice(np.float32([0.1, 0.7, 0.95, 1.0, 1.5]), N).astype(np.float32)
+    ban = np.where(rng.random(N) < 0.5, rng.integers(0, V, N), -1).astype(np.int32)
+    u = oracle.uniform(int(rng.integers(0, 1 << 30)), 0, N, k)
+    xs = W.f32_to_bf16_bits(x) if bf16 else x
+    compare(oracle, gpu, xs, u, T, top_p, banned=ban, row_stride=stride, vocab=V,
+            label=f"random case {case}: V={V} k={k} N={N} stride={stride} bf16={bf16} sigma={sigma}")
+
+
 def test_shim_entry_points(gpu, oracle):
     """d3_sample (src/testapi.c:155-166): m_seed, device draws, sample."""
     w = W.make("C3", rows=32, seed=6, uniforms=False)
