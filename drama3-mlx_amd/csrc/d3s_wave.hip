@@ -882,12 +882,13 @@ void k_wide(SampleArgs a) {
     return;
   }
 
-  /* ---- tau: the k-th largest of the 1024 lane maxima to 24 bits of its
-   * order key (a lower bound: at least k elements reach it) */
+  /* ---- tau: the k-th largest of the 1024 lane maxima to 16 bits of its
+   * order key (a lower bound: at least k elements reach it; the candidates
+   * are ranked exactly after, so a coarser bound only admits a few more) */
   const uint32_t lkey = d3s_ordkey(lm);
   uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)k;
 #pragma unroll
-  for (int pass = 0; pass < 3; pass++) {
+  for (int pass = 0; pass < 2; pass++) {
     const int shift = 24 - 8 * pass;
     if (threadIdx.x < NB) S.hist[threadIdx.x] = 0u;
     __syncthreads();
