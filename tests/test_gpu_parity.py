@@ -540,6 +540,38 @@ def test_random_configurations_across_routes(gpu, oracle, case):
             label=f"random case {case}: V={V} k={k} N={N} stride={stride} bf16={bf16} sigma={sigma}")
 
 
+def test_calls_on_several_streams_at_once(gpu, oracle):
+    """d3s_sample is reentrant across streams: four streams each take another
+    route (a 512-row batch for the wave kernel, wide bf16 rows, k = V rows
+    for the nucleus kernel, one row), their launches issued in turn three
+    times with no wait between the streams, each writing its own ids; after
+    one device-wide wait every stream's ids equal the oracle's."""
+    import hiprt
+    rng = np.random.default_rng(77)
+    cases = [(4097, 30, 512, False), (151936, 30, 8, True), (4097, 4097, 64, False), (4097, 30, 1, False)]
+    streams, runs = [], []
+    try:
+        for V, k, N, bf16 in cases:
+            x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+            xs = W.f32_to_bf16_bits(x) if bf16 else x
+            u = oracle.uniform(77, V, N, k)
+            runs.append((xs, u, N, V, k, bf16, hiprt.to_device(xs), hiprt.to_device(u), hiprt.DeviceBuffer(4 * N)))
+            streams.append(hiprt.Stream())
+        hiprt.synchronize()
+        banner("four routes on four streams, three rounds")
+        for _ in range(3):
+            for s, (xs, u, N, V, k, bf16, bl, bu, bi) in zip(streams, runs):
+                dt = gpu.DTYPE_BF16 if bf16 else gpu.DTYPE_F32
+                assert gpu.sample_raw(bl.ptr, dt, N, V, V, bu.ptr, k, 0.8, 0.9, None, bi.ptr, stream=s.ptr) == 0
+        hiprt.synchronize()
+        for xs, u, N, V, k, bf16, bl, bu, bi in runs:
+            exp = oracle.sample(xs, u, 0.8, 0.9, n_threads=8)
+            assert np.array_equal(bi.download((N,), np.int32), exp["ids"]), (V, k, N, bf16)
+    finally:
+        for s in streams:
+            s.destroy()
+
+
 def test_shim_entry_points(gpu, oracle):
     """d3_sample (src/testapi.c:155-166): m_seed, device draws, sample."""
     w = W.make("C3", rows=32, seed=6, uniforms=False)
