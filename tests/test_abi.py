@@ -4,6 +4,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -76,3 +77,15 @@ def test_argument_validation_without_device(lib):
     big = dict(base, vocab=20000, row_stride=20000, k=16385)
     assert d3s.sample_raw(**big) == -2
     assert d3s.sample_raw(**{**base, "n_rows": 0}) == 0  # nothing to do, nothing launched
+
+
+def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
+    """No CPU fallback: with the built library absent, the first call into the
+    product raises instead of computing anything."""
+    import d3s
+    monkeypatch.setattr(d3s, "LIB_PATH", str(tmp_path / "libd3sampler.so"))
+    monkeypatch.setattr(d3s, "_lib", None)
+    with pytest.raises(RuntimeError, match="no fallback"):
+        d3s.lib()
+    with pytest.raises(RuntimeError, match="no fallback"):
+        d3s.sample(np.zeros((1, 8), np.float32), np.zeros((1, 2), np.float32), 1.0, 0.9)
