@@ -4,7 +4,9 @@ Headline (`value`): sampled rows/s on C3, the batched backbone head
 (fp32 [256, 4097], per-row T/top_p, k = 30) in steady state: multi-batch
 launches, `--batches-per-launch` batches of 256 rows per d3s_sample call
 (default 512: 131 072 rows), taken in turn by `--headline-streams` streams
-(default 3), so that one launch's last waves overlap the next one's first, over
+(default 3), so that one launch's last waves overlap the next one's first.
+A step is one such launch: `--warmup` untimed launches, then `--steps` timed
+ones (ms_per_step is per launch).  The launches cycle over
 a pool of `--pool-batches` batches in device memory (default 512 batches,
 2.2 GB, over eight times the 256 MB Infinity Cache, so every launch reads HBM;
 16 distinct generated contents, every batch with its own uniforms).  Beside it: one batch
@@ -17,10 +19,12 @@ roofline.whole_job is the headline's rate in the same units.
 cpu_baseline = the C oracle (the port of the
 reference semantics; the reference's own CPU path needs mlx-c, absent here)
 on a bounded sample of the same workload, all host cores.
-Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), launch
-times of C2, C4 and C5 at their own shapes, the fused repetition-aware draw
-against its two separate launches, and the backbone head's gemv and its sample
-as two launches and as one HIP graph (`other_configs`).
+Also reported: p50 / p90 of single-row C1 launches ([1, 4097] fp32), from
+Python and from a C caller (drama3-mlx_amd/d3s_latency); launch times of C2,
+C4 and C5 at their own shapes, the fused repetition-aware draw against its two
+separate launches, the backbone head's gemv and its sample as two launches and
+as one HIP graph, one decode frame's sampler launches and the reference's
+"samplers (11)" micro-benchmark (`other_configs`).
 """
 import argparse
 import json
@@ -76,18 +80,20 @@ class Pool:
                               ("ptr", self.top_p.ptr + r0 * 4), None, ids.ptr, stream=stream)
 
 
-def time_batches(pool, batches, warmup, g, n_streams):
-    """`batches` batches, g per launch, round robin over n_streams streams;
-    returns (device ms between the first and last event, host wall s)."""
+def time_launches(pool, launches, warmup, g, n_streams):
+    """`warmup` untimed launches, then `launches` timed launches of g batches
+    each, round robin over n_streams streams, between a start event on the
+    first stream (the others wait on it) and a stop event after every
+    stream's last launch; returns (device ms between the events, host wall s,
+    launches timed)."""
     import hiprt
     streams = [hiprt.Stream() for _ in range(n_streams)]
     ids = [hiprt.DeviceBuffer(4 * ROWS * g) for _ in range(n_streams)]
     windows = pool.n // g
-    for i in range(max(1, warmup // g)):
+    for i in range(warmup):
         s = i % n_streams
         assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
     hiprt.synchronize()
-    launches = max(1, batches // g)
     start, stop = hiprt.Event(), hiprt.Event()
     joins = [hiprt.Event() for _ in streams[1:]]
     t0 = time.perf_counter()
@@ -96,7 +102,7 @@ def time_batches(pool, batches, warmup, g, n_streams):
         st.wait(start)
     for i in range(launches):
         s = i % n_streams
-        assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
+        assert pool.launch(((warmup + i) % windows) * g, g, ids[s], streams[s].ptr) == 0
     for st, ev in zip(streams[1:], joins):
         ev.record(st)
         streams[0].wait(ev)
@@ -427,12 +433,131 @@ def head_latency(reps):
     return res
 
 
+def frame_latency(reps):
+    """The sampler work of one decode frame (src/tower.c:420-446), on one
+    stream: the main token's repetition-aware draw on the backbone head's bf16
+    [1, 4097] row (one d3s_sample_ras launch holding both draws), then the nine
+    codebook heads' bf16 [1, 4096] draws, one launch each (each head's logits
+    follow from the code before it, so the tower cannot batch them).  Beside
+    it, the reference's own sampler micro-benchmark (tools/bench.c:287-328,
+    "samplers (11)"): eleven sample_top_k_top_p calls on fp32 [1, 4097]
+    uniform(0, 1) logits with T 1.0, top_k 30, top_p 0.9 (bench.c:313), here
+    eleven pairs of d3s_uniform_fill and d3s_sample.  p50 / p90 of events
+    around each frame over `reps` frames, and the host wall time per frame."""
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    L = d3s.lib()
+    rng = np.random.default_rng(31)
+    head = W.f32_to_bf16_bits((rng.standard_normal((64, V)) * 2.5).astype(np.float32))
+    books = W.make("C2", rows=9 * 8, seed=31, uniforms=False)["logits"]
+    dh, db = hiprt.to_device(head), hiprt.to_device(books)
+    u = hiprt.DeviceBuffer(4 * 64 * 11 * K)
+    assert L.d3s_uniform_fill(u.ptr, 64 * 11 * K, 31, 0, None) == 0
+    hist = hiprt.to_device(np.full(16, 151669, np.int32))
+    frame = hiprt.DeviceBuffer(4 * 11)
+    P = d3s.ras_params(temperature=0.7, top_p=0.7, top_k=K, eos_id=151645, semantic_start=151669,
+                       semantic_end=151669 + 4095, code_vocab=4096)
+    lg = hiprt.to_device(rng.random((1, V)).astype(np.float32))
+    u11 = hiprt.DeviceBuffer(4 * 11 * K)
+    ids11 = hiprt.DeviceBuffer(4 * 11)
+    s = hiprt.Stream()
+    a, b = hiprt.Event(), hiprt.Event()
+
+    def one_frame(i):
+        r = i % 64
+        ub = u.ptr + r * 11 * K * 4
+        assert d3s.sample_ras_raw(dh.ptr + r * V * 2, d3s.DTYPE_BF16, 1, V, V, ub, ub + K * 4, hist.ptr, 16, P,
+                                  frame.ptr, frame.ptr + 4, stream=s.ptr) == 0
+        for j in range(9):
+            row = db.ptr + ((r % 8) * 9 + j) * 4096 * 2
+            assert d3s.sample_raw(row, d3s.DTYPE_BF16, 1, 4096, 4096, ub + (2 + j) * K * 4, K, 0.7, 0.7, None,
+                                  frame.ptr + 4 * (2 + j), stream=s.ptr) == 0
+
+    def samplers11(i):
+        for j in range(11):
+            assert L.d3s_uniform_fill(u11.ptr + j * K * 4, K, 42, 11 * i + j, s.ptr) == 0
+            assert d3s.sample_raw(lg.ptr, d3s.DTYPE_F32, 1, V, V, u11.ptr + j * K * 4, K, 1.0, 0.9, None,
+                                  ids11.ptr + 4 * j, stream=s.ptr) == 0
+
+    out = {}
+    for name, fn in (("frame", one_frame), ("samplers_11", samplers11)):
+        ev, wall = [], []
+        for i in range(reps + 20):
+            t0 = time.perf_counter()
+            a.record(s)
+            fn(i)
+            b.record(s)
+            b.synchronize()
+            t1 = time.perf_counter()
+            if i >= 20:
+                ev.append(a.elapsed_ms(b) * 1e3)
+                wall.append((t1 - t0) * 1e6)
+        out[name] = {"p50_us": float(np.median(ev)), "p90_us": float(np.percentile(ev, 90)),
+                     "host_p50_us": float(np.median(wall)), "frames": reps}
+    out["frame"]["launches"] = 10
+    out["frame"]["what"] = ("d3s_sample_ras on bf16 [1,4097] (both draws) + 9 d3s_sample on bf16 [1,4096], "
+                            "one stream (src/tower.c:420-446)")
+    out["samplers_11"]["launches"] = 22
+    out["samplers_11"]["what"] = ("11 x (d3s_uniform_fill + d3s_sample) on fp32 [1,4097] uniform(0,1) logits, "
+                                  "T 1.0, top_k 30, top_p 0.9 (tools/bench.c:313)")
+    s.destroy()
+    log(f"frame (RAS + 9 codebooks, 10 launches): p50 {out['frame']['p50_us']:.2f} us; "
+        f"samplers (11) as tools/bench.c: p50 {out['samplers_11']['p50_us']:.2f} us")
+    return out
+
+
+def c_caller_latency(calls):
+    """C1 one-row calls timed by drama3-mlx_amd/d3s_latency, a C program
+    linked to the library (what a C caller such as tower.c sees, without
+    Python's call overhead): host call-to-synchronize p50 and event p50.  Run
+    in a child process before this process touches the GPU."""
+    import subprocess
+    import tempfile
+    import d3s_workloads as W
+    exe = os.path.join(ROOT, "drama3-mlx_amd", "d3s_latency")
+    if not os.path.exists(exe):
+        return None
+    w = W.make("C1", rows=256, seed=42, uniforms=True)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "c1.bin")
+        with open(path, "wb") as f:
+            f.write(np.ascontiguousarray(w["logits"], np.float32).tobytes())
+            f.write(np.ascontiguousarray(w["u"], np.float32).tobytes())
+        r = subprocess.run([exe, path, "256", str(V), str(K), str(calls), "0.7", "0.7"], capture_output=True,
+                           text=True, timeout=300)
+    if r.returncode != 0:
+        log(f"d3s_latency failed: {r.stderr.strip()[-300:]}")
+        return None
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"C caller, C1 one row: host p50 {res['host_p50_us']:.2f} us, event p50 {res['event_p50_us']:.2f} us")
+    return res
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(seconds):
     """The oracle (ids only: no probabilities or float64 boundary shadow) on
     all host cores over a bounded sample of C3 rows, and its per-row time on
     one thread for C1 rows (a 2000-row call, so the per-call cost is spread)."""
+    import tempfile
     import d3s_oracle
     import d3s_workloads as W
+    tmp = tempfile.mkdtemp()
+    native = d3s_oracle.build_native(tmp)
+    if native:
+        d3s_oracle.use_library(native)
+        flags = "-O3 -march=native, built on this host"
+    else:
+        flags = "-O2 -march=x86-64-v3 (no C compiler on this host)"
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     w = W.make("C3", rows=ROWS, seed=7, uniforms=False)
     u = d3s_oracle.uniform(42, 0, ROWS, K)
@@ -454,15 +579,16 @@ def cpu_baseline(seconds):
     c1_us = (time.perf_counter() - t0) / 2000 * 1e6
     return dict(value=n * ROWS / dt, unit="rows/s", cores=int(threads), kind="port",
                 sample=f"{n} batches x {ROWS} rows of C3 (fp32 [256,4097], k=30), C oracle "
-                       f"(-O2 -march=x86-64-v3, OpenMP over rows, ids only) on {threads} threads, {dt:.1f} s",
-                c1_row_us_1_thread=c1_us)
+                       f"({flags}, OpenMP over rows, ids only) on {threads} threads, {dt:.1f} s",
+                cpu_model=cpu_model(), c1_row_us_1_thread=c1_us)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20480, help="C3 batches timed")
-    ap.add_argument("--warmup", type=int, default=8192, help="C3 batches before timing (clocks settle)")
+    ap.add_argument("--steps", type=int, default=40,
+                    help="timed launches, each of --batches-per-launch C3 batches")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed launches before (clocks settle)")
     ap.add_argument("--batches-per-launch", type=int, default=512,
                     help="C3 batches one d3s_sample call carries in the headline figure")
     ap.add_argument("--headline-streams", type=int, default=3,
@@ -484,6 +610,10 @@ def main():
               "(rows are independent: N GPUs would each run this kernel on N/G rows)",
               file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("bench.py: --steps must be at least 1 and --warmup at least 0")
+    # the C caller's figure first, in a child process, before this one starts HIP
+    c_lat = c_caller_latency(10000) if args.single_rows else None
     import hiprt
     if hiprt.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -507,25 +637,26 @@ def main():
     # the dominant kernel alone: G batches per launch, back to back on one
     # stream, HIP events on that stream (the roofline's launch duration)
     bytes_per_launch = G * ROWS * BYTES_PER_ROW
-    ms_k, _, lk = time_batches(pool, args.steps, args.warmup, G, 1)
+    ms_k, _, lk = time_launches(pool, args.steps, args.warmup, G, 1)
     kmean = ms_k * 1e3 / lk
     achieved = bytes_per_launch / (kmean * 1e-6) / 1e9
-    log(f"one stream: {lk} launches of {G} batches, {kmean:.2f} us per launch -> {achieved:.0f} GB/s")
+    log(f"one stream: {lk} timed launches of {G} batches after {args.warmup} untimed, {kmean:.2f} us per "
+        f"launch -> {achieved:.0f} GB/s")
     # headline: the same launches taken in turn by S streams, so that one
     # launch's last waves overlap the next launch's first
     S = args.headline_streams
-    ms, wall, launches = time_batches(pool, args.steps, args.warmup, G, S)
+    ms, wall, launches = time_launches(pool, args.steps, args.warmup, G, S)
     batches = launches * G
     value = batches * ROWS / (ms * 1e-3)
     job_gbs = value * BYTES_PER_ROW / 1e9
-    log(f"steady state: {batches} batches in {launches} launches of {G} over {S} streams in {ms:.2f} ms: "
-        f"{value:.3e} rows/s -> {job_gbs:.0f} GB/s (host wall {wall:.3f} s)")
-    # one batch per launch, one stream and several
-    n1 = min(args.steps, 5000)
-    ms1, _, l1 = time_batches(pool, n1, 100, 1, 1)
+    log(f"steady state: {launches} timed launches of {G} batches ({batches} batches) over {S} streams in "
+        f"{ms:.2f} ms: {value:.3e} rows/s -> {job_gbs:.0f} GB/s (host wall {wall:.3f} s)")
+    # one batch (256 rows) per launch, one stream and several
+    n1 = 5000
+    ms1, _, l1 = time_launches(pool, n1, 100, 1, 1)
     single = l1 * ROWS / (ms1 * 1e-3)
     log(f"one batch per launch, one stream: {single:.3e} rows/s ({ms1 * 1e3 / l1:.2f} us/launch)")
-    msS, _, lS = time_batches(pool, n1, 100, 1, args.streams)
+    msS, _, lS = time_launches(pool, n1, 100, 1, args.streams)
     multi = lS * ROWS / (msS * 1e-3)
     log(f"one batch per launch, {args.streams} streams: {multi:.3e} rows/s")
     floor_us = launch_floor(500)
@@ -539,6 +670,7 @@ def main():
         others = other_configs(200)
         others["RAS"] = ras_latency(500)
         others["head"] = head_latency(300)
+        others.update(frame_latency(300))
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_k_wave_C3.json")
     if os.path.exists(tpath):
@@ -556,9 +688,9 @@ def main():
         "value": value,
         "unit": "rows/s",
         "n_gpus": 1,
-        "steps": batches,
+        "steps": launches,
         "warmup": args.warmup,
-        "ms_per_step": ms / batches,
+        "ms_per_step": ms / launches,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -568,7 +700,7 @@ def main():
                                "peaks, rows 0-127 T 0.7/top_p 0.7, rows 128-255 T 1.0/top_p 0.9, "
                                "top_k 30, per-row Philox uniforms",
                    "global_batch": ROWS, "vocab": V, "k": K, "pool_MB": round(pool_mb),
-                   "step": "one batch of 256 rows",
+                   "step": f"one d3s_sample launch of {G} batches of 256 rows ({G * ROWS} rows)",
                    "steady_state": f"multi-batch launches: {G} batches per d3s_sample call, "
                                    f"taken in turn by {S} streams",
                    "batches_per_launch": G, "streams": S},
@@ -584,6 +716,7 @@ def main():
         "p50_us_single_row": lat["p50_us"] if lat else None,
         "event_floor_us": floor_us,
         "single_row": lat,
+        "single_row_c_caller": c_lat,
         "other_configs": others,
     }
     print(json.dumps(out), flush=True)

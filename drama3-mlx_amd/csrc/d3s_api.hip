@@ -1,28 +1,75 @@
-/* C-ABI of the MI355X token sampler (include/d3s_sampler.h): argument checks
- * and routing between the fused and the streaming kernel.
+/* C-ABI of the MI355X token sampler (include/d3s_sampler.h): argument checks,
+ * the choice of definition and the routing between kernels.
  *
- * Routing mirrors sample_with_noise (src/sampling.c:194-203): the one-kernel
- * path when k <= 64 and the row fits it, unless D3_NO_FUSED_SAMPLER is set in
- * the environment (read once per process) or D3S_FLAG_GENERIC is passed.  The
- * reference also requires k < V for its kernel; here both kernels compute the
- * same definition, so k == V <= 64 stays on the fused kernel. */
+ * The definition mirrors sample_with_noise (src/sampling.c:194-203): the
+ * reference kernel's sequential sums when k <= 64, k < V, V <= 65536 and
+ * D3_NO_FUSED_SAMPLER is unset (the environment is read at every call, as the
+ * reference's getenv is), else the op graph's exact prefix sums.  Either
+ * definition runs on whichever kernel holds the row; every kernel computes
+ * both bit for bit. */
 #include <stdlib.h>
 #include <string.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/d3s_sampler.h"
 #include "d3s_internal.h"
 
-namespace {
+namespace d3s {
 
-bool env_no_fused() {
-  static const bool v = [] {
-    const char *e = getenv("D3_NO_FUSED_SAMPLER");
-    return e != nullptr && *e != '\0';
-  }();
-  return v;
+namespace {
+struct Block {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, uintptr_t>, Block> g_ws; /* (device, stream) -> block */
+}  // namespace
+
+void *stream_workspace(hipStream_t s, size_t bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  Block &b = g_ws[{dev, (uintptr_t)s}];
+  if (b.bytes >= bytes) return b.ptr;
+  const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1); /* whole MiB */
+  if (b.ptr) {
+    (void)hipFree(b.ptr); /* waits for the device: no kernel still uses the block */
+    b = Block{};
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) return nullptr;
+  if (hipMemset(p, 0, want) != hipSuccess) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  b.ptr = p;
+  b.bytes = want;
+  return p;
 }
 
+}  // namespace d3s
+
+namespace {
+
+/* set, with any value, as src/sampling.c:197 tests it */
+bool env_no_fused() { return getenv("D3_NO_FUSED_SAMPLER") != nullptr; }
+
 int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
+
+/* the first kernel that holds the row: one wave, the fused workgroup (kernel
+ * order only), the wide workgroup, the nucleus kernel, else the streaming one */
+int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s) {
+  const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
+  if (!generic && d3s::launch_wave(a, dt, s)) return launched();
+  if (!generic && !a.opgraph && d3s::launch_fused(a, dt, s)) return launched();
+  if (!generic && d3s::launch_wide(a, dt, s)) return launched();
+  if (!generic && d3s::launch_topp(a, dt, s)) return launched();
+  if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
+  return launched();
+}
 
 }  // namespace
 
@@ -42,7 +89,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   if (!logits || !u || !ids) return D3S_ERR_ARG;
   /* rows are addressed in whole elements */
   if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
-  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT)) != 0u)
+  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT | D3S_FLAG_OP_GRAPH)) != 0u)
     return D3S_ERR_ARG;
   d3s::SampleArgs a;
   a.logits = logits;
@@ -61,15 +108,9 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   a.cand = cand;
   a.counters = counters;
   a.flags = flags;
+  a.opgraph = d3s::op_graph_order(a.vocab, k, (flags & D3S_FLAG_OP_GRAPH) || env_no_fused());
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
-  hipStream_t s = (hipStream_t)stream;
-  const bool generic = (flags & D3S_FLAG_GENERIC) || env_no_fused();
-  if (!generic && d3s::launch_wave(a, dt, s)) return launched();
-  if (!generic && d3s::launch_fused(a, dt, s)) return launched();
-  if (!generic && d3s::launch_wide(a, dt, s)) return launched();
-  if (!generic && d3s::launch_topp(a, dt, s)) return launched();
-  if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
-  return launched();
+  return sample_routed(a, dt, (hipStream_t)stream);
 }
 
 int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
@@ -102,8 +143,11 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
   a.cand = nullptr;
   a.counters = counters;
   a.flags = 0u;
+  const bool no_fused = env_no_fused();
+  a.opgraph = d3s::op_graph_order(a.vocab, a.k, no_fused);
   r.retry = a;
   r.retry.k = params->retry_top_k < vocab ? params->retry_top_k : (int)vocab;
+  r.retry.opgraph = d3s::op_graph_order(a.vocab, r.retry.k, no_fused);
   r.retry.u = u_retry;
   r.retry.temperature_scalar = params->retry_temperature;
   r.retry.top_p_scalar = params->retry_top_p;
@@ -117,7 +161,23 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
   r.main_tok = main_tok;
   r.code0 = code0;
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
-  if (!d3s::launch_ras(r, dt, (hipStream_t)stream)) return D3S_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  if (d3s::launch_ras(r, dt, s)) return launched();
+  /* rows the fused kernel does not hold (k above 64, or wider than one wave's
+   * registers): the two draws as routed launches, then the pick.  The first
+   * draw's indices go to first_idx or else main_tok (the pick reads each row's
+   * before it writes it); the retry's to retry_idx or else the workspace. */
+  if (r.first.k > d3s_max_k() || r.retry.k > d3s_max_k()) return D3S_ERR_UNSUPPORTED;
+  int32_t *fi = first_idx ? first_idx : main_tok;
+  int32_t *ri = retry_idx;
+  if (!ri) ri = (int32_t *)d3s::stream_workspace(s, (size_t)n_rows * sizeof(int32_t));
+  if (!ri) return D3S_ERR_NOMEM;
+  r.first.ids = fi;
+  r.retry.ids = ri;
+  int rc = sample_routed(r.first, dt, s);
+  if (rc == D3S_OK) rc = sample_routed(r.retry, dt, s);
+  if (rc != D3S_OK) return rc;
+  d3s::launch_ras_select(r, fi, ri, s);
   return launched();
 }
 

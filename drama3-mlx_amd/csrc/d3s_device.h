@@ -79,6 +79,27 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
   return ((uint64_t)hi << 24) + lo;
 }
 
+/* inclusive prefix sum over the wave of per-lane values below 2^40 (lane i
+ * gets lanes 0..i), exact: the low 24 bits and the rest scanned apart */
+__device__ __forceinline__ uint64_t wave_scan_u64(uint64_t v) {
+  const uint32_t lo = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t hi = wave_scan_add_u32((uint32_t)(v >> 24));
+  return ((uint64_t)hi << 24) + lo;
+}
+
+/* inclusive prefix sum over the wave in fp32 (a fixed tree order; its
+ * rounding is within the usual (n - 1) 2^-24 bound of any order for
+ * non-negative terms) */
+__device__ __forceinline__ float wave_scan_add_f32(float v) {
+  v = v + dpp_f<DPP_SHR1, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR2, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR4, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_SHR8, 0xf>(0.0f, v);
+  v = v + dpp_f<DPP_BCAST15, 0xa>(0.0f, v);
+  v = v + dpp_f<DPP_BCAST31, 0xc>(0.0f, v);
+  return v;
+}
+
 /* The best (score, rank) over the wave: the greatest score, ties to the
  * smaller rank (the reference's first maximum).  Wave-uniform result. */
 __device__ __forceinline__ void wave_argmax(float &s, int &r) {

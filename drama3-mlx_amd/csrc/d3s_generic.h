@@ -3,8 +3,8 @@
  * global memory for every pass (any V, k <= 16384): exact log-sum-exp
  * (src/sampling.c:81-89), an 8-bit radix select of the k-th rank over
  * order-preserving keys of x (:90-121), an LDS bitonic sort of the k selected,
- * then the reference kernel's tail for k <= 64 (:123-139) or exact prefix
- * sums over ranks for k > 64 (the op graph's cumsum and softmax, :39-44).
+ * then the reference kernel's tail (:123-139) or, in the op graph's order,
+ * exact prefix sums over ranks (its cumsum and softmax, :39-44).
  * Device code only; every translation unit gets its own copy. */
 #ifndef D3S_GENERIC_H
 #define D3S_GENERIC_H
@@ -208,7 +208,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
   }
 
   const float top_p = rp.top_p;
-  if (k <= KF) {
+  if (!a.opgraph) { /* the reference kernel's order (k <= 64 then) */
     if (wid == 0) {
       const uint64_t key = lane < k ? glist[lane] : 0ull;
       const float v = key_x(key);
@@ -220,7 +220,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
     return;
   }
 
-  /* ---- k > 64: exact prefix sums over ranks (the op graph's cumsum and
+  /* ---- the op graph's order: exact prefix sums over ranks (its cumsum and
    * softmax, src/sampling.c:39-44), each thread owning R consecutive ranks */
   const int R = (k + GBLOCK - 1) / GBLOCK;
   const int r0 = tid * R;

@@ -27,6 +27,11 @@ struct SampleArgs {
   int32_t *cand;            /* [n_rows, k] or null */
   uint32_t *counters;       /* [D3S_NUM_COUNTERS] or null */
   unsigned flags;
+  /* the op graph's order for the cumulative and the kept sum (exact prefix
+   * sums, src/sampling.c:22-49) instead of the reference kernel's sequential
+   * fp32 sums (:123-131): every call the reference does not send to its
+   * kernel (src/sampling.c:197) */
+  bool opgraph;
 };
 
 /* Repetition-aware sampling of the main token (src/tower.c:13-16,:405-433):
@@ -64,7 +69,15 @@ enum : unsigned {
   FLAG_GENERIC = 1u,
   FLAG_EXACT_LSE = 2u,
   FLAG_EXACT_SELECT = 4u,
+  FLAG_OP_GRAPH = 8u,
 };
+
+/* The reference sends a call to its one-kernel sampler iff k <= 64, k < V,
+ * V <= 65536 and D3_NO_FUSED_SAMPLER is unset (src/sampling.c:17,197); every
+ * other call takes its op graph.  Returns true for the op graph. */
+inline bool op_graph_order(int vocab, int k, bool forced) {
+  return forced || !(k <= 64 && k < vocab && vocab <= 1024 * 64);
+}
 
 enum Dtype { DT_F32 = 0, DT_BF16 = 1 };
 
@@ -75,6 +88,15 @@ int wave_max_vocab(Dtype dt);
 /* Launch the fused RAS kernel (both draws k <= 64, V within the wave kernel's
  * reach).  Returns false if no instantiation fits. */
 bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s);
+/* The pick of the main token alone, from the two draws' indices already in
+ * device memory (one wave per row). */
+void launch_ras_select(const RasArgs &r, const int32_t *first, const int32_t *retry, hipStream_t s);
+/* Device memory the library keeps for one stream of the current device, at
+ * least `bytes`, zero when first allocated (kernels that count in it leave it
+ * zero again).  The first call on a stream, or one that needs more, allocates
+ * (hipMalloc; the old block is freed, which waits for the device); later
+ * calls return the same block.  Null when the allocation fails. */
+void *stream_workspace(hipStream_t s, size_t bytes);
 /* Launch the head's gemv. */
 void launch_linear(const LinearArgs &la, hipStream_t s);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */

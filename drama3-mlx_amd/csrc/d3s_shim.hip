@@ -19,8 +19,9 @@
 
 struct d3s_array_s {
   void *data;
-  int dtype, rows, cols;
+  int dtype, rows, cols; /* storage: rows x cols elements, row_stride apart */
   int64_t row_stride;
+  int ndim;     /* 2, or 1 for sampled ids (shape [rows], as src/sampling.c:48,161) */
   bool owns;    /* hipFree on release */
   bool sampled; /* ids from the sampler: -1 marks a refused row */
 };
@@ -59,6 +60,7 @@ d3s_array new_device(int dtype, int rows, int cols) {
   a->rows = rows;
   a->cols = cols;
   a->row_stride = cols;
+  a->ndim = 2;
   a->owns = true;
   const size_t bytes = (size_t)rows * cols * elem_size(dtype);
   if (bytes) check(hipMalloc(&a->data, bytes), "hipMalloc");
@@ -100,6 +102,7 @@ d3s_array sample_with_noise(d3s_array logits, d3s_array u, float temperature, fl
   if (u->dtype != D3S_ARRAY_F32 || u->rows != logits->rows || u->row_stride != u->cols)
     die("sample_with_noise: u must be contiguous fp32 [%d, k]", logits->rows);
   d3s_array ids = new_device(D3S_ARRAY_I32, logits->rows, 1);
+  ids->ndim = 1; /* int32 [N] */
   ids->sampled = true;
   const int rc = d3s_sample(logits->data, logits->dtype == D3S_ARRAY_F32 ? D3S_DTYPE_F32 : D3S_DTYPE_BF16,
                             logits->rows, logits->cols, logits->row_stride, (const float *)u->data,
@@ -139,11 +142,20 @@ d3s_array d3s_array_from_device(void *ptr, int dtype, int rows, int cols, int64_
   a->rows = rows;
   a->cols = cols;
   a->row_stride = row_stride;
+  a->ndim = 2;
   return track(a);
 }
 
 int d3s_array_rows(d3s_array a) { return a->rows; }
 int d3s_array_cols(d3s_array a) { return a->cols; }
+int d3s_array_ndim(d3s_array a) { return a->ndim; }
+
+int d3s_array_dim(d3s_array a, int axis) {
+  if (axis < 0) axis += a->ndim; /* src/mlxu.c:848-851 */
+  if (axis < 0 || axis >= a->ndim) die("d3s_array_dim: axis out of range");
+  if (a->ndim == 1) return a->rows * a->cols;
+  return axis == 0 ? a->rows : a->cols;
+}
 int d3s_array_dtype(d3s_array a) { return a->dtype; }
 void *d3s_array_data(d3s_array a) { return a->data; }
 

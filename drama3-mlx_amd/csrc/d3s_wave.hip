@@ -127,18 +127,13 @@ __device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float 
   wave_lds_sync();
 }
 
-/* The exclusive top-p cut over c_r, the probabilities and the race
- * (src/sampling.c:128-139); lane r < k holds rank r's index, c_r, ep_r =
- * exp(x_r - x_0), the prefix s_r of ep and noise -log(1 - u_r). */
-__device__ __forceinline__ int wave_race_prefix(const SampleArgs &a, int row, int idx, float c, float ep,
-                                                float s, float noise, float top_p) {
+/* The race (src/sampling.c:132-139): lane r < k holds rank r's index, its
+ * post-filter probability p_r and noise -log(1 - u_r); the first maximum of
+ * p / noise wins (initial best -1).  Writes ids / probs / cand; returns the id. */
+__device__ __forceinline__ int wave_race_p(const SampleArgs &a, int row, int idx, float p, float noise) {
   const int lane = lane_id();
   const int k = a.k;
   const bool act = lane < k;
-  const uint64_t dm = __ballot(act && lane > 0 && c > top_p);
-  const int cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
-  const float inv = 1.0f / readlane_f(s, cut - 1);
-  const float p = (act && lane < cut) ? ep * inv : 0.0f;
   float sc = -1.0f;
   if (act) {
     const float score = p / noise;
@@ -153,6 +148,93 @@ __device__ __forceinline__ int wave_race_prefix(const SampleArgs &a, int row, in
     if (a.cand) a.cand[(size_t)row * k + lane] = idx;
   }
   return id;
+}
+
+/* wave_tail's answer when the cut needs the exact lse and the wave cannot
+ * compute it (the caller samples the row again by an exact procedure) */
+constexpr int NEED_EXACT = (int)0x80000000;
+
+/* The tail of one row on one wave (src/sampling.c:123-139, or in the op
+ * graph's order :39-48): lane r < k holds rank r's key (composite_key of x_r
+ * and its index), M = x_0 = max x, noise = -log(1 - u_r).  lse is exact when
+ * `exact`, else the fast one with relative error bound eps_s.
+ *
+ * The cut only depends on lse through c_r; the probabilities use exp(x - x_0).
+ * With the fast lse, |c'_r - c_r| <= c'_r (eps_e + (2k + 2) 2^-24) (+ (k + 2)
+ * 2^-40 in the op graph's order, whose exact prefixes truncate each term to
+ * 2^-40), eps_e bounding the relative change of a term exp(v - lse) between
+ * the two lse values; when some c'_r lies that close to top_p, exact_lse()
+ * gives the exact lse (NaN: the wave cannot, and NEED_EXACT is returned
+ * before anything is written).
+ *  - kernel order: c_r and the kept sum are left-to-right fp32 sums in rank
+ *    order, p_r = e_r (1 / s_{cut-1});
+ *  - op graph order: c_r = RN(sum_{j<=r} fix40(exp(x_j - lse)) 2^-40), the
+ *    kept sum the same of exp(x_j - x_0) over the kept ranks. */
+template <class ExactLse>
+__device__ __forceinline__ int wave_tail(const SampleArgs &a, int row, uint64_t key, float M, float lse,
+                                         bool exact, float eps_s, float noise, float top_p, float *buf,
+                                         float *buf2, ExactLse &&exact_lse) {
+  const int lane = lane_id();
+  const int k = a.k;
+  const bool act = lane < k;
+  const float v = key_x(key);
+  const int idx = key_idx(key);
+  const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
+  /* the cumulative's terms: exact with the exact lse; with the fast lse only
+   * the cut depends on them, so the hardware 2^x, inside the margin below */
+  const float ec = exact ? d3s_expf_nonpos(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
+  /* the margin: |c'_r - c_r| <= B c'_r + slack (0 with the exact lse) */
+  float B = 0.0f;
+  if (!exact) {
+    const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
+    const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
+    /* a term's relative change: lse's, the rounding of v - lse on either
+     * side, of its product with log2(e) and of log2(e) itself (|v - lse| <=
+     * D), v_exp_f32's error and d3s_expf's */
+    const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f;
+    B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+  }
+  int cut;
+  float inv;
+  if (!a.opgraph) {
+    /* past stop, c - top_p > B c + 2^-60: certainly dropped, also with the
+     * exact lse, and never within the margin (for B < 1/2) */
+    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
+    float cc, sp;
+    wave_seq_prefix2(act ? ec : 0.0f, ep, k, buf, buf2, cc, sp, stop);
+    if (!exact) {
+      exact = __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) !=
+                  0ull ||
+              (a.flags & FLAG_EXACT_LSE) != 0;
+      if (exact) {
+        if (lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+        const float lx = exact_lse();
+        if (d3s_isnan(lx)) return NEED_EXACT;
+        cc = wave_seq_cumsum(act ? d3s_expf_nonpos(v - lx) : 0.0f, k, buf);
+      }
+    }
+    const uint64_t dm = __ballot(act && lane > 0 && cc > top_p);
+    cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
+    inv = 1.0f / readlane_f(sp, cut - 1);
+  } else {
+    float cc = 0.0f;
+    if (!exact) {
+      cc = wave_scan_add_f32(act ? ec : 0.0f);
+      exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + (float)(k + 2) * 0x1p-40f) != 0ull ||
+              (a.flags & FLAG_EXACT_LSE) != 0;
+      if (exact) {
+        if (lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+        lse = exact_lse();
+        if (d3s_isnan(lse)) return NEED_EXACT;
+      }
+    }
+    if (exact) cc = d3s_fixsum_to_f32(wave_scan_u64(act ? d3s_fix40_exp(v - lse) : 0ull));
+    const uint64_t dm = __ballot(act && lane > 0 && cc > top_p);
+    cut = dm ? __builtin_ctzll(dm) : k;
+    inv = 1.0f / d3s_fixsum_to_f32(wave_sum_u64(act && lane < cut ? d3s_fix40_unit(ep) : 0ull));
+  }
+  const float p = (act && lane < cut) ? ep * inv : 0.0f;
+  return wave_race_p(a, row, idx, p, noise);
 }
 
 /* A refused row (id -1) or an all -inf row (id 0, ranks 0..k-1); one wave.
@@ -444,10 +526,8 @@ struct WaveRow {
 
   /* Rank the n >= k candidates in S.keys by key and run the tail (the
    * reference kernel's cumulative, cut, softmax and race, src/sampling.c:
-   * 123-139).  With the fast lse, |c'_r - c_r| <= c'_r * (eps_e + (2k + 2)
-   * 2^-24), eps_e bounding the relative change of a term exp(v - lse) between
-   * the two lse values; the exact row sum is computed when a cut could fall
-   * differently. */
+   * 123-139, or the op graph's, :39-48); the exact row sum is computed when
+   * the fast lse cannot settle the cut. */
   __device__ __forceinline__ int finish(int n, float M, float lse, bool exact, float eps_s, float noise) {
     if (lane == 0) S.keys[n] = 0ull; /* pad for the pair reads; below every key */
     wave_lds_sync();
@@ -461,41 +541,9 @@ struct WaveRow {
     }
     if (lane < n && rank < k) S.ranked[rank] = my;
     wave_lds_sync();
-    const bool act = lane < k;
-    const uint64_t key = act ? S.ranked[lane] : 0ull;
-    const float v = key_x(key);
-    const int idx = key_idx(key);
-    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
-    /* the cumulative's terms: exact with the exact lse; with the fast lse only
-     * the cut depends on them, so the hardware 2^x, inside the margin below */
-    const float ec = exact ? d3s_expf_nonpos(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
-    /* the margin: |c'_r - c_r| <= B c'_r (0 with the exact lse) */
-    float B = 0.0f;
-    if (!exact) {
-      const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
-      const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
-      /* a term's relative change: lse's, the rounding of v - lse on either
-       * side, of its product with log2(e) and of log2(e) itself (|v - lse| <=
-       * D), v_exp_f32's error and d3s_expf's */
-      const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f;
-      B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-    }
-    /* past stop, c - top_p > B c + 2^-60: certainly dropped, also with the
-     * exact lse, and never within the margin (for B < 1/2) */
-    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
-    float cc, sp;
-    wave_seq_prefix2(act ? ec : 0.0f, ep, k, S.buf, S.buf2, cc, sp, stop);
-    if (!exact) {
-      exact = __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) !=
-                  0ull ||
-              (a.flags & FLAG_EXACT_LSE) != 0;
-      if (exact && lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-      if (exact) {
-        const float lx = exact_lse<CPT, BF16>(ref(), M);
-        cc = wave_seq_cumsum(act ? d3s_expf_nonpos(v - lx) : 0.0f, k, S.buf);
-      }
-    }
-    return wave_race_prefix(a, row, idx, cc, ep, sp, noise, top_p);
+    const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
+    return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf, S.buf2,
+                     [&]() { return exact_lse<CPT, BF16>(ref(), M); });
   }
 
   /* every quantity per element from x = L / T, as the oracle (T not finite,
@@ -761,32 +809,13 @@ __device__ __forceinline__ void wide_finish(const SampleArgs &a, int row, WideLd
     if (rank < k) S.ranked[rank] = my;
   }
   __syncthreads();
-  /* ---- the tail on wave 0 (the wave kernel's, with its margin test) */
+  /* ---- the tail on wave 0 (the wave kernel's, with its margin test); a cut
+   * the fast lse cannot settle samples the row again by the generic procedure */
   if (wid == 0) {
-    const bool act = lane < k;
-    const uint64_t key = act ? S.ranked[lane] : 0ull;
-    const float v = key_x(key);
-    const int idx = key_idx(key);
-    const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
-    const float D = lse - readlane_f(v, k - 1);
-    const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
-    const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f; /* as the wave kernel's */
-    const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
-    float cc, spp;
-    wave_seq_prefix2(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f, ep, k, S.buf, S.buf2, cc, spp,
-                     stop);
-    const bool exact =
-        __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) != 0ull ||
-        (a.flags & FLAG_EXACT_LSE) != 0;
-    if (exact) {
-      if (lane == 0) {
-        S.exact = 1u;
-        if (a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-      }
-    } else {
-      wave_race_prefix(a, row, idx, cc, ep, spp, noise, top_p);
-    }
+    const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
+    const int id = wave_tail(a, row, key, M, lse, false, eps_s, noise, top_p, S.buf, S.buf2,
+                             []() { return __builtin_nanf(""); });
+    if (id == NEED_EXACT && lane == 0) S.exact = 1u;
   }
   __syncthreads();
   if (S.exact) generic_row<BF16>(a, row, kpow, glist);
@@ -1016,13 +1045,33 @@ void k_wide(SampleArgs a) {
 }
 
 
+/* The main token of one row from its two draws' indices, on one wave (lane
+ * h checks history entry h): candidate index i -> token (0 -> eos, i ->
+ * semantic_start + i - 1, src/tower.c:405-409); the retry's token replaces the
+ * first's when the first is a semantic token found among the row's history
+ * (:429-433); code0 = clip(main - semantic_start, 0, code_vocab - 1) (:434-435).
+ * A refused draw (-1: the row's logits give a NaN or +inf x) writes -1 to
+ * main_tok and code0, the signal a caller checks where the reference's
+ * generation loop dies on non-finite logits (src/generate.c:92,130). */
+__device__ __forceinline__ void ras_pick(const RasArgs &ra, int row, int id1, int id2) {
+  const int lane = lane_id();
+  const int32_t first_tok = id1 == 0 ? ra.eos_id : id1 + ra.semantic_start - 1;
+  const int32_t retry_tok = id2 == 0 ? ra.eos_id : id2 + ra.semantic_start - 1;
+  const bool seen = lane < ra.history_len && ra.history[(size_t)row * ra.history_len + lane] == first_tok;
+  const bool repeated = __ballot(seen) != 0ull && first_tok >= ra.semantic_start && first_tok <= ra.semantic_end;
+  const bool refused = id1 < 0 || id2 < 0;
+  const int32_t tok = refused ? -1 : repeated ? retry_tok : first_tok;
+  if (lane == 0) {
+    ra.main_tok[row] = tok;
+    if (ra.code0) ra.code0[row] = refused ? -1 : min(max(tok - ra.semantic_start, 0), ra.code_vocab - 1);
+  }
+}
+
 /* k_ras: the main token's two draws (src/tower.c:425-433) in one launch.  Two
  * waves of a workgroup take one row: the first samples it with the caller's
  * parameters, the second with the retry's, side by side (the second's loads
  * of the row meet the first's in L2, so HBM reads it once).  Then the first
- * wave picks: candidate index i -> token (0 -> eos, i -> semantic_start + i -
- * 1, src/tower.c:405-409); the retry's token replaces the first's when the
- * first is a semantic token found among the row's history (:429-432). */
+ * wave picks the main token (ras_pick). */
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
 void k_ras(RasArgs ra) {
@@ -1044,16 +1093,17 @@ void k_ras(RasArgs ra) {
   }
   __syncthreads();
   if (retry || row >= ra.first.n_rows) return;
-  const int id1 = drawn[wid], id2 = drawn[wid + 1];
-  const int32_t first_tok = id1 == 0 ? ra.eos_id : id1 + ra.semantic_start - 1;
-  const int32_t retry_tok = id2 == 0 ? ra.eos_id : id2 + ra.semantic_start - 1;
-  const bool seen = lane < ra.history_len && ra.history[(size_t)row * ra.history_len + lane] == first_tok;
-  const bool repeated = __ballot(seen) != 0ull && first_tok >= ra.semantic_start && first_tok <= ra.semantic_end;
-  const int32_t tok = repeated ? retry_tok : first_tok;
-  if (lane == 0) {
-    ra.main_tok[row] = tok;
-    if (ra.code0) ra.code0[row] = min(max(tok - ra.semantic_start, 0), ra.code_vocab - 1);
-  }
+  ras_pick(ra, row, drawn[wid], drawn[wid + 1]);
+}
+
+/* The pick alone, one wave per row, after the two draws ran as separate
+ * launches that wrote their indices to `first` and `retry` (rows the fused
+ * kernel does not hold: k above 64, or rows wider than one wave's registers). */
+__global__ __launch_bounds__(WAVE *WR) void k_ras_select(RasArgs ra, const int32_t *first, const int32_t *retry) {
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int row = (int)(blockIdx.x * WR) + wid;
+  if (row >= ra.first.n_rows) return;
+  ras_pick(ra, row, first[row], retry[row]);
 }
 
 template <int CPT, bool BF16>
@@ -1147,6 +1197,11 @@ bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s) {
            try_ras<17, false>(r, max_off, s) || try_ras<24, false>(r, max_off, s);
   return try_ras<4, true>(r, max_off, s) || try_ras<8, true>(r, max_off, s) ||
          try_ras<10, true>(r, max_off, s) || try_ras<16, true>(r, max_off, s);
+}
+
+void launch_ras_select(const RasArgs &r, const int32_t *first, const int32_t *retry, hipStream_t s) {
+  const unsigned blocks = (unsigned)((r.first.n_rows + WR - 1) / WR);
+  hipLaunchKernelGGL(k_ras_select, dim3(blocks), dim3(WAVE * WR), 0, s, r, first, retry);
 }
 
 void launch_linear(const LinearArgs &la, hipStream_t s) {

@@ -17,6 +17,7 @@ DTYPE_BF16 = 1
 FLAG_GENERIC = 1
 FLAG_EXACT_LSE = 2
 FLAG_EXACT_SELECT = 4
+FLAG_OP_GRAPH = 8
 COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
 NUM_COUNTERS = 4
 OK = 0
@@ -219,10 +220,12 @@ def sample_ras_raw(logits, dtype, n_rows, vocab, row_stride, u, u_retry, history
                                 main_tok, code0, first_idx, retry_idx, counters, stream)
 
 
-def sample_ras(logits, u, u_retry, params, history=None):
+def sample_ras(logits, u, u_retry, params, history=None, indices=True):
     """Host arrays in and out: logits float32 or uint16 (bf16 bits) [N, V];
     u [N, k], u_retry [N, k2]; history int32 [N, H] or None; params: dict of
-    d3s_ras_params' fields.  Returns dict(rc, main, code0, first, retry, counters)."""
+    d3s_ras_params' fields; indices: ask for the two draws' indices too.
+    Returns dict(rc, main, code0, first, retry, counters) (first / retry
+    only with indices)."""
     import hiprt
     logits = np.ascontiguousarray(logits)
     dtype = DTYPE_F32 if logits.dtype == np.float32 else DTYPE_BF16
@@ -241,12 +244,12 @@ def sample_ras(logits, u, u_retry, params, history=None):
         bufs["hist"] = hiprt.to_device(history)
         hist = bufs["hist"].ptr
     rc = sample_ras_raw(bufs["logits"].ptr, dtype, N, V, V, bufs["u"].ptr, bufs["u2"].ptr, hist, H, P,
-                        bufs["main"].ptr, bufs["code0"].ptr, bufs["first"].ptr, bufs["retry"].ptr,
-                        bufs["counters"].ptr)
+                        bufs["main"].ptr, bufs["code0"].ptr, bufs["first"].ptr if indices else None,
+                        bufs["retry"].ptr if indices else None, bufs["counters"].ptr)
     out = dict(rc=rc)
     if rc == OK:
         hiprt.synchronize()
-        for name in ("main", "code0", "first", "retry"):
+        for name in ("main", "code0", "first", "retry") if indices else ("main", "code0"):
             out[name] = bufs[name].download((N,), np.int32)
         out["counters"] = bufs["counters"].download((NUM_COUNTERS,), np.uint32)
     for b in bufs.values():

@@ -35,7 +35,8 @@ typedef struct d3s_array_s *d3s_array;
 #define D3S_ARRAY_I32 2   /* int32 */
 
 /* ---- sampling (src/model.h:169-176) ---- */
-/* One id per row of logits [N, V] (positions into the last axis), int32 [N].
+/* One id per row of logits [N, V] (positions into the last axis), int32 [N]
+ * (a 1-D array, as the reference's ids are: src/sampling.c:48,161).
  * Replaces sample_top_k_top_p, src/sampling.c:205-209: draws u [N, min(top_k, V)]
  * on the device from the global seed, then samples. */
 d3s_array sample_top_k_top_p(d3s_array logits, float temperature, int top_k, float top_p);
@@ -55,8 +56,13 @@ void m_seed(uint64_t seed);
 d3s_array d3s_array_from_host(const void *data, int dtype, int rows, int cols);
 /* borrow caller-owned device memory [rows, cols] (row_stride elements apart) */
 d3s_array d3s_array_from_device(void *ptr, int dtype, int rows, int cols, int64_t row_stride);
+/* the 2-D storage: rows x cols elements (ids [N]: N x 1) */
 int d3s_array_rows(d3s_array a);
 int d3s_array_cols(d3s_array a);
+/* the logical shape: 1 for sampled ids [N], 2 otherwise; the size of an axis
+ * (negative axes count from the end).  Replace m_ndim / m_dim, src/mlxu.c:848-851. */
+int d3s_array_ndim(d3s_array a);
+int d3s_array_dim(d3s_array a, int axis);
 int d3s_array_dtype(d3s_array a);
 void *d3s_array_data(d3s_array a);
 /* Waits for the device and copies an int32 array to a malloc'd buffer (the

@@ -28,14 +28,18 @@ extern "C" {
 #define D3S_ERR_UNSUPPORTED -2 /* k beyond d3s_max_k() */
 #define D3S_ERR_LAUNCH -3      /* the HIP launch failed */
 #define D3S_ERR_DTYPE -4       /* unknown logits dtype */
+#define D3S_ERR_NOMEM -5       /* the library's workspace could not be allocated */
 
 /* flags for d3s_sample */
-#define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the reference's
-                                    D3_NO_FUSED_SAMPLER switch, src/sampling.c:197) */
+#define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the same results) */
 #define D3S_FLAG_EXACT_LSE 2u    /* register kernels: always compute the exact row
                                     sum (by default only rows whose top-p cut it
                                     could change) */
 #define D3S_FLAG_EXACT_SELECT 4u /* register kernels: always the radix select */
+#define D3S_FLAG_OP_GRAPH 8u     /* every row in the op graph's order, as the
+                                    reference computes it with D3_NO_FUSED_SAMPLER
+                                    set (src/sampling.c:197); the environment
+                                    variable has the same effect */
 
 /* counters[] slots, when a counters array is given (atomic per-row increments) */
 #define D3S_COUNTER_REFUSED 0      /* rows with a NaN / +inf x: id -1 */
@@ -52,6 +56,11 @@ extern "C" {
  * x = logit / T; ranks by (x desc, index asc); c_r = sum_{j<=r} exp(x_j - lse);
  * ranks r > 0 with c_r > top_p are dropped; p_r = softmax over the kept ranks;
  * ids[row] = index of argmax_r p_r / -log(1 - u_r) (first maximum).
+ * The sums take the reference kernel's order (sequential fp32) when the
+ * reference would run its kernel (k <= 64, k < vocab, vocab <= 65536, and
+ * neither D3S_FLAG_OP_GRAPH nor the environment variable D3_NO_FUSED_SAMPLER,
+ * read at every call as src/sampling.c:197 does), else the op graph's order
+ * (exact prefix sums, rounded once).
  *
  * temperature, top_p: per-row device arrays [n_rows], or NULL to use the
  * scalars.  banned: per-row index set to -inf first (any value outside
@@ -93,8 +102,14 @@ typedef struct {
  *   code0 = clip(main_tok - semantic_start, 0, code_vocab - 1).
  * history may be NULL with history_len 0; history_len <= 64.  code0, first_idx,
  * retry_idx (the two draws' indices) are optional.  counters count both draws.
- * Rows the one-wave kernel does not hold (k or k2 above 64, or a vocab beyond
- * its registers) return D3S_ERR_UNSUPPORTED.
+ * A row either of whose draws is refused (its logits give a NaN or +inf x)
+ * gets main_tok = code0 = -1: the caller checks for it where the reference's
+ * generation loop dies on non-finite logits (src/generate.c:92,130).
+ * Rows within one wave's reach (k and k2 <= 64, vocab within d3s_sample's
+ * one-wave rows) take one launch that reads each row once; any other k and
+ * vocab d3s_sample takes run as two d3s_sample launches and a third that picks
+ * (its retry indices go to retry_idx, or else to a workspace the library keeps
+ * per stream, allocated on the first such call: D3S_ERR_NOMEM if it cannot).
  * Replaces: the two sample_with_noise calls, candidate_token and the repeat test of
  * tower_decode_step (src/tower.c:420-433). */
 int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,

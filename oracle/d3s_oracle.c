@@ -9,8 +9,16 @@
 
 #include "../drama3-mlx_amd/csrc/d3s_math.h"
 
-#define KERNEL_MAX_K 64 /* src/sampling.c:17: the kernel's order applies up to here */
+#define KERNEL_MAX_K 64       /* src/sampling.c:17 */
+#define KERNEL_MAX_V (1024 * 64) /* src/sampling.c:197 */
 #define MIN_TEMPERATURE 1e-5f /* src/sampling.c:16 */
+
+/* The reference takes its kernel's operation order iff k <= 64, k < V,
+ * V <= 65536 and D3_NO_FUSED_SAMPLER is unset (src/sampling.c:197); every other
+ * call takes the op graph (src/sampling.c:22-49, :199-201). */
+static int kernel_order(int64_t V, int k, int op_graph) {
+  return !op_graph && k <= KERNEL_MAX_K && (int64_t)k < V && V <= KERNEL_MAX_V;
+}
 
 typedef struct {
   float x;
@@ -74,8 +82,8 @@ static void top_k_ranked(const float *x, int64_t V, int k, Cand *out, Cand *scra
   qsort(out, (size_t)k, sizeof(Cand), cmp_rank);
 }
 
-static void sample_row(const float *L, int64_t V, int k, const float *u, float T, float top_p,
-                       int32_t *id_out, float *probs, int32_t *cand, float *lse_out,
+static void sample_row(const float *L, int64_t V, int k, int kernel, const float *u, float T,
+                       float top_p, int32_t *id_out, float *probs, int32_t *cand, float *lse_out,
                        uint8_t *flags_out, double *gaps, float *x, Cand *top, Cand *scratch,
                        int *drop, float *score) {
   uint8_t flags = 0;
@@ -121,7 +129,7 @@ static void sample_row(const float *L, int64_t V, int k, const float *u, float T
   const float v0 = top[0].x;
   int cut = k;
   float inv;
-  if (k <= KERNEL_MAX_K) {
+  if (kernel) {
     /* the reference kernel's order, src/sampling.c:123-131 */
     float cum = 0.0f, sum = 0.0f;
     for (int r = 0; r < k; r++) {
@@ -205,11 +213,12 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
                       int64_t row_stride, const float *u, int k, const float *temperature,
                       const float *top_p, float temperature_scalar, float top_p_scalar,
                       const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
-                      float *lse, uint8_t *flags, double *gaps, int n_threads) {
+                      float *lse, uint8_t *flags, double *gaps, int op_graph, int n_threads) {
   if (n_rows < 0 || vocab < 1 || row_stride < vocab || k < 1 || k > vocab || !ids ||
       (n_rows > 0 && (!logits || !u)) || (dtype != D3S_ORACLE_DTYPE_F32 && dtype != D3S_ORACLE_DTYPE_BF16))
     return -1;
   if (n_threads < 1) n_threads = 1;
+  const int kernel = kernel_order(vocab, k, op_graph);
   int failed = 0;
 #pragma omp parallel num_threads(n_threads)
   {
@@ -232,7 +241,7 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
           for (int64_t i = 0; i < vocab; i++) L[i] = d3s_bf16_to_f32(b[i]);
         }
         if (banned && banned[row] >= 0 && banned[row] < vocab) L[banned[row]] = -D3S_INF;
-        sample_row(L, vocab, k, u + row * (int64_t)k, temperature ? temperature[row] : temperature_scalar,
+        sample_row(L, vocab, k, kernel, u + row * (int64_t)k, temperature ? temperature[row] : temperature_scalar,
                    top_p ? top_p[row] : top_p_scalar, ids + row, probs ? probs + row * (int64_t)k : NULL,
                    cand ? cand + row * (int64_t)k : NULL, lse ? lse + row : NULL,
                    flags ? flags + row : NULL, gaps ? gaps + 2 * row : NULL, x, top, scratch, drop, score);
@@ -253,6 +262,11 @@ void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n
                            int32_t semantic_start, int32_t semantic_end, int32_t code_vocab,
                            int32_t *main_tok, int32_t *code0) {
   for (int64_t r = 0; r < n_rows; r++) {
+    if (first[r] < 0 || retry[r] < 0) { /* a refused draw: the row's logits are not finite */
+      main_tok[r] = -1;
+      if (code0) code0[r] = -1;
+      continue;
+    }
     const int32_t t1 = first[r] == 0 ? eos_id : first[r] + semantic_start - 1;
     const int32_t t2 = retry[r] == 0 ? eos_id : retry[r] + semantic_start - 1;
     int seen = 0;

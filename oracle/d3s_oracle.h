@@ -21,12 +21,13 @@
  *   - exp and log are d3s_expf / d3s_logf (drama3-mlx_amd/csrc/d3s_math.h);
  *   - the row sum inside lse is the exact fixed-point sum (2^-40 units) of the
  *     fp32 terms exp(x_i - m), rounded once to fp32: order independent;
- *   - k <= 64: c_r and sum_kept are sequential fp32 sums in rank order and
- *     p_r = e_r * (1/sum_kept), the operation order of the reference kernel
- *     (src/sampling.c:123-139);
- *   - k > 64 (the reference's op graph, src/sampling.c:22-49, whose MLX scan
- *     and softmax order is unpublished): c_r and sum_kept are exact fixed-point
- *     prefix sums rounded to fp32, p_r = e_r * (1/sum_kept).
+ *   - calls the reference sends to its kernel (k <= 64, k < V, V <= 65536 and
+ *     D3_NO_FUSED_SAMPLER unset, src/sampling.c:197): c_r and sum_kept are
+ *     sequential fp32 sums in rank order and p_r = e_r * (1/sum_kept), the
+ *     operation order of the reference kernel (src/sampling.c:123-139);
+ *   - every other call (the reference's op graph, src/sampling.c:22-49, whose
+ *     MLX scan and softmax order is unpublished): c_r and sum_kept are exact
+ *     fixed-point prefix sums rounded to fp32, p_r = e_r * (1/sum_kept).
  * Rows whose logits (after the optional banned index) give a NaN or +inf x are
  * refused: id -1 (the reference's caller refuses them, src/generate.c:92,130).
  * A row whose x are all -inf returns index 0, as the reference kernel does.
@@ -55,12 +56,14 @@ extern "C" {
  * Outputs (each may be NULL except ids): ids [n_rows]; probs, cand [n_rows, k]
  * (post-filter probability and index by rank); lse [n_rows]; flags [n_rows];
  * gaps [n_rows, 2] = (min_r |c64_r - top_p|, relative gap of the top two scores).
+ * op_graph: nonzero takes the op graph's order for every call, as the
+ * reference does when D3_NO_FUSED_SAMPLER is set (src/sampling.c:197).
  * Returns 0, or -1 for bad arguments. */
 int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
                       int64_t row_stride, const float *u, int k, const float *temperature,
                       const float *top_p, float temperature_scalar, float top_p_scalar,
                       const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
-                      float *lse, uint8_t *flags, double *gaps, int n_threads);
+                      float *lse, uint8_t *flags, double *gaps, int op_graph, int n_threads);
 
 /* elementwise d3s_expf / d3s_logf / true division, for the math tests */
 /* Repetition-aware selection of the main token (src/tower.c:405-409,:425-433),
@@ -70,7 +73,10 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
  *   main = token(retry) if semantic_start <= token(first) <= semantic_end
  *          and token(first) is one of the row's history_len recent main
  *          tokens (:429-431), else token(first)                     (:432)
- *   code0 = clip(main - semantic_start, 0, code_vocab - 1)          (:433-434) */
+ *   code0 = clip(main - semantic_start, 0, code_vocab - 1)          (:433-434)
+ * A row either of whose draws was refused (index -1: a NaN or +inf x) gets
+ * main = code0 = -1, the signal a caller checks where the reference's
+ * generation loop dies on non-finite logits (src/generate.c:92,130). */
 void d3s_oracle_ras_select(const int32_t *first, const int32_t *retry, int64_t n_rows,
                            const int32_t *history, int history_len, int32_t eos_id,
                            int32_t semantic_start, int32_t semantic_end, int32_t code_vocab,

@@ -27,15 +27,41 @@ def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
-def lib():
+def build_native(out_dir):
+    """Compile the oracle for the host it runs on (-O3 -march=native, the same
+    flags otherwise) into out_dir; returns the library's path, or None when no
+    C compiler is at hand.  The shipped build (oracle/Makefile) targets
+    x86-64-v3 so that one binary runs on every host; this one is for timing
+    the CPU baseline where it runs."""
+    path = os.path.join(out_dir, "libd3s_oracle_native.so")
+    cmd = ["gcc", "-O3", "-march=native", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
+           "-fopenmp", "-shared", "-o", path, os.path.join(HERE, "d3s_oracle.c"), "-lm"]
+    try:
+        subprocess.run(cmd, check=True, capture_output=True)
+    except (OSError, subprocess.CalledProcessError):
+        return None
+    return path
+
+
+def use_library(path):
+    """Load the oracle from `path` instead of oracle/libd3s_oracle.so (the
+    native build of build_native) for the calls that follow."""
+    global _lib
+    _lib = None
+    return lib(path)
+
+
+def lib(path=None):
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            build()
-        L = ctypes.CDLL(LIB_PATH)
+        if path is None:
+            path = LIB_PATH
+            if not os.path.exists(LIB_PATH):
+                build()
+        L = ctypes.CDLL(path)
         vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
         L.d3s_oracle_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp,
-                                        vp, vp, vp, vp, vp, i32]
+                                        vp, vp, vp, vp, vp, i32, i32]
         L.d3s_oracle_sample.restype = i32
         for name in ("d3s_oracle_expf", "d3s_oracle_logf", "d3s_oracle_fix40", "d3s_oracle_fix40_exp",
                      "d3s_oracle_fixsum_gt_threshold", "d3s_oracle_fix40_unit", "d3s_oracle_expf_nonpos"):
@@ -62,9 +88,12 @@ def _p(a):
 
 
 def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=None, vocab=None,
-           detail=True):
+           detail=True, op_graph=False):
     """Oracle sampling.  logits: float32 [N, >=V] or uint16 (bf16 bits) [N, >=V];
     u: float32 [N, k]; temperature / top_p: scalars or float32 [N] arrays.
+    op_graph: every row in the op graph's order (the reference with
+    D3_NO_FUSED_SAMPLER set); otherwise the order follows the reference's
+    routing (src/sampling.c:197).
     Returns dict(ids, probs, cand, lse, flags, gaps); with detail=False only
     ids (no probabilities, candidates, lse or float64 boundary shadow)."""
     logits = np.ascontiguousarray(logits)
@@ -100,7 +129,7 @@ def sample(logits, u, temperature, top_p, banned=None, n_threads=1, row_stride=N
     gaps = np.empty((N, 2), np.float64) if detail else None
     rc = lib().d3s_oracle_sample(_p(logits), dtype, N, V, stride, _p(u), k, _p(t_arr), _p(p_arr), t_s,
                                  p_s, _p(ban), _p(ids), _p(probs), _p(cand), _p(lse), _p(flags),
-                                 _p(gaps), n_threads)
+                                 _p(gaps), 1 if op_graph else 0, n_threads)
     if rc != 0:
         raise ValueError("oracle rejected the arguments")
     return dict(ids=ids, probs=probs, cand=cand, lse=lse, flags=flags, gaps=gaps)

@@ -19,3 +19,23 @@ def oracle():
     import d3s_oracle
     d3s_oracle.lib()
     return d3s_oracle
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Rows, id mismatches and boundary rows of every configuration the GPU
+    parity tests compared (BASELINE.json's C1-C5 first)."""
+    try:
+        import parity_report
+    except ImportError:
+        return
+    recs = parity_report.RECORDS
+    if not recs:
+        return
+    tr = terminalreporter
+    tr.section("parity: rows / id mismatches / boundary rows")
+    configs = [r for r in recs if r[0].startswith("config ")]
+    for label, rows, bad, edge in configs:
+        tr.write_line(f"{label}: rows {rows}, id mismatches {bad}, boundary rows {edge}")
+    tot = [sum(r[i] for r in recs) for i in (1, 2, 3)]
+    tr.write_line(f"all {len(recs)} comparisons: rows {tot[0]}, id mismatches {tot[1]}, "
+                  f"boundary rows {tot[2]}")

@@ -72,7 +72,7 @@ def test_argument_validation_without_device(lib):
     assert d3s.sample_raw(**{**base, "n_rows": -1}) == -1
     assert d3s.sample_raw(**{**base, "ids": None}) == -1
     assert d3s.sample_raw(**{**base, "flags": 64}) == -1
-    assert d3s.sample_raw(**{**base, "flags": 8}) == -1
+    assert d3s.sample_raw(**{**base, "flags": 16}) == -1  # 1, 2, 4, 8 are flags; 16 is not
     assert d3s.sample_raw(**{**base, "flags": 2 | 64}) == -1
     big = dict(base, vocab=20000, row_stride=20000, k=16385)
     assert d3s.sample_raw(**big) == -2

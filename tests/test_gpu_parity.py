@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import d3s_workloads as W
+import parity_report
 
 pytestmark = pytest.mark.gpu
 
@@ -34,10 +35,14 @@ def banner(msg):
 
 
 def compare(oracle, gpu, logits, u, T, top_p, banned=None, flags=0, label="", row_stride=None,
-            vocab=None):
+            vocab=None, op_graph=False):
+    """GPU against the oracle; op_graph: every row in the op graph's order on
+    both sides (D3S_FLAG_OP_GRAPH, the reference's D3_NO_FUSED_SAMPLER)."""
+    if op_graph:
+        flags |= gpu.FLAG_OP_GRAPH
     banner(f"{label} shape={logits.shape} k={u.shape[1]} flags={flags}")
     exp = oracle.sample(logits, u, T, top_p, banned=banned, n_threads=8, row_stride=row_stride,
-                        vocab=vocab)
+                        vocab=vocab, op_graph=op_graph)
     got = gpu.sample(logits, u, T, top_p, banned=banned, flags=flags, row_stride=row_stride,
                      vocab=vocab)
     assert got["rc"] == 0, got["rc"]
@@ -45,6 +50,7 @@ def compare(oracle, gpu, logits, u, T, top_p, banned=None, flags=0, label="", ro
     edge = int(np.sum((exp["flags"] & (oracle.TOPP_EDGE | oracle.RACE_EDGE)) != 0))
     banner(f"  rows={len(exp['ids'])} mismatched={len(bad)} boundary={edge} "
            f"counters={got['counters'].tolist()}")
+    parity_report.record(label, len(exp["ids"]), len(bad), edge)
     assert len(bad) == 0, (bad[:10], got["ids"][bad[:10]], exp["ids"][bad[:10]])
     assert np.array_equal(got["cand"], exp["cand"])
     both_nan = np.isnan(got["probs"]) & np.isnan(exp["probs"])
@@ -117,12 +123,15 @@ def test_uniform_fill_matches_host(gpu, oracle):
     assert np.array_equal(u, oracle.uniform(42, 7, 1, 100_003)[0])
 
 
-@pytest.mark.parametrize("name,rows", [("C1", 2000), ("C2", 9), ("C3", 256), ("C4", 64),
+@pytest.mark.parametrize("name,rows", [("C1", 10000), ("C2", 9), ("C3", 256), ("C4", 64),
                                        ("C5", 4096)])
 def test_parity_on_configs(gpu, oracle, name, rows):
+    """BASELINE.json's five configurations at their full shapes (C1: its
+    10 000 seeded rows in one launch)."""
     w = W.make(name, rows=rows, seed=42, uniforms=False)
     u = oracle.uniform(42, 0, rows, w["k"])
-    compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], w["banned"], label=name)
+    compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], w["banned"],
+            label=f"config {name}")
 
 
 def test_single_row_launches(gpu, oracle):

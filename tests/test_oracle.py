@@ -52,13 +52,45 @@ def test_oracle_matches_closed_form(oracle, V, k, T, top_p, dtype):
     assert n_edge <= n // 3
 
 
-@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C5"])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
 def test_oracle_matches_closed_form_on_configs(oracle, name):
-    rows = {"C1": 64, "C2": 9, "C3": 64, "C5": 8}[name]
+    rows = {"C1": 64, "C2": 9, "C3": 64, "C4": 8, "C5": 8}[name]
     w = W.make(name, rows=rows, seed=11)
     n, n_edge = check_rows(oracle, w["logits"], w["u"], w["temperature"], w["top_p"], w["k"],
                            w["banned"])
     assert n_edge <= max(1, n // 3)
+
+
+@pytest.mark.parametrize("V,k", [(65536, 30), (65537, 30), (1000, 64), (1000, 65), (64, 64),
+                                 (64, 63), (4097, 30)])
+def test_oracle_order_follows_the_reference_routing(oracle, V, k):
+    """The cumulative's order: the reference kernel's left-to-right fp32 sum iff
+    k <= 64, k < V and V <= 65536 (src/sampling.c:197), else the op graph's,
+    modelled as the exact prefix sum rounded once; op_graph=True forces the
+    latter (D3_NO_FUSED_SAMPLER).  Checked on rows whose top_p lies where the
+    two orders cut at different ranks, against both orders' cumulatives built
+    here from the elementwise exp and fixed-point image: the number of kept
+    ranks must be the cut of the order the routing names."""
+    import order_rows
+    rng = np.random.default_rng([V, k, 17])
+    N = 8
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    x[np.arange(N), rng.integers(0, V, N)] += 6.0
+    kk = min(k, V)
+    top_p = order_rows.split_top_p(oracle, x, 1.0, kk)
+    split = ~np.isnan(top_p)
+    assert split.sum() >= 3
+    top_p = np.where(split, top_p, 0.9).astype(np.float32)
+    u = W.uniform_rows(17, 0, N, kk)
+    default = oracle.sample(x, u, 1.0, top_p)
+    forced = oracle.sample(x, u, 1.0, top_p, op_graph=True)
+    kernel = k <= 64 and k < V and V <= 65536
+    for r in np.nonzero(split)[0]:
+        seq, ex = order_rows.cumulatives(oracle, x[r], default["lse"][r], kk)
+        cut = lambda c: next((j for j in range(1, kk) if c[j] > top_p[r]), kk)
+        assert cut(seq) != cut(ex)
+        assert np.count_nonzero(default["probs"][r]) == (cut(seq) if kernel else cut(ex)), r
+        assert np.count_nonzero(forced["probs"][r]) == cut(ex), r
 
 
 def test_brute_force_tiny_rows(oracle):

@@ -38,11 +38,17 @@ def test_selection_known_answers(oracle):
     hist[5, 1] = END                # the last code, seen
     hist[6, 0] = START              # the first code, seen
     main, code0 = oracle.ras_select(first, retry, hist, EOS, START, END, CODES)
-    assert main.tolist() == [EOS, START + 8, START + 4, EOS, START - 2, START + 1, START + 1, START + 2]
-    assert code0.tolist() == [0, 8, 4, 0, 0, 1, 1, 2]  # eos lies below the band: clipped to 0
+    # row 4: the first draw was refused (non-finite logits): -1 for both outputs
+    assert main.tolist() == [EOS, START + 8, START + 4, EOS, -1, START + 1, START + 1, START + 2]
+    assert code0.tolist() == [0, 8, 4, 0, -1, 1, 1, 2]  # eos lies below the band: clipped to 0
     # no history: the first draw always stands
     main0, _ = oracle.ras_select(first, retry, np.zeros((8, 0), np.int32), EOS, START, END, CODES)
-    assert np.array_equal(main0, np.where(first == 0, EOS, first + START - 1))
+    ok = first >= 0
+    assert np.array_equal(main0[ok], np.where(first == 0, EOS, first + START - 1)[ok])
+    # a refused retry refuses the row too, repeated or not
+    m2, c2 = oracle.ras_select(np.array([5, 5], np.int32), np.array([-1, -1], np.int32),
+                               np.array([[START + 4], [7]], np.int32), EOS, START, END, CODES)
+    assert m2.tolist() == [-1, -1] and c2.tolist() == [-1, -1]
 
 
 def test_ras_argument_validation_without_device():
@@ -82,11 +88,11 @@ def _case(oracle, name, rows, seed, top_k=30, temperature=0.7, top_p=0.7, H=16, 
     return x, u, u2, hist, params
 
 
-def _check(oracle, gpu, x, u, u2, hist, params):
+def _check(oracle, gpu, x, u, u2, hist, params, indices=True):
     exp = oracle.ras(x, u, u2, params, hist, n_threads=8)
-    got = gpu.sample_ras(x, u, u2, params, hist)
+    got = gpu.sample_ras(x, u, u2, params, hist, indices=indices)
     assert got["rc"] == 0, got["rc"]
-    for name in ("first", "retry", "main", "code0"):
+    for name in ("first", "retry", "main", "code0") if indices else ("main", "code0"):
         bad = np.nonzero(got[name] != exp[name])[0]
         assert len(bad) == 0, (name, bad[:8], got[name][bad[:8]], exp[name][bad[:8]])
     return got, exp
@@ -123,15 +129,61 @@ def test_ras_bf16_head_and_parameters(gpu, oracle):
 
 
 @pytest.mark.gpu
-def test_ras_rows_beyond_the_wave_kernel(gpu, oracle):
-    """k above 64 or a row wider than one wave's registers: unsupported, nothing launched."""
-    x = np.zeros((2, 4097), np.float32)
-    u = np.full((2, 100), 0.5, np.float32)
-    got = gpu.sample_ras(x, u, u[:, :30], dict(temperature=1.0, top_p=0.9, top_k=100, **MAP))
-    assert got["rc"] == -2
-    wide = np.zeros((1, 20000), np.float32)
-    got = gpu.sample_ras(wide, u[:1, :30], u[:1, :30], dict(temperature=1.0, top_p=0.9, top_k=30, **MAP))
-    assert got["rc"] == -2
+@pytest.mark.parametrize("indices", [True, False])
+def test_ras_rows_beyond_the_wave_kernel(gpu, oracle, indices):
+    """What the fused launch does not hold runs as two routed draws and a pick
+    (the reference draws both for any top_k >= 1 and any head width,
+    src/tower.c:425-433, src/main.c:165): top_k 100 for either draw, fp32 rows
+    of 20000 and bf16 rows of 151936.  Without the index outputs the first
+    draw's indices pass through main_tok and the retry's through the library's
+    workspace."""
+    rng = np.random.default_rng(23)
+    cases = []
+    x = (rng.standard_normal((64, 4097)) * 2.5).astype(np.float32)
+    x[np.arange(64), rng.integers(0, 4097, 64)] += 6.0
+    cases.append((x, 100, 30))
+    cases.append((x, 30, 100))
+    w = (rng.standard_normal((8, 20000)) * 2.5).astype(np.float32)
+    w[np.arange(8), rng.integers(0, 20000, 8)] += 8.0
+    cases.append((w, 30, 30))
+    c4 = W.make("C4", rows=4, seed=23, uniforms=False)["logits"]
+    cases.append((c4, 30, 30))
+    for xs, top_k, retry_top_k in cases:
+        N, V = xs.shape
+        k, k2 = min(top_k, V), min(retry_top_k, V)
+        u = oracle.uniform(23, 0, N, k)
+        u2 = oracle.uniform(23, 1, N, k2)
+        first = oracle.sample(xs, u, 0.7, 0.7, n_threads=8)["ids"]
+        hist = rng.integers(START, END + 1, (N, 16)).astype(np.int32)
+        hist[::2, 3] = np.where(first[::2] == 0, EOS, first[::2] + START - 1)
+        params = dict(temperature=0.7, top_p=0.7, top_k=top_k, retry_top_k=retry_top_k, **MAP)
+        print(f"[ras] fallback V={V} top_k={top_k} retry_top_k={retry_top_k} indices={indices}", flush=True)
+        _check(oracle, gpu, xs, u, u2, hist, params, indices=indices)
+
+
+@pytest.mark.gpu
+def test_ras_refused_rows_signal(gpu, oracle):
+    """A row whose logits hold a NaN or +inf, or whose finite logits overflow
+    at the first draw's temperature only: main_tok = code0 = -1 (the caller's
+    check, where the reference's generation loop dies, src/generate.c:92,130),
+    on the fused launch and on the fallback; the other rows as the oracle's."""
+    rng = np.random.default_rng(29)
+    x = (rng.standard_normal((8, 4097)) * 2.5).astype(np.float32)
+    x[1, 100] = np.nan
+    x[3, 4096] = np.inf
+    x[5, 7] = 3e38  # x = 3e38 / 0.7 overflows; the retry's T = 1.0 does not
+    u = oracle.uniform(29, 0, 8, 30)
+    u2 = oracle.uniform(29, 1, 8, 30)
+    hist = np.full((8, 16), START, np.int32)
+    for top_k in (30, 100):
+        uk = oracle.uniform(29, 0, 8, top_k)
+        params = dict(temperature=0.7, top_p=0.7, top_k=top_k, **MAP)
+        got, exp = _check(oracle, gpu, x, uk if top_k > 30 else u, u2, hist, params)
+        for r in (1, 3, 5):
+            assert got["main"][r] == -1 and got["code0"][r] == -1, (top_k, r)
+        assert np.all(got["main"][[0, 2, 4, 6, 7]] >= 0)
+        assert got["retry"][5] >= 0  # the retry alone was not refused
+        assert got["counters"][gpu.COUNTER_REFUSED] == 5  # rows 1 and 3 twice, row 5 once
 
 
 @pytest.mark.gpu

@@ -32,6 +32,8 @@ def shim():
         ("d3s_array_rows", [vp], i32),
         ("d3s_array_cols", [vp], i32),
         ("d3s_array_dtype", [vp], i32),
+        ("d3s_array_ndim", [vp], i32),
+        ("d3s_array_dim", [vp, i32], i32),
         ("d3s_array_copy_to_host", [vp, vp], None),
         ("d3s_arena_mark", [], sz),
         ("d3s_arena_release", [sz], None),
@@ -58,6 +60,10 @@ def test_reference_names_on_device_arrays(shim, oracle):
         L.m_seed(99)
         ids = L.sample_top_k_top_p(lx, 0.7, 30, 0.7)  # draw 0
         assert L.d3s_array_dtype(ids) == I32
+        # ids are 1-D [N], as the reference's (src/sampling.c:48,161)
+        assert L.d3s_array_ndim(ids) == 1
+        assert L.d3s_array_dim(ids, 0) == 16 and L.d3s_array_dim(ids, -1) == 16
+        assert L.d3s_array_ndim(lx) == 2 and L.d3s_array_dim(lx, -1) == 4097
         got = to_host(L, ids, np.int32).reshape(-1)  # [rows, 1]
         u0 = oracle.uniform(99, 0, 1, 16 * 30).reshape(16, 30)
         assert np.array_equal(got, oracle.sample(x, u0, 0.7, 0.7)["ids"])
