@@ -7,7 +7,9 @@ gemv's order (within a lane, across blocks, and in the lane tree: a sum of
 2^24, 1 and -2^24 is 0 or 1 depending on which pair meets first), by float64
 within the bf16 rounding, and by exact integer dot products.  Whether the
 reference's Metal compiler fuses its multiply-adds is not pinned (fast-math
-contraction); the oracle fuses them."""
+contraction); the oracle fuses them, and a bf16 product's exactness in fp32
+makes the choice immaterial unless a product overflows or goes subnormal (a
+hand-derived row shows the split)."""
 import numpy as np
 import pytest
 
@@ -49,6 +51,59 @@ def test_gemv_order_known_answers(oracle, placements, expected):
     x, w = _one_row(384, placements)
     y = oracle.linear_bf16(x, w)
     assert f32(y)[0, 0] == np.float32(expected)
+
+
+# Lane 0, block 0: element 0 adds -1.5 * 2^127, element 1 adds 1.5 * 2^127 * 2
+# (a product of 1.5 * 2^128, above FLT_MAX).  Fused, the exact running sum
+# 1.5 * 2^127 is finite; a multiply then an add gives +inf first.
+FMA_SPLIT = ([(0, -1.5 * 2.0 ** 127), (1, 1.5 * 2.0 ** 127)], 1, 2.0)
+
+
+def _fma_split_row():
+    placements, xi, xv = FMA_SPLIT
+    x, w = _one_row(128, placements)
+    xf = f32(x).copy()
+    xf[0, xi] = xv
+    return bf16(xf), w
+
+
+def test_gemv_fused_multiply_add_known_answer(oracle):
+    """A bf16 x bf16 product has at most 16 significant bits, so it is exact in
+    fp32 whenever it lies in fp32's normal range, and then a fused multiply-add
+    RN(w x + acc) equals RN(RN(w x) + acc): the reference's unpinned contraction
+    (Metal fast math on `result += in[t] * v[t]`, src/mlxu.c:393) cannot change
+    such sums.  The two differ only when a product overflows or falls below
+    2^-133 (its 16 bits then reach under 2^-149).  This row separates them: the
+    oracle fuses, so the sum is 1.5 * 2^127 (exact in bf16), not +inf."""
+    x, w = _fma_split_row()
+    y = f32(oracle.linear_bf16(x, w))[0, 0]
+    assert y == np.float32(1.5 * 2.0 ** 127)
+
+
+def _mul_then_add(x, w):
+    """the gemv order with a separate fp32 multiply and add (numpy float32)"""
+    xf, wf = f32(x)[0], f32(w)
+    V, K = wf.shape
+    acc = np.zeros((V, 32), np.float32)
+    for c in range(K // 128):
+        for t in range(4):
+            cols = c * 128 + 4 * np.arange(32) + t
+            acc = acc + (wf[:, cols] * xf[cols]).astype(np.float32)
+    for sn in (16, 8, 4, 2, 1):
+        acc[:, :sn] = acc[:, :sn] + acc[:, sn:2 * sn]
+    return bf16(acc[:, 0])[None, :]
+
+
+def test_gemv_normal_range_products_do_not_depend_on_fusing(oracle):
+    """On data whose products stay in fp32's normal range (as a head's do) the
+    oracle's fused sums equal a multiply-then-add restatement of the same order
+    bit for bit, as the exactness of bf16 products implies."""
+    rng = np.random.default_rng(5)
+    x = bf16(rng.standard_normal((1, 512)))
+    w = bf16(rng.standard_normal((300, 512)) * 0.05)
+    assert np.array_equal(oracle.linear_bf16(x, w), _mul_then_add(x, w))
+    xs, ws = _fma_split_row()
+    assert f32(_mul_then_add(xs, ws))[0, 0] == np.inf  # the split row does tell them apart
 
 
 def test_gemv_exact_integers(oracle):
@@ -113,6 +168,8 @@ def test_gemv_equals_the_oracle(gpu, oracle, N, K, V):
     assert np.array_equal(y, oracle.linear_bf16(x, w))
     x2, w2 = _one_row(384, [(0, BIG), (32, 1.0), (64, -BIG)])
     assert np.array_equal(gpu.linear_bf16(x2, w2)[1], oracle.linear_bf16(x2, w2))
+    x3, w3 = _fma_split_row()  # fused multiply-add: finite, where multiply-then-add overflows
+    assert np.array_equal(gpu.linear_bf16(x3, w3)[1], oracle.linear_bf16(x3, w3))
 
 
 @pytest.mark.gpu
