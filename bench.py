@@ -118,6 +118,24 @@ def time_launches(pool, launches, warmup, g, n_streams):
     return ms, wall, launches
 
 
+PREWARM_S = 0.3
+
+
+def prewarm(pool, g):
+    """Headline launches back to back until PREWARM_S seconds have passed
+    (the GPU's clocks ramp up over the first milliseconds of work)."""
+    import hiprt
+    ids = hiprt.DeviceBuffer(4 * ROWS * g)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < PREWARM_S:
+        for _ in range(8):
+            assert pool.launch((n % (pool.n // g)) * g, g, ids, None) == 0
+            n += 1
+        hiprt.synchronize()
+    return n
+
+
 def traffic_probe(pool, g, n):
     """For rocprofv3 --pmc runs: one 256 MiB device-to-device copy (the
     calibration dispatch of known traffic: 256 MiB read, 256 MiB written),
@@ -634,6 +652,11 @@ def main():
     if args.counter_probe:
         counter_probe(args.counter_probe, pool, G)
         return
+    # clocks settle: headline launches for at least PREWARM_S seconds before
+    # anything is timed (a fresh box runs its first ~10 ms of launches about
+    # 15 % slower), then --warmup untimed launches, then --steps timed ones
+    prewarm_launches = prewarm(pool, G)
+    log(f"pre-warm: {prewarm_launches} launches over {PREWARM_S} s")
     # the dominant kernel alone: G batches per launch, back to back on one
     # stream, HIP events on that stream (the roofline's launch duration)
     bytes_per_launch = G * ROWS * BYTES_PER_ROW
@@ -703,7 +726,9 @@ def main():
                    "step": f"one d3s_sample launch of {G} batches of 256 rows ({G * ROWS} rows)",
                    "steady_state": f"multi-batch launches: {G} batches per d3s_sample call, "
                                    f"taken in turn by {S} streams",
-                   "batches_per_launch": G, "streams": S},
+                   "batches_per_launch": G, "streams": S,
+                   "prewarm": f"{prewarm_launches} untimed launches over {PREWARM_S} s before the "
+                              f"--warmup launches (clocks settle)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel_us_mean": kmean, "bytes_per_launch": bytes_per_launch,

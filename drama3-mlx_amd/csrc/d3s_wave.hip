@@ -48,11 +48,10 @@ constexpr int BUFFER_FLAGS = 0x00020000;
 constexpr float LN2_F = 0.693147182f;
 
 struct __align__(16) WaveLds {
-  uint64_t keys[WAVE + 1]; /* dense candidate keys (+ a zero pad for pair reads) */
+  float buf[WAVE];         /* lane maxima for the threshold; sequential sums */
+  uint64_t keys[WAVE + 2]; /* dense candidate keys (+ a zero pad for pair reads) */
   uint64_t ranked[WAVE];   /* keys by rank */
   uint32_t hist[NB];       /* radix-select histogram */
-  float buf[WAVE];         /* sequential sums */
-  float buf2[WAVE];
 };
 
 __device__ __forceinline__ float fmaximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
@@ -83,48 +82,14 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-/* Lane r (< k) gets the left-to-right fp32 prefix sums c_r = e_0 + ... + e_r
- * and s_r = f_0 + ... + f_r (the reference kernel's sequential cumulative,
- * src/sampling.c:126-127, and its kept sum, :129-131, whose value at the cut
- * is s_{cut-1}).  One lane runs both chains side by side over the terms in
- * LDS, four at a time, and writes each prefix back in place; every lane then
- * reads its own.  The chains stop after the group in which c passes `stop`:
- * every later rank has c_r > stop too (the terms are non-negative), so those
- * lanes get c = +inf (and s = 0, never read: the cut lies before them). */
-__device__ __forceinline__ void wave_seq_prefix2(float e, float f, int k, float *be, float *bf, float &c,
-                                                 float &s, float stop = __builtin_inff()) {
-  const int lane = lane_id();
-  be[lane] = lane < k ? e : 0.0f;
-  bf[lane] = lane < k ? f : 0.0f;
-  wave_lds_sync();
-  int done = 0;
-  if (lane == 0) {
-    float4 *e4 = (float4 *)be;
-    float4 *f4 = (float4 *)bf;
-    float ce = 0.0f, cf = 0.0f;
-    int r4 = 0;
-    while (r4 < (k + 3) / 4) {
-      float4 qe = e4[r4], qf = f4[r4];
-      qe.x = ce = ce + qe.x;
-      qf.x = cf = cf + qf.x;
-      qe.y = ce = ce + qe.y;
-      qf.y = cf = cf + qf.y;
-      qe.z = ce = ce + qe.z;
-      qf.z = cf = cf + qf.z;
-      qe.w = ce = ce + qe.w;
-      qf.w = cf = cf + qf.w;
-      e4[r4] = qe;
-      f4[r4] = qf;
-      r4++;
-      if (ce > stop) break;
-    }
-    done = 4 * r4;
-  }
-  done = (int)readlane_u((uint32_t)done, 0);
-  wave_lds_sync();
-  c = lane < done ? be[lane] : __builtin_inff();
-  s = lane < done ? bf[lane] : 0.0f;
-  wave_lds_sync();
+/* e_0 + e_1 + ... + e_{n-1} added left to right in fp32 (lane r holds e_r,
+ * n <= 64 wave-uniform), the same value in every lane: the reference kernel's
+ * kept sum (src/sampling.c:129-131).  Each term comes from its lane by
+ * readlane (a scalar broadcast), so the chain is one add per term. */
+__device__ __forceinline__ float wave_seq_sum_rl(float e, int n) {
+  float s = 0.0f;
+  for (int r = 0; r < n; r++) s = s + readlane_f(e, r);
+  return s;
 }
 
 /* The race (src/sampling.c:132-139): lane r < k holds rank r's index, its
@@ -160,31 +125,29 @@ constexpr int NEED_EXACT = (int)0x80000000;
  * `exact`, else the fast one with relative error bound eps_s.
  *
  * The cut only depends on lse through c_r; the probabilities use exp(x - x_0).
- * With the fast lse, |c'_r - c_r| <= c'_r (eps_e + (2k + 2) 2^-24) (+ (k + 2)
+ * With the fast lse the cumulative c'_r is a parallel fp32 scan of hardware
+ * 2^x terms, and |c'_r - c_r| <= c'_r (eps_e + (2k + 2) 2^-24) (+ (k + 2)
  * 2^-40 in the op graph's order, whose exact prefixes truncate each term to
- * 2^-40), eps_e bounding the relative change of a term exp(v - lse) between
- * the two lse values; when some c'_r lies that close to top_p, exact_lse()
- * gives the exact lse (NaN: the wave cannot, and NEED_EXACT is returned
- * before anything is written).
+ * 2^-40), whichever order the two sums add in; eps_e bounds the relative
+ * change of a term exp(v - lse) between the two lse values.  When no c'_r lies
+ * that close to top_p, the cut from c' is the cut from c; otherwise
+ * exact_lse() gives the exact lse (NaN: the wave cannot, and NEED_EXACT is
+ * returned before anything is written) and c is computed in its own order.
  *  - kernel order: c_r and the kept sum are left-to-right fp32 sums in rank
- *    order, p_r = e_r (1 / s_{cut-1});
+ *    order, p_r = e_r (1 / sum_{r < cut} e_r);
  *  - op graph order: c_r = RN(sum_{j<=r} fix40(exp(x_j - lse)) 2^-40), the
  *    kept sum the same of exp(x_j - x_0) over the kept ranks. */
 template <class ExactLse>
 __device__ __forceinline__ int wave_tail(const SampleArgs &a, int row, uint64_t key, float M, float lse,
                                          bool exact, float eps_s, float noise, float top_p, float *buf,
-                                         float *buf2, ExactLse &&exact_lse) {
+                                         ExactLse &&exact_lse) {
   const int lane = lane_id();
   const int k = a.k;
   const bool act = lane < k;
   const float v = key_x(key);
   const int idx = key_idx(key);
   const float ep = act ? d3s_expf_nonpos(v - M) : 0.0f; /* exp(x - x_0), x_0 = m */
-  /* the cumulative's terms: exact with the exact lse; with the fast lse only
-   * the cut depends on them, so the hardware 2^x, inside the margin below */
-  const float ec = exact ? d3s_expf_nonpos(v - lse) : __builtin_amdgcn_exp2f((v - lse) * LOG2E_F);
-  /* the margin: |c'_r - c_r| <= B c'_r + slack (0 with the exact lse) */
-  float B = 0.0f;
+  float cc = 0.0f;
   if (!exact) {
     const float D = lse - readlane_f(v, k - 1); /* ranks have non-increasing x */
     const float dl = eps_s + 0x1p-18f + 0x1p-23f * (fabsf(lse) + 1.0f);
@@ -192,47 +155,28 @@ __device__ __forceinline__ int wave_tail(const SampleArgs &a, int row, uint64_t 
      * side, of its product with log2(e) and of log2(e) itself (|v - lse| <=
      * D), v_exp_f32's error and d3s_expf's */
     const float eps_e = dl + 0x1p-22f * (D + 1.0f) + 0x1p-20f;
-    B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
-  }
-  int cut;
-  float inv;
-  if (!a.opgraph) {
-    /* past stop, c - top_p > B c + 2^-60: certainly dropped, also with the
-     * exact lse, and never within the margin (for B < 1/2) */
-    const float stop = B < 0.5f ? (top_p + 0x1p-60f) / (1.0f - B) * (1.0f + 0x1p-20f) : __builtin_inff();
-    float cc, sp;
-    wave_seq_prefix2(act ? ec : 0.0f, ep, k, buf, buf2, cc, sp, stop);
-    if (!exact) {
-      exact = __ballot(act && lane > 0 && cc != __builtin_inff() && fabsf(cc - top_p) <= B * cc + 0x1p-60f) !=
-                  0ull ||
-              (a.flags & FLAG_EXACT_LSE) != 0;
-      if (exact) {
-        if (lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-        const float lx = exact_lse();
-        if (d3s_isnan(lx)) return NEED_EXACT;
-        cc = wave_seq_cumsum(act ? d3s_expf_nonpos(v - lx) : 0.0f, k, buf);
-      }
+    const float B = 1.01f * (eps_e + (float)(2 * k + 2) * 0x1p-24f);
+    const float slack = a.opgraph ? (float)(k + 2) * 0x1p-40f : 0x1p-60f;
+    cc = wave_scan_add_f32(act ? __builtin_amdgcn_exp2f((v - lse) * LOG2E_F) : 0.0f);
+    exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + slack) != 0ull ||
+            (a.flags & FLAG_EXACT_LSE) != 0;
+    if (exact) {
+      if (lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
+      lse = exact_lse();
+      if (d3s_isnan(lse)) return NEED_EXACT;
     }
-    const uint64_t dm = __ballot(act && lane > 0 && cc > top_p);
-    cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
-    inv = 1.0f / readlane_f(sp, cut - 1);
-  } else {
-    float cc = 0.0f;
-    if (!exact) {
-      cc = wave_scan_add_f32(act ? ec : 0.0f);
-      exact = __ballot(act && lane > 0 && fabsf(cc - top_p) <= B * cc + (float)(k + 2) * 0x1p-40f) != 0ull ||
-              (a.flags & FLAG_EXACT_LSE) != 0;
-      if (exact) {
-        if (lane == 0 && a.counters) atomicAdd(&a.counters[CNT_EXACT_LSE], 1u);
-        lse = exact_lse();
-        if (d3s_isnan(lse)) return NEED_EXACT;
-      }
-    }
-    if (exact) cc = d3s_fixsum_to_f32(wave_scan_u64(act ? d3s_fix40_exp(v - lse) : 0ull));
-    const uint64_t dm = __ballot(act && lane > 0 && cc > top_p);
-    cut = dm ? __builtin_ctzll(dm) : k;
-    inv = 1.0f / d3s_fixsum_to_f32(wave_sum_u64(act && lane < cut ? d3s_fix40_unit(ep) : 0ull));
   }
+  if (exact) {
+    if (!a.opgraph)
+      cc = wave_seq_cumsum(act ? d3s_expf_nonpos(v - lse) : 0.0f, k, buf);
+    else
+      cc = d3s_fixsum_to_f32(wave_scan_u64(act ? d3s_fix40_exp(v - lse) : 0ull));
+  }
+  const uint64_t dm = __ballot(act && lane > 0 && cc > top_p);
+  const int cut = dm ? __builtin_ctzll(dm) : k; /* c_r is non-decreasing: drops are a suffix */
+  const float kept = !a.opgraph ? wave_seq_sum_rl(ep, cut)
+                                : d3s_fixsum_to_f32(wave_sum_u64(act && lane < cut ? d3s_fix40_unit(ep) : 0ull));
+  const float inv = 1.0f / kept;
   const float p = (act && lane < cut) ? ep * inv : 0.0f;
   return wave_race_p(a, row, idx, p, noise);
 }
@@ -542,7 +486,7 @@ struct WaveRow {
     if (lane < n && rank < k) S.ranked[rank] = my;
     wave_lds_sync();
     const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
-    return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf, S.buf2,
+    return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf,
                      [&]() { return exact_lse<CPT, BF16>(ref(), M); });
   }
 
@@ -773,7 +717,7 @@ struct __align__(16) WideLds {
   uint64_t keys[WCAP + 2]; /* candidates, then zero pads for the pair reads */
   uint64_t ranked[WAVE];
   uint32_t hist[NB];
-  float buf[WAVE], buf2[WAVE];
+  float buf[WAVE];
   float wmax[WIDE_NW], wsum[WIDE_NW];
   uint32_t wcnt[WIDE_NW];
   uint32_t exact;
@@ -813,7 +757,7 @@ __device__ __forceinline__ void wide_finish(const SampleArgs &a, int row, WideLd
    * the fast lse cannot settle samples the row again by the generic procedure */
   if (wid == 0) {
     const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
-    const int id = wave_tail(a, row, key, M, lse, false, eps_s, noise, top_p, S.buf, S.buf2,
+    const int id = wave_tail(a, row, key, M, lse, false, eps_s, noise, top_p, S.buf,
                              []() { return __builtin_nanf(""); });
     if (id == NEED_EXACT && lane == 0) S.exact = 1u;
   }
