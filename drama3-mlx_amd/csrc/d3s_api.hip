@@ -17,6 +17,14 @@
 #include "../../include/d3s_sampler.h"
 #include "d3s_internal.h"
 
+/* The allocation-free entry point's scratch: one block per GPU the library
+ * runs on, held until the process ends.  Host code never uses this name as
+ * an address (it is a host-side stand-in): each device's address comes from
+ * hipGetSymbolAddress, taken once per device with that device current.  It
+ * starts zero (the segmented kernel's arrival counters must) and every
+ * segmented launch leaves its counters zero again. */
+static __device__ __align__(256) unsigned char scratch[D3S_SCRATCH_BYTES];
+
 namespace d3s {
 
 namespace {
@@ -54,16 +62,49 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
 
 namespace {
 
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[MAX_DEVICES]; /* each device's address of `scratch`, null until taken */
+
+/* the current device's address of the scratch array (null on failure) */
+void *device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 /* set, with any value, as src/sampling.c:197 tests it */
 bool env_no_fused() { return getenv("D3_NO_FUSED_SAMPLER") != nullptr; }
 
 int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
 
-/* the first kernel that holds the row: one wave, the fused workgroup (kernel
- * order only), the wide workgroup, the nucleus kernel, else the streaming one */
-int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s) {
+/* launches of at most this many segment workgroups take the segmented kernel */
+constexpr int64_t SPLIT_MAX_BLOCKS = 4096;
+
+/* the first kernel that holds the row: one wave, the rows cut into segments
+ * over many CUs (with a workspace), the fused workgroup (kernel order only),
+ * the wide workgroup, the nucleus kernel, else the streaming one.  ws: the
+ * workspace for the segmented kernel, or null to take the stream's (allocated
+ * on first use); ws_bytes its size. */
+int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s, void *ws = nullptr,
+                  size_t ws_bytes = 0, bool stream_ws = true) {
   const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
   if (!generic && d3s::launch_wave(a, dt, s)) return launched();
+  const int nseg = generic ? 0 : d3s::split_segments(a, dt);
+  if (nseg > 0 && (int64_t)a.n_rows * nseg <= SPLIT_MAX_BLOCKS) {
+    const size_t need = d3s::split_workspace_bytes(a, dt);
+    if (!ws && stream_ws) {
+      ws = d3s::stream_workspace(s, need);
+      ws_bytes = ws ? need : 0;
+    }
+    if (ws && d3s::launch_split(a, dt, ws, ws_bytes, s)) return launched();
+  }
   if (!generic && !a.opgraph && d3s::launch_fused(a, dt, s)) return launched();
   if (!generic && d3s::launch_wide(a, dt, s)) return launched();
   if (!generic && d3s::launch_topp(a, dt, s)) return launched();
@@ -71,15 +112,12 @@ int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s) {
   return launched();
 }
 
-}  // namespace
-
-extern "C" {
-
-int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
-               const float *u, int k, const float *temperature, const float *top_p,
-               float temperature_scalar, float top_p_scalar, const int32_t *banned,
-               int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
-               void *stream) {
+/* d3s_sample's checks and routing; no_alloc: the segmented kernel's records
+ * go to the fixed per-device scratch instead of the stream's workspace */
+int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                const float *u, int k, const float *temperature, const float *top_p, float temperature_scalar,
+                float top_p_scalar, const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
+                uint32_t *counters, unsigned flags, void *stream, bool no_alloc) {
   if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;
   if (n_rows < 0 || n_rows > 0x7fffffff || vocab < 1 || vocab > (1 << 26) ||
       row_stride < vocab || k < 1 || k > vocab)
@@ -110,7 +148,37 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
   a.flags = flags;
   a.opgraph = d3s::op_graph_order(a.vocab, k, (flags & D3S_FLAG_OP_GRAPH) || env_no_fused());
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
-  return sample_routed(a, dt, (hipStream_t)stream);
+  if (!no_alloc) return sample_routed(a, dt, (hipStream_t)stream);
+  void *ws = nullptr;
+  const int nseg = (flags & D3S_FLAG_GENERIC) ? 0 : d3s::split_segments(a, dt);
+  if (nseg > 0 && (int64_t)a.n_rows * nseg <= SPLIT_MAX_BLOCKS) { /* the segmented kernel takes it */
+    if (d3s::split_workspace_bytes(a, dt) > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
+    ws = device_scratch();
+    if (!ws) return D3S_ERR_LAUNCH;
+  }
+  return sample_routed(a, dt, (hipStream_t)stream, ws, D3S_SCRATCH_BYTES, false);
+}
+
+}  // namespace
+
+extern "C" {
+
+int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+               const float *u, int k, const float *temperature, const float *top_p,
+               float temperature_scalar, float top_p_scalar, const int32_t *banned,
+               int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+               void *stream) {
+  return sample_call(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, temperature_scalar,
+                     top_p_scalar, banned, ids, probs, cand, counters, flags, stream, false);
+}
+
+int d3s_sample_noalloc(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                       const float *u, int k, const float *temperature, const float *top_p,
+                       float temperature_scalar, float top_p_scalar, const int32_t *banned,
+                       int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+                       void *stream) {
+  return sample_call(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, temperature_scalar,
+                     top_p_scalar, banned, ids, probs, cand, counters, flags, stream, true);
 }
 
 int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
@@ -168,14 +236,22 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
    * draw's indices go to first_idx or else main_tok (the pick reads each row's
    * before it writes it); the retry's to retry_idx or else the workspace. */
   if (r.first.k > d3s_max_k() || r.retry.k > d3s_max_k()) return D3S_ERR_UNSUPPORTED;
+  /* one workspace block: the segmented kernel's records and counters first
+   * (both draws use them in turn), then the retry's indices */
+  size_t split_bytes = d3s::split_workspace_bytes(r.first, dt);
+  const size_t split_retry = d3s::split_workspace_bytes(r.retry, dt);
+  if (split_retry > split_bytes) split_bytes = split_retry;
+  split_bytes = (split_bytes + 255) & ~(size_t)255;
+  const size_t total = split_bytes + (retry_idx ? 0 : (size_t)n_rows * sizeof(int32_t));
+  void *ws = total ? d3s::stream_workspace(s, total) : nullptr;
+  if (total && !ws) return D3S_ERR_NOMEM;
   int32_t *fi = first_idx ? first_idx : main_tok;
-  int32_t *ri = retry_idx;
-  if (!ri) ri = (int32_t *)d3s::stream_workspace(s, (size_t)n_rows * sizeof(int32_t));
-  if (!ri) return D3S_ERR_NOMEM;
+  int32_t *ri = retry_idx ? retry_idx : (int32_t *)((char *)ws + split_bytes);
   r.first.ids = fi;
   r.retry.ids = ri;
-  int rc = sample_routed(r.first, dt, s);
-  if (rc == D3S_OK) rc = sample_routed(r.retry, dt, s);
+  void *split_ws = split_bytes ? ws : nullptr;
+  int rc = sample_routed(r.first, dt, s, split_ws, split_bytes, false);
+  if (rc == D3S_OK) rc = sample_routed(r.retry, dt, s, split_ws, split_bytes, false);
   if (rc != D3S_OK) return rc;
   d3s::launch_ras_select(r, fi, ri, s);
   return launched();

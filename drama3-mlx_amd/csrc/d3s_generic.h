@@ -27,14 +27,16 @@ __device__ __forceinline__ float load_logit(const void *rowp, int i, int banned)
   return i == banned ? -__builtin_inff() : v;
 }
 
-/* exclusive block scan of per-thread counts in thread order; `tot` = total */
+/* exclusive block scan of per-thread counts in thread order (NW waves);
+ * `tot` = total */
+template <int NW>
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t *sh, uint32_t &tot) {
   const int lane = lane_id(), wid = threadIdx.x / WAVE;
   const uint32_t incl = wave_scan_add_u32(v);
   if (lane == WAVE - 1) sh[wid] = incl;
   __syncthreads();
   uint32_t wbase = 0u, t = 0u;
-  for (int w = 0; w < GNW; w++) {
+  for (int w = 0; w < NW; w++) {
     const uint32_t x = sh[w];
     if (w < wid) wbase += x;
     t += x;
@@ -45,6 +47,7 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t *sh
 }
 
 /* the same for per-thread fixed-point sums below 2^45 (split in 24-bit parts) */
+template <int NW>
 __device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint32_t *sh_lo, uint32_t *sh_hi) {
   const int lane = lane_id(), wid = threadIdx.x / WAVE;
   const uint32_t lo = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
@@ -71,12 +74,13 @@ __device__ __forceinline__ int wave_min_i32(int v) {
   return (int)readlane_u((uint32_t)v, 63);
 }
 
-/* Row `row` by the whole 1024-thread workgroup; glist: LDS for kpow >= k
- * composite keys (kpow a power of two).  Every thread of the workgroup calls
- * it and returns from it. */
-template <bool BF16>
+/* Row `row` by the whole BLOCK-thread workgroup (BLOCK a multiple of 256);
+ * glist: LDS for kpow >= k composite keys (kpow a power of two).  Every thread
+ * of the workgroup calls it and returns from it. */
+template <bool BF16, int BLOCK = GBLOCK>
 __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, const int kpow,
                                             uint64_t *glist) {
+  constexpr int GBLOCK = BLOCK, GNW = BLOCK / WAVE;
   __shared__ uint32_t hist[NB];
   __shared__ float sh_max[GNW];
   __shared__ uint32_t sh_flag[GNW], sh_u32[GNW], sh_lo[GNW], sh_hi[GNW];
@@ -179,7 +183,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
         tie = d3s_ordkey(xi) == prefix;
       }
       uint32_t tot;
-      const uint32_t ord = base + block_excl_scan_u32(tie, sh_u32, tot);
+      const uint32_t ord = base + block_excl_scan_u32<GNW>(tie, sh_u32, tot);
       if (tie && ord < need) {
         const int slot = atomicAdd(&n_gather, 1);
         if (slot < kpow) glist[slot] = composite_key(xi, i);
@@ -230,7 +234,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
     const int r = r0 + q;
     if (r < k) loc += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
   }
-  uint64_t P = block_excl_scan_u64(loc, sh_lo, sh_hi);
+  uint64_t P = block_excl_scan_u64<GNW>(loc, sh_lo, sh_hi);
   int cut_local = k;
   for (int q = 0; q < R; q++) {
     const int r = r0 + q;

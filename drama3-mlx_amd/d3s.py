@@ -21,6 +21,8 @@ FLAG_OP_GRAPH = 8
 COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
 NUM_COUNTERS = 4
 OK = 0
+ERR_SCRATCH = -6
+SCRATCH_BYTES = 4 << 20
 
 _lib = None
 
@@ -54,6 +56,9 @@ def lib():
         L.d3s_sample.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
                                  vp, u32, vp]
         L.d3s_sample.restype = i32
+        L.d3s_sample_noalloc.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
+                                         vp, u32, vp]
+        L.d3s_sample_noalloc.restype = i32
         L.d3s_sample_ras.argtypes = [vp, i32, i64, i64, i64, vp, vp, vp, i32,
                                      ctypes.POINTER(RasParams), vp, vp, vp, vp, vp, vp]
         L.d3s_sample_ras.restype = i32

@@ -8,7 +8,9 @@
  *     src/mlxu.c:771-774), as d3s_uniform_fill.
  * Plain pointers and sizes only; every pointer argument is device memory (or
  * memory the device can read); `stream` is a hipStream_t (NULL: the null stream).
- * Calls enqueue work and return; nothing here allocates device memory.
+ * Calls enqueue work and return.  d3s_sample allocates device memory only on a
+ * stream's first call that needs its workspace (rows spread over several CUs)
+ * and keeps it for that stream; d3s_sample_noalloc never allocates.
  */
 #ifndef D3S_SAMPLER_H
 #define D3S_SAMPLER_H
@@ -29,6 +31,10 @@ extern "C" {
 #define D3S_ERR_LAUNCH -3      /* the HIP launch failed */
 #define D3S_ERR_DTYPE -4       /* unknown logits dtype */
 #define D3S_ERR_NOMEM -5       /* the library's workspace could not be allocated */
+#define D3S_ERR_SCRATCH -6     /* d3s_sample_noalloc: the call needs more than D3S_SCRATCH_BYTES */
+
+/* the fixed device scratch of d3s_sample_noalloc, per GPU */
+#define D3S_SCRATCH_BYTES (4u << 20)
 
 /* flags for d3s_sample */
 #define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the same results) */
@@ -76,6 +82,24 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
                float temperature_scalar, float top_p_scalar, const int32_t *banned,
                int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
                void *stream);
+
+/* d3s_sample without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid it).  No counterpart in the reference.  Same arguments, results and
+ * status codes as d3s_sample; the scratch that d3s_sample takes from a
+ * per-stream workspace (allocated on a stream's first call that needs it:
+ * the records and arrival counters of the kernel that spreads a wide row over
+ * several CUs) comes instead from one fixed block of D3S_SCRATCH_BYTES per GPU,
+ * in the library's static device memory, held until the process ends.  Every
+ * call the segmented kernel takes fits (it takes at most 4096 segments per
+ * launch, at most 2.4 MB); a call that would not returns D3S_ERR_SCRATCH.
+ * All calls on one GPU share that block: calls that overlap on one GPU
+ * (several streams or threads at once) race and must not be issued. */
+int d3s_sample_noalloc(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                       const float *u, int k, const float *temperature, const float *top_p,
+                       float temperature_scalar, float top_p_scalar, const int32_t *banned,
+                       int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+                       void *stream);
 
 /* Parameters of d3s_sample_ras: the first draw (SamplingParams, src/model.h:146-149),
  * the retry (RAS_TEMPERATURE / RAS_TOP_K / RAS_TOP_P, src/tower.c:13-16: 1.0, 30,

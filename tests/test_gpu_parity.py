@@ -364,6 +364,78 @@ def test_wide_kernel_on_many_rows(gpu, oracle, bf16):
     compare(oracle, gpu, xs, u, 0.8, 0.9, label=f"wide kernel, {N} rows bf16={bf16}")
 
 
+@pytest.mark.parametrize("V,bf16,N", [(8190, False, 20), (16381, False, 12), (16382, True, 9),
+                                      (131069, False, 4), (262137, True, 3), (262138, True, 2),
+                                      (40000, True, 40)])
+def test_segmented_rows(gpu, oracle, V, bf16, N):
+    """Rows cut into segments of 2048 chunks (2 to 16 per row, and one past the
+    most: the generic kernel), with structure across segments: the top k at
+    segment bounds, a NaN in the last segment, a segment all -inf, the banned
+    index at a bound, fewer finite elements than k, per-row T and top_p;
+    against the oracle and the generic kernel."""
+    rng = np.random.default_rng([V, 91])
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    seg = 8192 * (2 if bf16 else 1)  # elements per segment (at offset 0)
+    bounds = np.arange(seg, V, seg)
+    if N > 1 and len(bounds):
+        x[1, np.clip(np.concatenate([bounds - 1, bounds]), 0, V - 1)] += 9.0
+    if N > 2:
+        x[2, V - 2] = np.nan
+    if N > 3:
+        x[3, : min(V, seg)] = -np.inf
+    if N > 4:
+        x[4, :] = -np.inf
+        x[4, [0, V // 2, V - 1]] = 1.0
+    ban = np.full(N, -1, np.int32)
+    if len(bounds):
+        ban[0] = int(bounds[0])
+        x[0, bounds[0]] = 40.0
+    T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    u = oracle.uniform(91, 0, N, 30)
+    xs = W.f32_to_bf16_bits(x) if bf16 else x
+    got, _ = compare(oracle, gpu, xs, u, T, top_p, banned=ban, label=f"segmented V={V} bf16={bf16}")
+    if N > 2:
+        assert got["ids"][2] == -1
+    compare(oracle, gpu, xs, u, T, top_p, banned=ban, flags=gpu.FLAG_GENERIC,
+            label=f"segmented V={V}, generic kernel")
+
+
+@pytest.mark.parametrize("V,bf16", [(300, False), (4097, False), (4097, True), (20000, False), (100000, True)])
+def test_top_k_reaching_minus_inf_x(gpu, oracle, V, bf16):
+    """T at its 1e-5 clamp: 10 logits near 0 give finite x, 25 logits of -1e35
+    overflow to x = -inf, every other logit is -inf (masked), among them the
+    lowest indices.  The top 30 end in 20 ties at x = -inf, ranked by index,
+    where the masked logits come first: the candidates a threshold on the
+    logits files (the -1e35 ones) are not those ties.  Every route against the
+    oracle."""
+    rng = np.random.default_rng([V, 57])
+    N = 6
+    x = np.full((N, V), -np.inf, np.float32)
+    for r in range(N):
+        pos = rng.choice(np.arange(V // 3, V), 35, replace=False)
+        x[r, pos[:10]] = rng.standard_normal(10).astype(np.float32)
+        x[r, pos[10:]] = -1e35 if not bf16 else -9.9e34
+    u = oracle.uniform(57, 0, N, 30)
+    xs = W.f32_to_bf16_bits(x) if bf16 else x
+    for top_p in (2.0, 0.9):
+        got, exp = compare(oracle, gpu, xs, u, 0.0, top_p, label=f"-inf ties V={V} bf16={bf16}")
+        assert np.all(np.isneginf(np.float32(x[0, exp["cand"][0, 10:]])))  # masked logits rank there
+        compare(oracle, gpu, xs, u, 0.0, top_p, flags=gpu.FLAG_GENERIC, label=f"-inf ties V={V} generic")
+
+
+def test_wide_kernel_past_the_segment_limit(gpu, oracle):
+    """A launch of more segments than the segmented kernel takes at once (600
+    rows of 9 segments): one workgroup per row (the wide kernel)."""
+    rng = np.random.default_rng(46)
+    N, V = 600, 70000
+    x = (rng.standard_normal((N, V)) * 3).astype(np.float32)
+    x[np.arange(N), rng.integers(0, V, N)] += 7.0
+    u = oracle.uniform(46, 0, N, 30)
+    T = rng.uniform(0.6, 1.2, N).astype(np.float32)
+    compare(oracle, gpu, x, u, T, 0.9, label=f"wide kernel, {N} rows")
+
+
 def test_wide_top_p_on_a_cumulative_boundary(gpu, oracle):
     """top_p one ulp either side of a row's own cumulative value: every row is
     within the fast sum's margin and takes the exact fallback."""
