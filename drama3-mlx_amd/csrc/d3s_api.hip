@@ -84,9 +84,6 @@ bool env_no_fused() { return getenv("D3_NO_FUSED_SAMPLER") != nullptr; }
 
 int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
 
-/* launches of at most this many segment workgroups take the segmented kernel */
-constexpr int64_t SPLIT_MAX_BLOCKS = 4096;
-
 /* the first kernel that holds the row: one wave, the rows cut into segments
  * over many CUs (with a workspace), the fused workgroup (kernel order only),
  * the wide workgroup, the nucleus kernel, else the streaming one.  ws: the
@@ -96,8 +93,7 @@ int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s, void *
                   size_t ws_bytes = 0, bool stream_ws = true) {
   const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
   if (!generic && d3s::launch_wave(a, dt, s)) return launched();
-  const int nseg = generic ? 0 : d3s::split_segments(a, dt);
-  if (nseg > 0 && (int64_t)a.n_rows * nseg <= SPLIT_MAX_BLOCKS) {
+  if (!generic && d3s::split_segments(a, dt) > 0) {
     const size_t need = d3s::split_workspace_bytes(a, dt);
     if (!ws && stream_ws) {
       ws = d3s::stream_workspace(s, need);
@@ -150,8 +146,7 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
   if (!no_alloc) return sample_routed(a, dt, (hipStream_t)stream);
   void *ws = nullptr;
-  const int nseg = (flags & D3S_FLAG_GENERIC) ? 0 : d3s::split_segments(a, dt);
-  if (nseg > 0 && (int64_t)a.n_rows * nseg <= SPLIT_MAX_BLOCKS) { /* the segmented kernel takes it */
+  if (!(flags & D3S_FLAG_GENERIC) && d3s::split_segments(a, dt) > 0) { /* the segmented kernel takes it */
     if (d3s::split_workspace_bytes(a, dt) > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
     ws = device_scratch();
     if (!ws) return D3S_ERR_LAUNCH;
@@ -236,20 +231,22 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
    * draw's indices go to first_idx or else main_tok (the pick reads each row's
    * before it writes it); the retry's to retry_idx or else the workspace. */
   if (r.first.k > d3s_max_k() || r.retry.k > d3s_max_k()) return D3S_ERR_UNSUPPORTED;
-  /* one workspace block: the segmented kernel's records and counters first
-   * (both draws use them in turn), then the retry's indices */
+  /* one workspace block: the segmented kernel's counters and records first
+   * (both draws use them in turn), then the retry's indices, never on the
+   * counters (which must stay zero for later launches on this stream) */
   size_t split_bytes = d3s::split_workspace_bytes(r.first, dt);
   const size_t split_retry = d3s::split_workspace_bytes(r.retry, dt);
   if (split_retry > split_bytes) split_bytes = split_retry;
+  if (split_bytes < d3s::split_counter_bytes()) split_bytes = d3s::split_counter_bytes();
   split_bytes = (split_bytes + 255) & ~(size_t)255;
   const size_t total = split_bytes + (retry_idx ? 0 : (size_t)n_rows * sizeof(int32_t));
-  void *ws = total ? d3s::stream_workspace(s, total) : nullptr;
-  if (total && !ws) return D3S_ERR_NOMEM;
+  void *ws = d3s::stream_workspace(s, total);
+  if (!ws) return D3S_ERR_NOMEM;
   int32_t *fi = first_idx ? first_idx : main_tok;
   int32_t *ri = retry_idx ? retry_idx : (int32_t *)((char *)ws + split_bytes);
   r.first.ids = fi;
   r.retry.ids = ri;
-  void *split_ws = split_bytes ? ws : nullptr;
+  void *split_ws = ws;
   int rc = sample_routed(r.first, dt, s, split_ws, split_bytes, false);
   if (rc == D3S_OK) rc = sample_routed(r.retry, dt, s, split_ws, split_bytes, false);
   if (rc != D3S_OK) return rc;

@@ -109,7 +109,7 @@ bool launch_wide(const SampleArgs &a, Dtype dt, hipStream_t s);
 int wide_max_vocab(Dtype dt);
 /* Launch the segmented kernel: rows cut into segments of 4 waves, every
  * segment one workgroup, the last to arrive merging the row (k <= 64, rows of
- * 2 to 16 segments).  ws: device memory of ws_bytes for the records and the
+ * 2 to 16 segments, at most 4096 segments a launch).  ws: device memory of ws_bytes for the records and the
  * arrival counters (counters zero on entry; the kernel leaves them zero).
  * Returns false (nothing launched) when the row does not fit or ws is too
  * small. */
@@ -118,6 +118,9 @@ bool launch_split(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipS
  * take them), and the workspace it needs */
 int split_segments(const SampleArgs &a, Dtype dt);
 size_t split_workspace_bytes(const SampleArgs &a, Dtype dt);
+/* the workspace's first bytes: the segmented kernel's arrival counters, which
+ * must stay zero between launches (nothing else may be placed there) */
+size_t split_counter_bytes();
 /* Launch the fused one-workgroup-per-row kernel (k <= 64, V within the
  * register-resident limit).  Returns false if no instantiation fits. */
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);

@@ -29,6 +29,11 @@ constexpr int SPLIT_CPT = 8;             /* 16-byte chunks per lane */
 constexpr int SPLIT_T = SPLIT_NW * WAVE; /* threads per segment */
 constexpr int SCAP = SPLIT_T;            /* candidates a segment ranks (one per thread) */
 constexpr int SPLIT_MAX_SEG = 16;        /* segments per row */
+constexpr int SPLIT_MAX_BLOCKS = 4096;   /* segments per launch */
+/* The workspace: arrival counters (one per 128 bytes) for the most rows a
+ * launch can have, then the records.  The counters' place never depends on
+ * the launch, so records of one launch never land on another's counters. */
+constexpr size_t SPLIT_CNT_BYTES = (size_t)(SPLIT_MAX_BLOCKS / 2) * 128;
 constexpr int MCAP = SPLIT_MAX_SEG * KF; /* keys the merger ranks */
 
 /* record flags */
@@ -36,15 +41,18 @@ constexpr uint32_t SEG_GENERIC = 1u;  /* T not finite or logits too large: the g
 constexpr uint32_t SEG_OVERFLOW = 2u; /* more candidates than the segment files (or forced) */
 
 struct __align__(16) SplitLds {
-  uint64_t keys[MCAP + 2]; /* a segment's candidates; the merger's keys (+ zero pads) */
+  uint64_t keys[MCAP + 2]; /* a segment's candidates; the merger's keys at or above its cut (+ zero pads) */
+  uint64_t kth[SPLIT_MAX_SEG]; /* the merger's k-th key of each segment */
+  uint64_t kc[SPLIT_MAX_SEG];  /* the merger's ceil(k / nseg)-th key of each segment */
   uint64_t ranked[KF];
-  uint32_t hist[NB];
+  uint32_t lk[SPLIT_T];        /* order keys of the lane maxima */
   float buf[WAVE];
   float wmax[SPLIT_NW], wsum[SPLIT_NW];
-  uint32_t wcnt[SPLIT_NW];
+  uint32_t wpre[SPLIT_NW];
+  uint32_t ncand; /* a segment's candidates filed */
   float smax[SPLIT_MAX_SEG], ssum[SPLIT_MAX_SEG];
   uint32_t sflags[SPLIT_MAX_SEG], sn[SPLIT_MAX_SEG];
-  uint32_t last, exact;
+  uint32_t last, exact, mcount;
   uint32_t slo[SPLIT_NW], shi[SPLIT_NW];
 };
 
@@ -78,26 +86,85 @@ __device__ __forceinline__ float split_exact_lse(const SampleArgs &a, int row, f
   return M + d3s_logf(d3s_fixsum_to_f32(tot));
 }
 
-/* rank the n keys in S.keys (n <= cap): every key counts the keys above its
- * own; those below k land in S.ranked by rank.  Called by every thread. */
-__device__ __forceinline__ void split_rank(SplitLds &S, uint32_t n, int k) {
+/* rank the n keys of list (n + 2 entries of room): every key counts the keys
+ * above its own; those below k land in ranked by rank.  Keys are distinct.
+ * G adjacent lanes share a key (G = 4 when n <= SPLIT_T / 4, 2 when n <=
+ * SPLIT_T / 2), each counting a share of the list; quad DPP adds the shares.
+ * Called by every thread. */
+__device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k, uint64_t *ranked) {
   if (threadIdx.x == 0) {
-    S.keys[n] = 0ull; /* pads below every key */
-    S.keys[n + 1] = 0ull;
+    list[n] = 0ull; /* pads below every key */
+    list[n + 1] = 0ull;
   }
   __syncthreads();
-  const ulonglong2 *k2 = (const ulonglong2 *)S.keys;
-  for (uint32_t t = threadIdx.x; t < n; t += SPLIT_T) {
-    const uint64_t my = S.keys[t];
-    int rank = 0;
+  const ulonglong2 *k2 = (const ulonglong2 *)list;
+  const uint32_t lg = n <= SPLIT_T / 4 ? 2u : n <= SPLIT_T / 2 ? 1u : 0u; /* log2 G */
+  const uint32_t np = (n + 1) / 2;                                         /* pairs */
+  const uint32_t share = (np + (1u << lg) - 1) >> lg;
+  const uint32_t part = threadIdx.x & ((1u << lg) - 1);
+  const uint32_t p0 = min(np, part * share), p1 = min(np, p0 + share);
+  for (uint32_t base = 0; base < n; base += SPLIT_T >> lg) {
+    const uint32_t t = base + (threadIdx.x >> lg);
+    const uint64_t my = t < n ? list[t] : ~0ull;
+    uint32_t rank = 0u;
 #pragma unroll 4
-    for (int j2 = 0; j2 < (int)(n + 1) / 2; j2++) {
+    for (uint32_t j2 = p0; j2 < p1; j2++) {
       const ulonglong2 q = k2[j2];
-      rank += (q.x > my ? 1 : 0) + (q.y > my ? 1 : 0);
+      rank += (q.x > my ? 1u : 0u) + (q.y > my ? 1u : 0u);
     }
-    if (rank < k) S.ranked[rank] = my;
+    if (lg >= 1) rank += dpp_u<0xb1, 0xf>(0u, rank); /* quad_perm [1,0,3,2] */
+    if (lg >= 2) rank += dpp_u<0x4e, 0xf>(0u, rank); /* quad_perm [2,3,0,1] */
+    if (part == 0 && t < n && rank < (uint32_t)k) ranked[rank] = my;
   }
   __syncthreads();
+}
+
+/* the k-th largest of the wave's lane keys to 20 bits (the largest prefix that
+ * at least k lanes reach; 0 when fewer than k lanes hold a key), by ballot
+ * radix search; wave-uniform */
+__device__ __forceinline__ uint32_t wave_kth_prefix(uint32_t key, uint32_t k) {
+  uint32_t pre = 0u;
+#pragma unroll
+  for (int bit = 31; bit >= 12; bit--) {
+    const uint32_t cnd = pre | (1u << bit);
+    if ((uint32_t)__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
+  }
+  return pre;
+}
+
+/* the same over the SPLIT_T keys of a workgroup held in LDS, by every wave */
+__device__ __forceinline__ uint32_t group_kth_prefix(const uint32_t *keys, uint32_t k) {
+  const int lane = lane_id();
+  uint32_t kk[SPLIT_NW];
+#pragma unroll
+  for (int w = 0; w < SPLIT_NW; w++) kk[w] = keys[w * WAVE + lane];
+  uint32_t pre = 0u;
+#pragma unroll
+  for (int bit = 31; bit >= 12; bit--) {
+    const uint32_t cnd = pre | (1u << bit);
+    uint32_t c = 0u;
+#pragma unroll
+    for (int w = 0; w < SPLIT_NW; w++) c += (uint32_t)__popcll(__ballot(kk[w] >= cnd));
+    if (c >= k) pre = cnd;
+  }
+  return pre;
+}
+
+/* wave maximum of 64-bit values (the high words, then the low words of the
+ * lanes that hold the highest); wave-uniform */
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  auto wmax = [](uint32_t x) {
+    x = max(x, dpp_u<DPP_SHR1, 0xf>(0u, x));
+    x = max(x, dpp_u<DPP_SHR2, 0xf>(0u, x));
+    x = max(x, dpp_u<DPP_SHR4, 0xf>(0u, x));
+    x = max(x, dpp_u<DPP_SHR8, 0xf>(0u, x));
+    x = max(x, dpp_u<DPP_BCAST15, 0xa>(0u, x));
+    x = max(x, dpp_u<DPP_BCAST31, 0xc>(0u, x));
+    return readlane_u(x, 63);
+  };
+  const uint32_t hi = wmax((uint32_t)(v >> 32));
+  const uint32_t lo = wmax((uint32_t)(v >> 32) == hi ? (uint32_t)v : 0u);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 template <int CPT, bool BF16>
@@ -106,7 +173,6 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   using C = Chunks<CPT, BF16>;
   constexpr int ES = BF16 ? 2 : 4, EPC = C::EPC, NV = C::NV;
   constexpr int CAP = SPLIT_NW * CPT * WAVE; /* chunks per segment */
-  constexpr int EARLY = 3;
   __shared__ SplitLds S;
   __shared__ uint64_t glist[KF]; /* the generic procedure's sort list */
   const int row = (int)blockIdx.x / nseg, seg = (int)blockIdx.x % nseg;
@@ -124,15 +190,20 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   const int off = (int)(((uintptr_t)rowp & 15u) / ES);
   const uint4 *src = (const uint4 *)(rowp - off * ES);
   const int nchunks = (off + V + EPC - 1) / EPC;
-  const int cbase = seg * CAP + wid * CPT * WAVE; /* this wave's first chunk */
+  /* the row's chunks in nseg equal parts (at most CAP each): every wave of a
+   * segment holds logits, the last segment as much as the others */
+  const int segc = (nchunks + nseg - 1) / nseg;
+  const int cend = min(nchunks, (seg + 1) * segc);    /* past the segment's last chunk */
+  const int cbase = seg * segc + wid * CPT * WAVE;    /* this wave's first chunk */
+  const int vend = min(V, cend * EPC - off);          /* past the segment's last position */
   C c;
-  c.load(src + cbase, min(max(nchunks - cbase, 0), CPT * WAVE), lane);
+  c.load(src + cbase, min(max(cend - cbase, 0), CPT * WAVE), lane);
   const int pos0 = (cbase + lane) * EPC - off;
-  auto valid = [&](int i) { return (unsigned)C::pos(pos0, i) < (unsigned)V; };
+  auto valid = [&](int i) { return (unsigned)C::pos(pos0, i) < (unsigned)vend; };
 #pragma unroll
   for (int j = 0; j < CPT; j++) {
     const int p_lo = (cbase + j * WAVE) * EPC - off; /* wave-uniform */
-    if (p_lo < 0 || p_lo + WAVE * EPC > V) {
+    if (p_lo < 0 || p_lo + WAVE * EPC > vend) {
 #pragma unroll
       for (int e = 0; e < EPC; e++) c.mask(j * EPC + e, !valid(j * EPC + e));
     }
@@ -150,19 +221,38 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
     }
   }
 
-  /* ---- the segment's max of the logits; NaN propagates */
+  /* ---- each chunk's max, the segment's max (NaN propagates) and, per wave,
+   * the ceil(k / SPLIT_NW)-th largest of its lane maxima */
   const float ninf = -__builtin_inff();
+  float cm[CPT];
   float lm = ninf;
 #pragma unroll
-  for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
+  for (int j = 0; j < CPT; j++) {
+    float m = c.val(j * EPC);
+#pragma unroll
+    for (int e = 1; e < EPC; e++) m = fmaximum(m, c.val(j * EPC + e));
+    cm[j] = m;
+    lm = fmaximum(lm, m);
+  }
+  const uint32_t lkey = d3s_ordkey(lm);
   {
     const float wm = wave_maximum_f(lm);
-    if (lane == 0) S.wmax[wid] = wm;
+    const uint32_t wp = wave_kth_prefix(lkey, (uint32_t)(k + SPLIT_NW - 1) / SPLIT_NW);
+    if (lane == 0) {
+      S.wmax[wid] = wm;
+      S.wpre[wid] = wp;
+    }
+    S.lk[threadIdx.x] = lkey;
+    if (threadIdx.x == 0) S.ncand = 0u;
   }
   __syncthreads();
   float Ls = S.wmax[0];
+  uint32_t prefix = S.wpre[0];
 #pragma unroll
-  for (int w = 1; w < SPLIT_NW; w++) Ls = fmaximum(Ls, S.wmax[w]);
+  for (int w = 1; w < SPLIT_NW; w++) {
+    Ls = fmaximum(Ls, S.wmax[w]);
+    prefix = min(prefix, S.wpre[w]);
+  }
   uint32_t flags = 0u, nfiled = 0u;
   float ssum = 0.0f;
   const float cf = LOG2E_F / T;
@@ -173,23 +263,12 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   }
   if (live && flags == 0u) {
     const float b = -(Ls * cf);
-    /* ---- tau: the k-th largest of the segment's lane maxima to 16 bits of
-     * its order key (a lower bound: at least k elements reach it) */
-    const uint32_t lkey = d3s_ordkey(lm);
-    uint32_t prefix = 0u, pmask = 0u, need = (uint32_t)k;
-#pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-      const int shift = 24 - 8 * pass;
-      S.hist[threadIdx.x] = 0u; /* SPLIT_T == NB */
-      __syncthreads();
-      if ((lkey & pmask) == prefix) atomicAdd(&S.hist[(lkey >> shift) & 255u], 1u);
-      __syncthreads();
-      const BinSel bs = wave_find_bin<false>(S.hist, need); /* 256 keys >= need */
-      prefix |= bs.bin << shift;
-      pmask |= 0xffu << shift;
-      need -= bs.above;
-      __syncthreads(); /* every wave has read the histogram */
-    }
+    /* ---- tau, a lower bound with at least k elements reaching it: the least
+     * of the waves' prefixes (SPLIT_NW ceil(k / SPLIT_NW) >= k lane maxima
+     * reach it).  When a wave holds fewer finite lane maxima than its share
+     * (a segment past the row's end, or -inf logits), the k-th largest of all
+     * the segment's lane maxima instead. */
+    if (prefix < d3s_ordkey(-0x1.fffffep127f)) prefix = group_kth_prefix(S.lk, (uint32_t)k);
     bool over = (a.flags & FLAG_EXACT_SELECT) != 0;
     /* below every logit whose x ties with tau's (as in the one-wave kernel);
      * when the k-th lane max is -inf, every finite logit is a candidate (a
@@ -200,60 +279,13 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
     /* a threshold at -inf would take masked padding for candidates */
     if (!(tau_lo >= -0x1.fffffep127f)) over = true;
 
-    /* ---- the candidates as a bit per element, no branches */
-    if (BF16) c.launder();
-    constexpr int NWORD = (NV + 31) / 32;
-    uint32_t bits[NWORD];
+    /* ---- the candidate chunks (their max reaches tau_lo), one bit each */
+    uint32_t cb = 0u;
 #pragma unroll
-    for (int w = 0; w < NWORD; w++) bits[w] = 0u;
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-      asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-          : "+v"(bits[i / 32])
-          : "v"(c.val(i)), "v"(tau_lo)
-          : "vcc");
-    }
-    if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
-    int cnt = 0;
-#pragma unroll
-    for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
-    const uint32_t wtot = wave_sum_u32((uint32_t)cnt);
-    over = over || __ballot(cnt > LCAP) != 0ull;
-    auto next_cand = [&]() {
-      int i = 0;
-      bool found = false;
-#pragma unroll
-      for (int w = 0; w < NWORD; w++) {
-        const int e = __builtin_clz(bits[w] | 1u); /* bits[w] != 0 below */
-        const bool here = !found && bits[w] != 0u;
-        i = here ? 32 * w + e : i;
-        bits[w] = here ? bits[w] & ~(0x80000000u >> e) : bits[w];
-        found = found || here;
-      }
-      return C::pos(pos0, i);
-    };
-    auto read_logit = [&](int p) {
-      return BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[p]) : ((const float *)rowp)[p];
-    };
-    /* the first candidates read again now, while the segment is in L2 */
-    int cpos[EARLY];
-    float cl[EARLY];
-#pragma unroll
-    for (int q = 0; q < EARLY; q++) {
-      cpos[q] = 0;
-      cl[q] = 0.0f;
-    }
-    if (!over) {
-#pragma unroll
-      for (int q = 0; q < EARLY; q++) {
-        if (q > 0 && !__ballot(q < cnt)) break;
-        cpos[q] = next_cand();
-        if (q < cnt) cl[q] = read_logit(cpos[q]);
-      }
-    }
+    for (int j = 0; j < CPT; j++) cb |= (cm[j] >= tau_lo ? 1u : 0u) << j;
+    if (over) cb = 0u;
 
     /* ---- the segment's fast sum, relative to its own max */
-    if (BF16) c.launder();
     float acc[EPC];
 #pragma unroll
     for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
@@ -265,38 +297,54 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
       for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
     {
       const float ws = wave_sum_f(acc[0]);
-      if (lane == 0) {
-        S.wsum[wid] = ws;
-        S.wcnt[wid] = over ? 0xffffffffu : wtot;
+      if (lane == 0) S.wsum[wid] = ws;
+    }
+
+    /* ---- file the candidates: each candidate chunk (taken from the
+     * registers by selects) files its valid elements that reach tau_lo, at
+     * slots taken from an LDS counter */
+#pragma unroll 1
+    while (__ballot(cb != 0u)) {
+      const int jc = cb ? __builtin_ctz(cb) : CPT;
+      cb &= cb - 1u;
+      uint32_t qw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) qw[t] = jc == j ? c.w[4 * j + t] : qw[t];
+      const int pb = C::pos(pos0, jc * EPC); /* the chunk's first position */
+      float v[EPC];
+      uint32_t vm = 0u;
+#pragma unroll
+      for (int e = 0; e < EPC; e++) {
+        v[e] = BF16 ? d3s_u2f((e & 1) ? (qw[e / 2] & 0xffff0000u) : (qw[e / 2] << 16)) : d3s_u2f(qw[e]);
+        const bool ok = jc < CPT && v[e] >= tau_lo; /* masked elements hold -inf */
+        vm |= (ok ? 1u : 0u) << e;
       }
+      /* the logit's bits and its position; the keys are made after the loop,
+       * one per thread */
+      uint32_t slot = vm ? atomicAdd(&S.ncand, (uint32_t)__popc(vm)) : 0u;
+#pragma unroll
+      for (int e = 0; e < EPC; e++)
+        if ((vm >> e) & 1u) {
+          if (slot < (uint32_t)SCAP) S.keys[slot] = ((uint64_t)d3s_f2u(v[e]) << 32) | (uint32_t)(pb + e);
+          slot++;
+        }
     }
     __syncthreads();
-    uint32_t tot = 0u, base = 0u;
     ssum = S.wsum[0];
 #pragma unroll
-    for (int w = 0; w < SPLIT_NW; w++) {
-      const uint32_t t = S.wcnt[w];
-      over = over || t == 0xffffffffu;
-      base += w < wid ? t : 0u;
-      tot += t;
-      if (w > 0) ssum = ssum + S.wsum[w]; /* the same order in every wave */
-    }
-    over = over || tot > (uint32_t)SCAP;
-    if (over) {
+    for (int w = 1; w < SPLIT_NW; w++) ssum = ssum + S.wsum[w]; /* the same order in every wave */
+    const uint32_t tot = S.ncand;
+    if (over || tot > (uint32_t)SCAP) {
       flags |= SEG_OVERFLOW;
     } else {
-      /* ---- file the keys, rank them, keep the top k */
-      const uint32_t excl = base + wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
-#pragma unroll
-      for (int q = 0; q < EARLY; q++)
-        if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(cl[q], T, y, true), cpos[q]);
-#pragma unroll 1
-      for (int q = EARLY; q < LCAP; q++) {
-        if (!__ballot(q < cnt)) break;
-        const int p = next_cand();
-        if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(read_logit(p), T, y, true), p);
+      /* ---- the keys, one per thread; rank them, keep the top k */
+      if (threadIdx.x < tot) {
+        const uint64_t lp = S.keys[threadIdx.x];
+        S.keys[threadIdx.x] = composite_key(scale_logit(d3s_u2f((uint32_t)(lp >> 32)), T, y, true), (int)(uint32_t)lp);
       }
-      split_rank(S, tot, k);
+      rank_by_count(S.keys, tot, k, S.ranked);
       nfiled = min(tot, (uint32_t)k);
     }
   }
@@ -317,28 +365,59 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
     S.last = old == (uint32_t)(nseg - 1);
     if (S.last) __hip_atomic_store(cnt_row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     S.exact = 0u;
+    S.mcount = 0u;
   }
   __syncthreads();
   if (!S.last) return;
 
-  /* ---- the last arrival merges the row's records */
+  /* ---- the last arrival merges the row's records: every word of them read
+   * at once (one round trip), the key of rank r of segment s in slot q of
+   * thread t (t + q SPLIT_T = r SPLIT_MAX_SEG + s), the headers by the first
+   * 2 nseg threads; the uniforms of wave 0 as well */
   const uint64_t *rrow = records + (size_t)row * nseg * rec_words;
-  if (threadIdx.x < (unsigned)nseg) {
-    const uint64_t h0 = ld_agent(rrow + (size_t)threadIdx.x * rec_words);
-    const uint64_t h1 = ld_agent(rrow + (size_t)threadIdx.x * rec_words + 1);
-    S.smax[threadIdx.x] = d3s_u2f((uint32_t)h0);
-    S.ssum[threadIdx.x] = d3s_u2f((uint32_t)(h0 >> 32));
-    S.sflags[threadIdx.x] = (uint32_t)h1;
-    S.sn[threadIdx.x] = (uint32_t)(h1 >> 32);
+  const int kc = (k + nseg - 1) / nseg;
+  constexpr int PK = (KF * SPLIT_MAX_SEG + SPLIT_T - 1) / SPLIT_T;
+  uint64_t kv[PK];
+#pragma unroll
+  for (int q = 0; q < PK; q++) {
+    const int i = (int)threadIdx.x + q * SPLIT_T, r = i / SPLIT_MAX_SEG, sg = i % SPLIT_MAX_SEG;
+    kv[q] = sg < nseg && r < k ? ld_agent(rrow + sg * rec_words + 2 + r) : 0ull;
+  }
+  const int ht = (int)threadIdx.x;
+  const uint64_t hv = ht < 2 * nseg ? ld_agent(rrow + (ht >> 1) * rec_words + (ht & 1)) : 0ull;
+  const float uval = (wid == 0 && lane < k) ? a.u[(size_t)row * k + lane] : 0.0f;
+#pragma unroll
+  for (int q = 0; q < PK; q++) {
+    const int i = (int)threadIdx.x + q * SPLIT_T, r = i / SPLIT_MAX_SEG, sg = i % SPLIT_MAX_SEG;
+    if (sg < nseg && r == k - 1) S.kth[sg] = kv[q];
+    if (sg < nseg && r == kc - 1) S.kc[sg] = kv[q];
+  }
+  if (ht < 2 * nseg) {
+    if (ht & 1) {
+      S.sflags[ht >> 1] = (uint32_t)hv;
+      S.sn[ht >> 1] = (uint32_t)(hv >> 32);
+    } else {
+      S.smax[ht >> 1] = d3s_u2f((uint32_t)hv);
+      S.ssum[ht >> 1] = d3s_u2f((uint32_t)(hv >> 32));
+    }
   }
   __syncthreads();
-  float Lmax = S.smax[0];
-  uint32_t F = S.sflags[0], total = S.sn[0];
-  for (int s = 1; s < nseg; s++) {
-    Lmax = fmaximum(Lmax, S.smax[s]);
-    F |= S.sflags[s];
-    total += S.sn[s];
-  }
+  /* every wave reduces the headers, lane s holding segment s: the row max,
+   * the flags, the keys filed, and a cut the row's k-th key reaches: T0, the
+   * largest k-th key of a segment that filed k (that segment alone has k keys
+   * at or above it), and T1, the least kc-th key, kc = ceil(k / nseg), when
+   * the segments that filed kc or more hold k keys at or above it */
+  const bool ls = lane < nseg;
+  const int sl = ls ? lane : 0;
+  const float lm_s = ls ? S.smax[sl] : ninf;
+  const uint32_t fl_s = ls ? S.sflags[sl] : 0u, n_s = ls ? S.sn[sl] : 0u;
+  const float Lmax = wave_maximum_f(lm_s);
+  const uint32_t F = (__ballot(fl_s & SEG_GENERIC) ? SEG_GENERIC : 0u) | (__ballot(fl_s & SEG_OVERFLOW) ? SEG_OVERFLOW : 0u);
+  const uint32_t total = wave_sum_u32(n_s);
+  const uint64_t T0 = wave_max_u64(ls && n_s == (uint32_t)k ? S.kth[sl] : 0ull);
+  const bool has_c = ls && n_s >= (uint32_t)kc;
+  const uint64_t T1 = ~wave_max_u64(has_c ? ~S.kc[sl] : 0ull); /* the least */
+  const uint64_t cut = (uint32_t)__popcll(__ballot(has_c)) * (uint32_t)kc >= (uint32_t)k ? max(T0, T1) : T0;
   if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) {
     if (wid == 0) wave_write_special(a, row, false);
     return;
@@ -352,92 +431,103 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
     if (wid == 0) wave_write_special(a, row, M == ninf);
     return;
   }
-  if ((F & SEG_GENERIC) || (F & SEG_OVERFLOW) || total < (uint32_t)k) {
-    if ((F & SEG_OVERFLOW) && !(F & SEG_GENERIC) && threadIdx.x == 0 && a.counters)
-      atomicAdd(&a.counters[CNT_EXACT_SELECT], 1u);
-    generic_row<BF16, SPLIT_T>(a, row, kpow, glist);
-    return;
-  }
-  /* the segments' keys, at offsets in segment order */
-  for (int i = threadIdx.x; i < nseg * KF; i += SPLIT_T) {
-    const int s = i / KF, j = i % KF;
-    if ((uint32_t)j < S.sn[s]) {
-      uint32_t o = 0u;
-      for (int q = 0; q < s; q++) o += S.sn[q];
-      S.keys[o + j] = ld_agent(rrow + (size_t)s * rec_words + 2 + j);
+  bool generic = (F & SEG_GENERIC) || (F & SEG_OVERFLOW) || total < (uint32_t)k;
+  if ((F & SEG_OVERFLOW) && !(F & SEG_GENERIC) && threadIdx.x == 0 && a.counters)
+    atomicAdd(&a.counters[CNT_EXACT_SELECT], 1u);
+  float lse = 0.0f, eps_s = 0.0f;
+  if (!generic) {
+    /* the rescaled fast sum and its error bound: the segment holding the max
+     * contributes 2^delta (about 1); segment s's terms were taken relative to
+     * h_s = RN(Ls cf) and are scaled by 2^(h_s - h) (hardware 2^x of the
+     * rounded difference).  Weighted by its share (at most CAP * EPC
+     * 2^(h_s - h), capped at 1), each segment adds its own term-rounding bound
+     * and the rescale's.  Lane s takes segment s; the wave sums them
+     * (non-negative terms: within the bound of nseg - 1 additions in any
+     * order). */
+    const float cfr = LOG2E_F / T;
+    const float h = Lmax * cfr;
+    const float delta = __builtin_fmaf(Lmax, cfr, -h); /* Lmax * cf - h exactly */
+    float term = 0.0f, eterm = 0.0f;
+    if (ls && lm_s != ninf) {
+      const float d = lm_s * cfr - h; /* <= 0 */
+      const float f = __builtin_amdgcn_exp2f(d);
+      term = S.ssum[sl] * f;
+      const float w = fminf(1.0f, (float)(CAP * EPC) * f);
+      eterm = w * (0x1p-24f * (2.0f * fabsf(lm_s) * y + 160.0f) + 0x1p-24f * fabsf(d) + EPS_EXP2);
     }
+    const float sp = wave_sum_f(term);
+    const float eps_seg = wave_sum_f(eterm) * (1.0f + 0x1p-20f); /* the bound's own rounding */
+    const float l2 = __builtin_amdgcn_logf(sp); /* within 2^-23 |log2 sp| + 2^-24 */
+    lse = M + (l2 * LN2_F - delta * LN2_F);
+    /* the one-wave kernel's bound (its term for the max's rounding is in
+     * eps_seg), with each segment's SPLIT_NW additions, the nseg products and
+     * additions of the rescale, and eps_seg */
+    eps_s = EPS_EXP2 + 0x1p-23f + (float)(CPT + 11 + SPLIT_NW + 2 * nseg) * 0x1p-24f + (float)V * 0x1p-40f +
+            0x1p-22f * fabsf(l2) + 0x1p-23f + eps_seg;
+    /* ---- the row's top k: the filed keys at or above the cut (at most nseg
+     * k of them; k or more by the cut's choice), ranked by counting */
+#pragma unroll
+    for (int q = 0; q < PK; q++) {
+      const int i = (int)threadIdx.x + q * SPLIT_T, r = i / SPLIT_MAX_SEG, sg = i % SPLIT_MAX_SEG;
+      if (sg < nseg && (uint32_t)r < S.sn[sg < nseg ? sg : 0] && kv[q] >= cut)
+        S.keys[atomicAdd(&S.mcount, 1u)] = kv[q];
+    }
+    __syncthreads();
+    rank_by_count(S.keys, S.mcount, k, S.ranked);
+    /* the top k reach x = -inf: ties the segments did not file */
+    generic = key_x(S.ranked[k - 1]) == ninf;
   }
-  /* the rescaled fast sum and its error bound: the segment holding the max
-   * contributes 2^delta (about 1); segment s's terms were taken relative to
-   * h_s = RN(Ls cf) and are scaled by 2^(h_s - h) (hardware 2^x of the rounded
-   * difference).  Weighted by its share (at most CAP * EPC 2^(h_s - h), capped
-   * at 1), each segment adds its own term-rounding bound and the rescale's. */
-  const float cfr = LOG2E_F / T;
-  const float h = Lmax * cfr;
-  const float delta = __builtin_fmaf(Lmax, cfr, -h); /* Lmax * cf - h exactly */
-  float sp = 0.0f, eps_seg = 0.0f;
-  for (int s = 0; s < nseg; s++) {
-    const float Lm = S.smax[s];
-    if (Lm == ninf) continue;
-    const float d = Lm * cfr - h; /* <= 0 */
-    const float f = __builtin_amdgcn_exp2f(d);
-    sp = sp + S.ssum[s] * f;
-    const float w = fminf(1.0f, (float)(CAP * EPC) * f);
-    eps_seg = eps_seg + w * (0x1p-24f * (2.0f * fabsf(Lm) * y + 160.0f) + 0x1p-24f * fabsf(d) + EPS_EXP2);
-  }
-  const float l2 = __builtin_amdgcn_logf(sp); /* within 2^-23 |log2 sp| + 2^-24 */
-  const float lse = M + (l2 * LN2_F - delta * LN2_F);
-  /* the one-wave kernel's bound (its term for the max's rounding is in
-   * eps_seg), with each segment's SPLIT_NW additions, the nseg products and
-   * additions of the rescale, and eps_seg */
-  const float eps_s = EPS_EXP2 + 0x1p-23f + (float)(CPT + 11 + SPLIT_NW + 2 * nseg) * 0x1p-24f +
-                      (float)V * 0x1p-40f + 0x1p-22f * fabsf(l2) + 0x1p-23f + eps_seg;
-  split_rank(S, total, k);
-  if (key_x(S.ranked[k - 1]) == ninf) { /* the top k reach x = -inf: ties the segments did not file */
+  if (generic) {
     generic_row<BF16, SPLIT_T>(a, row, kpow, glist);
     return;
   }
-  /* ---- the tail on wave 0; a cut within the margin takes the exact lse */
-  const float uval = (wid == 0 && lane < k) ? a.u[(size_t)row * k + lane] : 0.0f;
+  /* ---- the tail on wave 0; a cut within the margin takes the exact lse (by
+   * the whole workgroup) and the tail again */
   const float noise = -d3s_logf(1.0f - uval);
   const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
-  if (wid == 0) {
-    const int id = wave_tail(a, row, key, M, lse, false, eps_s, noise, top_p, S.buf,
-                             []() { return __builtin_nanf(""); });
-    if (id == NEED_EXACT && lane == 0) S.exact = 1u;
+  bool exact = false;
+#pragma unroll 1
+  for (;;) {
+    if (wid == 0) {
+      const int id = wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf,
+                               []() { return __builtin_nanf(""); });
+      if (id == NEED_EXACT && lane == 0) S.exact = 1u;
+    }
+    __syncthreads();
+    if (exact || !S.exact) return;
+    lse = split_exact_lse<BF16>(a, row, M, S);
+    exact = true;
   }
-  __syncthreads();
-  if (!S.exact) return;
-  const float lx = split_exact_lse<BF16>(a, row, M, S);
-  if (wid == 0) (void)wave_tail(a, row, key, M, lx, true, 0.0f, noise, top_p, S.buf, []() { return 0.0f; });
 }
 
 template <int CPT, bool BF16>
 bool try_split(const SampleArgs &a, int nseg, void *ws, size_t ws_bytes, hipStream_t s) {
-  if (nseg < 2 || nseg > SPLIT_MAX_SEG) return false;
-  const size_t cnt_bytes = ((size_t)a.n_rows * 128 + 255) & ~(size_t)255;
-  const int rec_words = 2 + KF;
-  const size_t need = cnt_bytes + (size_t)a.n_rows * nseg * rec_words * 8;
+  if (nseg < 2 || nseg > SPLIT_MAX_SEG || (int64_t)a.n_rows * nseg > SPLIT_MAX_BLOCKS) return false;
+  const int rec_words = 2 + a.k; /* header, then the keys by rank */
+  const size_t need = SPLIT_CNT_BYTES + (size_t)a.n_rows * nseg * rec_words * 8;
   if (!ws || need > ws_bytes) return false;
   hipLaunchKernelGGL((k_split<CPT, BF16>), dim3((unsigned)(a.n_rows * nseg)), dim3(SPLIT_T), 0, s, a,
-                     (uint32_t *)ws, (uint64_t *)((char *)ws + cnt_bytes), nseg, rec_words);
+                     (uint32_t *)ws, (uint64_t *)((char *)ws + SPLIT_CNT_BYTES), nseg, rec_words);
   return true;
 }
 
 }  // namespace
+
+size_t split_counter_bytes() { return SPLIT_CNT_BYTES; }
 
 int split_segments(const SampleArgs &a, Dtype dt) {
   const int EPC = dt == DT_F32 ? 4 : 8;
   const int cap = SPLIT_NW * SPLIT_CPT * WAVE;
   const int nchunks = (EPC - 1 + a.vocab + EPC - 1) / EPC; /* any start offset */
   const int nseg = (nchunks + cap - 1) / cap;
-  return (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG) ? 0 : nseg;
+  if (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG || (int64_t)a.n_rows * nseg > SPLIT_MAX_BLOCKS) return 0;
+  return nseg;
 }
 
 size_t split_workspace_bytes(const SampleArgs &a, Dtype dt) {
   const int nseg = split_segments(a, dt);
   if (!nseg) return 0;
-  return (((size_t)a.n_rows * 128 + 255) & ~(size_t)255) + (size_t)a.n_rows * nseg * (2 + KF) * 8;
+  return SPLIT_CNT_BYTES + (size_t)a.n_rows * nseg * (2 + KF) * 8;
 }
 
 bool launch_split(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {

@@ -92,7 +92,8 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
  * several CUs) comes instead from one fixed block of D3S_SCRATCH_BYTES per GPU,
  * in the library's static device memory, held until the process ends.  Every
  * call the segmented kernel takes fits (it takes at most 4096 segments per
- * launch, at most 2.4 MB); a call that would not returns D3S_ERR_SCRATCH.
+ * launch: 256 KiB of counters and at most 2.1 MiB of records); a call that
+ * would not returns D3S_ERR_SCRATCH.
  * All calls on one GPU share that block: calls that overlap on one GPU
  * (several streams or threads at once) race and must not be issued. */
 int d3s_sample_noalloc(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,

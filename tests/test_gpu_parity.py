@@ -364,32 +364,54 @@ def test_wide_kernel_on_many_rows(gpu, oracle, bf16):
     compare(oracle, gpu, xs, u, 0.8, 0.9, label=f"wide kernel, {N} rows bf16={bf16}")
 
 
+def split_bounds(V, bf16, row):
+    """Positions where the segmented kernel's segments of row `row` begin (rows
+    contiguous from a 16-byte aligned base): the row's 16-byte chunks from the
+    aligned address at or below its start, in nseg equal parts of at most 2048
+    chunks; nseg from the chunk count at any start offset.  Empty when the
+    row is not cut (2 to 16 segments)."""
+    EPC, ES = (8, 2) if bf16 else (4, 4)
+    off = (row * V * ES) % 16 // ES
+    nseg = -(-((EPC - 1 + V + EPC - 1) // EPC) // 2048)
+    if not 2 <= nseg <= 16:
+        return np.array([], np.int64)
+    segc = -(-((off + V + EPC - 1) // EPC) // nseg)
+    return np.array([s * segc * EPC - off for s in range(1, nseg)], np.int64)
+
+
 @pytest.mark.parametrize("V,bf16,N", [(8190, False, 20), (16381, False, 12), (16382, True, 9),
                                       (131069, False, 4), (262137, True, 3), (262138, True, 2),
-                                      (40000, True, 40)])
+                                      (40000, True, 40), (151936, True, 6)])
 def test_segmented_rows(gpu, oracle, V, bf16, N):
-    """Rows cut into segments of 2048 chunks (2 to 16 per row, and one past the
-    most: the generic kernel), with structure across segments: the top k at
-    segment bounds, a NaN in the last segment, a segment all -inf, the banned
-    index at a bound, fewer finite elements than k, per-row T and top_p;
-    against the oracle and the generic kernel."""
+    """Rows cut into equal segments of at most 2048 chunks (2 to 16 per row,
+    and one past the most: the generic kernel), with structure across
+    segments: the top k at segment bounds, a NaN in the last segment, a
+    segment all -inf, the banned index at a bound, fewer finite elements than
+    k, per-row T and top_p; against the oracle and the generic kernel."""
     rng = np.random.default_rng([V, 91])
     x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
-    seg = 8192 * (2 if bf16 else 1)  # elements per segment (at offset 0)
-    bounds = np.arange(seg, V, seg)
-    if N > 1 and len(bounds):
-        x[1, np.clip(np.concatenate([bounds - 1, bounds]), 0, V - 1)] += 9.0
+    seg = 8192 * (2 if bf16 else 1)  # nominal bounds for rows that are not cut
+
+    def bounds(r):
+        b = split_bounds(V, bf16, r)
+        return b if len(b) else np.arange(seg, V, seg)
+
+    if N > 1 and len(bounds(1)):
+        b1 = bounds(1)
+        x[1, np.clip(np.concatenate([b1 - 1, b1]), 0, V - 1)] += 9.0
     if N > 2:
         x[2, V - 2] = np.nan
     if N > 3:
-        x[3, : min(V, seg)] = -np.inf
+        b3 = bounds(3)
+        x[3, : (b3[0] if len(b3) else V)] = -np.inf
     if N > 4:
         x[4, :] = -np.inf
         x[4, [0, V // 2, V - 1]] = 1.0
     ban = np.full(N, -1, np.int32)
-    if len(bounds):
-        ban[0] = int(bounds[0])
-        x[0, bounds[0]] = 40.0
+    if len(bounds(0)):
+        b0 = int(bounds(0)[0])
+        ban[0] = b0
+        x[0, b0] = 40.0
     T = rng.uniform(0.5, 1.5, N).astype(np.float32)
     top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
     u = oracle.uniform(91, 0, N, 30)
@@ -422,6 +444,20 @@ def test_top_k_reaching_minus_inf_x(gpu, oracle, V, bf16):
         got, exp = compare(oracle, gpu, xs, u, 0.0, top_p, label=f"-inf ties V={V} bf16={bf16}")
         assert np.all(np.isneginf(np.float32(x[0, exp["cand"][0, 10:]])))  # masked logits rank there
         compare(oracle, gpu, xs, u, 0.0, top_p, flags=gpu.FLAG_GENERIC, label=f"-inf ties V={V} generic")
+
+
+def test_segmented_launches_of_changing_row_counts(gpu, oracle):
+    """The segmented kernel's workspace (records and arrival counters) carried
+    from launch to launch on one stream while the row count changes: 1, 64, 8,
+    64, 3, 300 rows of C4's width; every launch equal to the oracle."""
+    w = W.make("C4", rows=300, seed=47, uniforms=False)
+    u = oracle.uniform(47, 0, 300, 30)
+    exp = oracle.sample(w["logits"], u, 1.0, 0.9, n_threads=8)
+    for n in (1, 64, 8, 64, 3, 300):
+        got = gpu.sample(w["logits"][:n], u[:n], 1.0, 0.9, want_probs=False)
+        banner(f"segmented launch of {n} rows")
+        assert got["rc"] == 0
+        assert np.array_equal(got["ids"], exp["ids"][:n]), n
 
 
 def test_wide_kernel_past_the_segment_limit(gpu, oracle):

@@ -217,3 +217,20 @@ def test_frame_assembled_in_place(gpu, oracle):
                               frame.ptr + 4 * (2 + j)) == 0
     hiprt.synchronize()
     assert frame.download((11,), np.int32).tolist() == [int(v) for v in expected]
+
+
+@pytest.mark.gpu
+def test_fallback_workspace_leaves_the_segment_counters(gpu, oracle):
+    """The fallback's retry indices live in the stream's workspace; a later
+    launch of the segmented kernel on the same stream (whose arrival counters
+    open that workspace) still samples every row right."""
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((64, 4097)) * 2.5).astype(np.float32)
+    u = oracle.uniform(31, 0, 64, 100)
+    u2 = oracle.uniform(31, 1, 64, 30)
+    hist = np.full((64, 16), START, np.int32)
+    _check(oracle, gpu, x, u, u2, hist, dict(temperature=0.7, top_p=0.7, top_k=100, **MAP), indices=False)
+    w = W.make("C4", rows=8, seed=31, uniforms=False)
+    uc = oracle.uniform(31, 2, 8, 30)
+    got = gpu.sample(w["logits"], uc, 1.0, 0.9, want_probs=False)
+    assert np.array_equal(got["ids"], oracle.sample(w["logits"], uc, 1.0, 0.9, n_threads=8)["ids"])
