@@ -49,7 +49,10 @@ struct __align__(16) SplitLds {
   float buf[WAVE];
   float wmax[SPLIT_NW], wsum[SPLIT_NW];
   uint32_t wpre[SPLIT_NW];
-  uint32_t ncand; /* a segment's candidates filed */
+  uint32_t wcnt[SPLIT_NW];         /* pairs each wave filed (all ones: more than its region) */
+  uint4 stage[SPLIT_NW * WAVE];    /* each wave's candidate chunks */
+  uint32_t spos[SPLIT_NW * WAVE];  /* their first positions */
+  uint64_t raw[SPLIT_NW * WAVE];   /* each wave's (logit bits, position) pairs */
   float smax[SPLIT_MAX_SEG], ssum[SPLIT_MAX_SEG];
   uint32_t sflags[SPLIT_MAX_SEG], sn[SPLIT_MAX_SEG];
   uint32_t last, exact, mcount;
@@ -243,7 +246,6 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
       S.wpre[wid] = wp;
     }
     S.lk[threadIdx.x] = lkey;
-    if (threadIdx.x == 0) S.ncand = 0u;
   }
   __syncthreads();
   float Ls = S.wmax[0];
@@ -300,48 +302,79 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
       if (lane == 0) S.wsum[wid] = ws;
     }
 
-    /* ---- file the candidates: each candidate chunk (taken from the
-     * registers by selects) files its valid elements that reach tau_lo, at
-     * slots taken from an LDS counter */
-#pragma unroll 1
-    while (__ballot(cb != 0u)) {
-      const int jc = cb ? __builtin_ctz(cb) : CPT;
-      cb &= cb - 1u;
-      uint32_t qw[4] = {0u, 0u, 0u, 0u};
+    /* ---- file the candidates in one pass: each wave stages its candidate
+     * chunks in LDS (slots by a wave scan), lane t takes staged chunk t and
+     * files its valid elements that reach tau_lo as (logit bits, position)
+     * pairs in the wave's region; the keys are made after the barrier, one
+     * per thread.  A wave with more than 64 chunks or pairs overflows. */
+    {
+      const uint32_t nc = (uint32_t)__popc(cb);
+      const uint32_t cinc = wave_scan_add_u32(nc);
+      const uint32_t wchunks = readlane_u(cinc, 63);
+      uint32_t slot = cinc - nc;
+      uint4 *stg = S.stage + wid * WAVE;
+      uint32_t *sps = S.spos + wid * WAVE;
 #pragma unroll
       for (int j = 0; j < CPT; j++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) qw[t] = jc == j ? c.w[4 * j + t] : qw[t];
-      const int pb = C::pos(pos0, jc * EPC); /* the chunk's first position */
+        if ((cb >> j) & 1u) {
+          if (slot < (uint32_t)WAVE) {
+            stg[slot] = make_uint4(c.w[4 * j], c.w[4 * j + 1], c.w[4 * j + 2], c.w[4 * j + 3]);
+            sps[slot] = (uint32_t)C::pos(pos0, j * EPC);
+          }
+          slot++;
+        }
+      wave_lds_sync();
       float v[EPC];
-      uint32_t vm = 0u;
+      uint32_t vm = 0u, pb = 0u;
+      if ((uint32_t)lane < min(wchunks, (uint32_t)WAVE)) {
+        const uint4 q = stg[lane];
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        pb = sps[lane];
 #pragma unroll
-      for (int e = 0; e < EPC; e++) {
-        v[e] = BF16 ? d3s_u2f((e & 1) ? (qw[e / 2] & 0xffff0000u) : (qw[e / 2] << 16)) : d3s_u2f(qw[e]);
-        const bool ok = jc < CPT && v[e] >= tau_lo; /* masked elements hold -inf */
-        vm |= (ok ? 1u : 0u) << e;
+        for (int e = 0; e < EPC; e++) {
+          v[e] = BF16 ? d3s_u2f((e & 1) ? (qw[e / 2] & 0xffff0000u) : (qw[e / 2] << 16)) : d3s_u2f(qw[e]);
+          vm |= (v[e] >= tau_lo ? 1u : 0u) << e; /* masked elements hold -inf */
+        }
       }
-      /* the logit's bits and its position; the keys are made after the loop,
-       * one per thread */
-      uint32_t slot = vm ? atomicAdd(&S.ncand, (uint32_t)__popc(vm)) : 0u;
+      const uint32_t ne = (uint32_t)__popc(vm);
+      const uint32_t einc = wave_scan_add_u32(ne);
+      const uint32_t wpairs = readlane_u(einc, 63);
+      uint32_t at = einc - ne;
+      uint64_t *rw = S.raw + wid * WAVE;
 #pragma unroll
       for (int e = 0; e < EPC; e++)
         if ((vm >> e) & 1u) {
-          if (slot < (uint32_t)SCAP) S.keys[slot] = ((uint64_t)d3s_f2u(v[e]) << 32) | (uint32_t)(pb + e);
-          slot++;
+          if (at < (uint32_t)WAVE) rw[at] = ((uint64_t)d3s_f2u(v[e]) << 32) | (pb + (uint32_t)e);
+          at++;
         }
+      if (lane == 0) S.wcnt[wid] = wchunks > (uint32_t)WAVE || wpairs > (uint32_t)WAVE ? 0xffffffffu : wpairs;
     }
     __syncthreads();
     ssum = S.wsum[0];
 #pragma unroll
     for (int w = 1; w < SPLIT_NW; w++) ssum = ssum + S.wsum[w]; /* the same order in every wave */
-    const uint32_t tot = S.ncand;
+    uint32_t tot = 0u;
+#pragma unroll
+    for (int w = 0; w < SPLIT_NW; w++) {
+      const uint32_t t = S.wcnt[w];
+      over = over || t == 0xffffffffu;
+      tot += t == 0xffffffffu ? 0u : t;
+    }
     if (over || tot > (uint32_t)SCAP) {
       flags |= SEG_OVERFLOW;
     } else {
-      /* ---- the keys, one per thread; rank them, keep the top k */
+      /* ---- the keys, one per thread (from the waves' regions in wave
+       * order); rank them, keep the top k */
       if (threadIdx.x < tot) {
-        const uint64_t lp = S.keys[threadIdx.x];
+        uint32_t t = threadIdx.x;
+        int w = 0;
+#pragma unroll
+        for (int q = 0; q < SPLIT_NW - 1; q++)
+          if (w == q && t >= S.wcnt[q]) {
+            t -= S.wcnt[q];
+            w = q + 1;
+          }
+        const uint64_t lp = S.raw[w * WAVE + t];
         S.keys[threadIdx.x] = composite_key(scale_logit(d3s_u2f((uint32_t)(lp >> 32)), T, y, true), (int)(uint32_t)lp);
       }
       rank_by_count(S.keys, tot, k, S.ranked);
@@ -386,6 +419,7 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   const int ht = (int)threadIdx.x;
   const uint64_t hv = ht < 2 * nseg ? ld_agent(rrow + (ht >> 1) * rec_words + (ht & 1)) : 0ull;
   const float uval = (wid == 0 && lane < k) ? a.u[(size_t)row * k + lane] : 0.0f;
+  const float noise = -d3s_logf(1.0f - uval); /* off the tail's path */
 #pragma unroll
   for (int q = 0; q < PK; q++) {
     const int i = (int)threadIdx.x + q * SPLIT_T, r = i / SPLIT_MAX_SEG, sg = i % SPLIT_MAX_SEG;
@@ -469,8 +503,9 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
 #pragma unroll
     for (int q = 0; q < PK; q++) {
       const int i = (int)threadIdx.x + q * SPLIT_T, r = i / SPLIT_MAX_SEG, sg = i % SPLIT_MAX_SEG;
-      if (sg < nseg && (uint32_t)r < S.sn[sg < nseg ? sg : 0] && kv[q] >= cut)
-        S.keys[atomicAdd(&S.mcount, 1u)] = kv[q];
+      const bool take = sg < nseg && (uint32_t)r < S.sn[sg < nseg ? sg : 0] && kv[q] >= cut;
+      const int at = wave_append(take, (int *)&S.mcount);
+      if (take) S.keys[at] = kv[q];
     }
     __syncthreads();
     rank_by_count(S.keys, S.mcount, k, S.ranked);
@@ -483,7 +518,6 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   }
   /* ---- the tail on wave 0; a cut within the margin takes the exact lse (by
    * the whole workgroup) and the tail again */
-  const float noise = -d3s_logf(1.0f - uval);
   const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
   bool exact = false;
 #pragma unroll 1
