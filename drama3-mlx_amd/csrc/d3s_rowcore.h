@@ -47,6 +47,20 @@ __device__ __forceinline__ float wave_sum_f(float v) {
   return readlane_f(v, 63);
 }
 
+/* The k-th largest of the wave's 64 lane keys to 20 bits: the largest p
+ * (low 12 bits zero) that at least k lanes' keys reach, 0 when no such p
+ * (fewer than k lanes reach 2^12).  A ballot search, one bit a step (faster
+ * here than three counts a step).  Wave-uniform. */
+__device__ __forceinline__ uint32_t wave_kth_prefix(uint32_t key, uint32_t k) {
+  uint32_t pre = 0u;
+#pragma unroll
+  for (int bit = 31; bit >= 12; bit--) {
+    const uint32_t cnd = pre | (1u << bit);
+    if ((uint32_t)__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
+  }
+  return pre;
+}
+
 __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }

@@ -122,20 +122,8 @@ __device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k,
   __syncthreads();
 }
 
-/* the k-th largest of the wave's lane keys to 20 bits (the largest prefix that
- * at least k lanes reach; 0 when fewer than k lanes hold a key), by ballot
- * radix search; wave-uniform */
-__device__ __forceinline__ uint32_t wave_kth_prefix(uint32_t key, uint32_t k) {
-  uint32_t pre = 0u;
-#pragma unroll
-  for (int bit = 31; bit >= 12; bit--) {
-    const uint32_t cnd = pre | (1u << bit);
-    if ((uint32_t)__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
-  }
-  return pre;
-}
-
-/* the same over the SPLIT_T keys of a workgroup held in LDS, by every wave */
+/* wave_kth_prefix over the SPLIT_T keys of a workgroup held in LDS, by
+ * every wave */
 __device__ __forceinline__ uint32_t group_kth_prefix(const uint32_t *keys, uint32_t k) {
   const int lane = lane_id();
   uint32_t kk[SPLIT_NW];
@@ -193,14 +181,17 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   const int off = (int)(((uintptr_t)rowp & 15u) / ES);
   const uint4 *src = (const uint4 *)(rowp - off * ES);
   const int nchunks = (off + V + EPC - 1) / EPC;
-  /* the row's chunks in nseg equal parts (at most CAP each): every wave of a
-   * segment holds logits, the last segment as much as the others */
+  /* the row's chunks in nseg equal parts (at most CAP each), each part in
+   * SPLIT_NW equal runs, one per wave: every wave holds as many logits as the
+   * others (the per-wave thresholds below assume it) */
   const int segc = (nchunks + nseg - 1) / nseg;
-  const int cend = min(nchunks, (seg + 1) * segc);    /* past the segment's last chunk */
-  const int cbase = seg * segc + wid * CPT * WAVE;    /* this wave's first chunk */
-  const int vend = min(V, cend * EPC - off);          /* past the segment's last position */
+  const int wch = (segc + SPLIT_NW - 1) / SPLIT_NW;                  /* chunks per wave */
+  const int cend = min(nchunks, (seg + 1) * segc);                   /* past the segment's last chunk */
+  const int cbase = seg * segc + wid * wch;                          /* this wave's first chunk */
+  const int wend = min(cend, cbase + wch);                           /* past its last */
+  const int vend = min(V, wend * EPC - off);                         /* past its last position */
   C c;
-  c.load(src + cbase, min(max(cend - cbase, 0), CPT * WAVE), lane);
+  c.load(src + cbase, min(max(wend - cbase, 0), CPT * WAVE), lane);
   const int pos0 = (cbase + lane) * EPC - off;
   auto valid = [&](int i) { return (unsigned)C::pos(pos0, i) < (unsigned)vend; };
 #pragma unroll

@@ -215,6 +215,10 @@ struct WaveRow {
   const char *rowp;
   float T, y, uval, top_p;
   bool t_finite;
+  /* a cut that needs the exact lse returns NEED_EXACT (helper waves of the
+   * workgroup compute it) instead of the wave computing it alone */
+  bool defer_exact = false;
+  float fin_M = 0.0f, fin_noise = 0.0f; /* the tail's max x and noise */
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -298,8 +302,17 @@ struct WaveRow {
       rank_keys(exact_select<CPT, BF16>(ref()));
     }
     const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
-    return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf,
-                     [&]() { return exact_lse<CPT, BF16>(ref(), M); });
+    fin_M = M;
+    fin_noise = noise;
+    return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf, [&]() {
+      return defer_exact ? __builtin_nanf("") : exact_lse<CPT, BF16>(ref(), M);
+    });
+  }
+
+  /* the tail again with the exact lse lx, after finish() returned NEED_EXACT */
+  __device__ __forceinline__ int exact_tail(float lx) {
+    const uint64_t key = lane < k ? S.ranked[lane] : 0ull;
+    return wave_tail(a, row, key, fin_M, lx, true, 0.0f, fin_noise, top_p, S.buf, []() { return 0.0f; });
   }
 
   /* every quantity per element from x = L / T, as the oracle (T not finite,
@@ -317,7 +330,8 @@ struct WaveRow {
     const float ninf = -__builtin_inff();
     const float noise = -d3s_logf(1.0f - uval); /* the race's noise needs only u */
     bool slow = !t_finite;
-    float M = 0.0f, cf = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
+    const float cf = slow ? 0.0f : LOG2E_F / T; /* needs only T: off the max's path */
+    float M = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
     if (!slow) {
       /* ---- row max of the logits; NaN propagates */
 #pragma unroll
@@ -326,7 +340,6 @@ struct WaveRow {
       if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) return wave_write_special(a, row, false);
       M = scale_logit(Lmax, T, y, true); /* = max x */
       if (M == __builtin_inff() || M == ninf) return wave_write_special(a, row, M == ninf);
-      cf = LOG2E_F / T;
       const float h = Lmax * cf;
       slow = !(fabsf(h) < 0x1p24f);
       b = -h;
@@ -337,13 +350,7 @@ struct WaveRow {
     /* ---- tau: the k-th largest lane max, to 20 bits of its order key (a
      * lower bound: at least k elements reach it), by ballot radix search */
     bool need_sel = (a.flags & FLAG_EXACT_SELECT) != 0;
-    const uint32_t lkey = d3s_ordkey(lm);
-    uint32_t pre = 0u;
-#pragma unroll
-    for (int bit = 31; bit >= 12; bit--) {
-      const uint32_t cnd = pre | (1u << bit);
-      if (__popcll(__ballot(lkey >= cnd)) >= (uint32_t)k) pre = cnd;
-    }
+    const uint32_t pre = wave_kth_prefix(d3s_ordkey(lm), (uint32_t)k);
     /* keys below -FLT_MAX's: the k-th lane max is -inf */
     if (pre < d3s_ordkey(-0x1.fffffep127f)) need_sel = true;
     const float tau = d3s_from_ordkey(pre);
@@ -868,6 +875,55 @@ void k_ras(RasArgs ra) {
   ras_pick(ra, row, drawn[wid], drawn[wid + 1]);
 }
 
+/* k_wave for small launches: one row per 4-wave workgroup.  Wave 0 samples
+ * the row as k_wave's waves do; the other three wait, and join only when the
+ * cut needs the exact lse: the row's 2^-40 fixed-point sum of d3s_expf(x - M)
+ * by all four (an integer sum, the same in any order), then wave 0 runs the
+ * tail again with it. */
+template <int CPT, bool BF16>
+__global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
+void k_wave_row(SampleArgs a) {
+  __shared__ WaveLds lds;
+  __shared__ uint32_t need;
+  __shared__ float m_sh;
+  __shared__ uint32_t s_lo[WR], s_hi[WR];
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+  const int lane = lane_id();
+  const int row = (int)blockIdx.x;
+  WaveRow<CPT, BF16> r(a, lds, row);
+  if (wid == 0) {
+    r.V = a.vocab;
+    r.k = a.k;
+    r.lane = lane;
+    r.defer_exact = true;
+    r.load();
+    const int id = r.compute();
+    if (lane == 0) {
+      need = id == NEED_EXACT ? 1u : 0u;
+      m_sh = r.fin_M;
+    }
+  }
+  __syncthreads();
+  if (!need) return;
+  const RowP rp = row_params(a, row);
+  const float y = 1.0f / rp.T, M = m_sh;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  uint64_t acc = 0;
+  for (int i = (int)threadIdx.x; i < a.vocab; i += WAVE * WR)
+    acc += d3s_fix40_exp(scale_logit(load_logit<BF16>(rowp, i, rp.banned), rp.T, y, true) - M);
+  const uint64_t w = wave_sum_u64(acc);
+  if (lane == 0) {
+    s_lo[wid] = (uint32_t)w;
+    s_hi[wid] = (uint32_t)(w >> 32);
+  }
+  __syncthreads();
+  if (wid != 0) return;
+  uint64_t tot = 0;
+#pragma unroll
+  for (int q = 0; q < WR; q++) tot += ((uint64_t)s_hi[q] << 32) | s_lo[q];
+  (void)r.exact_tail(M + d3s_logf(d3s_fixsum_to_f32(tot)));
+}
+
 /* The pick alone, one wave per row, after the two draws ran as separate
  * launches that wrote their indices to `first` and `retry` (rows the fused
  * kernel does not hold: k above 64, or rows wider than one wave's registers). */
@@ -914,10 +970,12 @@ template <int CPT, bool BF16>
 bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
   if (a.vocab > wave_vmax<CPT, BF16>(max_off)) return false;
   /* a launch too small to fill the chip spreads its rows one per workgroup
-   * over more CUs; larger ones pack WR, which keeps the CUs fuller */
-  const int wr = a.n_rows <= WR_SPREAD_ROWS ? 1 : WR;
-  const unsigned blocks = (unsigned)((a.n_rows + wr - 1) / wr);
-  hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3(blocks), dim3(WAVE * wr), 0, s, a);
+   * over more CUs, with three helper waves for the exact lse; larger ones
+   * pack WR rows, which keeps the CUs fuller */
+  if (a.n_rows <= WR_SPREAD_ROWS)
+    hipLaunchKernelGGL((k_wave_row<CPT, BF16>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3((unsigned)((a.n_rows + WR - 1) / WR)), dim3(WAVE * WR), 0, s, a);
   return true;
 }
 
