@@ -219,6 +219,9 @@ struct WaveRow {
    * workgroup compute it) instead of the wave computing it alone */
   bool defer_exact = false;
   float fin_M = 0.0f, fin_noise = 0.0f; /* the tail's max x and noise */
+  /* the candidates from the registers (staged in LDS) instead of read again
+   * from L2: long launches, whose rows leave L2 before a second read */
+  bool reg_cands = false;
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -411,7 +414,7 @@ struct WaveRow {
       cpos[q] = 0;
       cl[q] = 0.0f;
     }
-    if (!need_sel) {
+    if (!need_sel && !reg_cands) {
 #pragma unroll
       for (int q = 0; q < EARLY; q++) {
         if (q > 0 && !__ballot(q < cnt)) break;
@@ -447,6 +450,52 @@ struct WaveRow {
     int n;
     if (need_sel) {
       n = exact_select<CPT, BF16>(ref());
+    } else if (reg_cands) {
+      /* each lane's chunks that hold a candidate are staged in LDS (the
+       * histogram's and buf's room, idle here; slots by a wave scan), then
+       * lane t files staged chunk t's elements that reach tau_lo (at most
+       * tot <= 64 chunks) */
+      uint32_t cm = 0u;
+#pragma unroll
+      for (int j = 0; j < CPT; j++) {
+        const int i0 = j * EPC; /* a chunk's elements lie in one word */
+        const uint32_t part = (bits[i0 / 32] >> (32 - EPC - i0 % 32)) & ((1u << EPC) - 1u);
+        cm |= (part != 0u ? 1u : 0u) << j;
+      }
+      const uint32_t nc = (uint32_t)__popc(cm);
+      const uint32_t cinc = wave_scan_add_u32(nc);
+      uint32_t slot = cinc - nc;
+      uint4 *stg = (uint4 *)S.hist;
+      uint32_t *sps = (uint32_t *)S.buf;
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if ((cm >> j) & 1u) {
+          stg[slot] = make_uint4(c.w[4 * j], c.w[4 * j + 1], c.w[4 * j + 2], c.w[4 * j + 3]);
+          sps[slot] = (uint32_t)C::pos(pos0, j * EPC);
+          slot++;
+        }
+      wave_lds_sync();
+      float v[EPC];
+      uint32_t vm = 0u, pb = 0u;
+      if ((uint32_t)lane < readlane_u(cinc, 63)) {
+        const uint4 q = stg[lane];
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        pb = sps[lane];
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          v[e] = BF16 ? d3s_u2f((e & 1) ? (qw[e / 2] & 0xffff0000u) : (qw[e / 2] << 16)) : d3s_u2f(qw[e]);
+          vm |= (v[e] >= tau_lo ? 1u : 0u) << e; /* masked elements hold -inf */
+        }
+      }
+      const uint32_t ne = (uint32_t)__popc(vm);
+      uint32_t at = wave_scan_add_u32(ne) - ne;
+#pragma unroll
+      for (int e = 0; e < EPC; e++)
+        if ((vm >> e) & 1u) {
+          S.keys[at] = composite_key(scale_logit(v[e], T, y, true), (int)pb + e);
+          at++;
+        }
+      n = (int)tot;
     } else {
       const uint32_t excl = wave_scan_add_u32((uint32_t)cnt) - (uint32_t)cnt;
 #pragma unroll
@@ -946,6 +995,7 @@ void k_wave(SampleArgs a) {
   r.V = a.vocab;
   r.k = a.k;
   r.lane = lane_id();
+  r.reg_cands = true;
   r.run();
 }
 
