@@ -232,6 +232,21 @@ def test_edge_rows(gpu, oracle):
     compare(oracle, gpu, x, u, 0.8, 0.9, flags=gpu.FLAG_GENERIC, label="edge rows generic")
 
 
+def test_finite_logit_overflowing_after_temperature(gpu, oracle):
+    """x = L / T overflowing to +inf refuses the row (id -1), as the oracle's
+    rule on x; the same logits at T = 1 are sampled; on the one-wave and the
+    generic kernel."""
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((6, 4097)) * 2).astype(np.float32)
+    x[:, 11] = 3e38
+    x[3:, 20] = -np.inf
+    T = np.array([0.7, 1e-5, 0.5, 1.0, 1.0, 0.99999], np.float32)
+    u = rng.random((6, 30)).astype(np.float32)
+    for flags in (0, gpu.FLAG_GENERIC):
+        got, _ = compare(oracle, gpu, x, u, T, 0.9, flags=flags, label=f"overflow after T flags={flags}")
+        assert np.all(got["ids"][:3] == -1) and np.all(got["ids"][3:5] == 11)
+
+
 @pytest.mark.parametrize("T,top_p", [(0.0, 0.7), (np.inf, 0.9), (np.nan, 0.9), (1e-5, 0.5),
                                      (1e4, 0.8), (0.7, np.nan), (0.7, -1.0), (0.7, 1.0)])
 def test_parameter_edges(gpu, oracle, T, top_p):

@@ -182,6 +182,23 @@ def test_non_finite_rows_are_refused(oracle):
     assert out["ids"][3] == 7
 
 
+def test_finite_logit_overflowing_after_temperature_is_refused(oracle):
+    """The refusal rule is on x = L / T, not on L (a deliberate deviation: the
+    reference's generation loop dies on any non-finite logit, -inf included,
+    src/generate.c:91,123, and never on finite ones): a finite logit whose x
+    overflows to +inf refuses the row; the same row at T = 1 does not; -inf
+    logits are masked, not refused."""
+    x = np.zeros((3, 64), np.float32)
+    x[:, 9] = 3e38
+    x[2, 4] = -np.inf
+    u = np.full((3, 8), 0.5, np.float32)
+    T = np.array([0.7, 1.0, 1.0], np.float32)
+    out = oracle.sample(x, u, T, 0.9)
+    assert out["ids"][0] == -1 and out["flags"][0] & oracle.BAD
+    assert out["ids"][1] == 9 and out["ids"][2] == 9
+    assert not (out["flags"][1] & oracle.BAD) and not (out["flags"][2] & oracle.BAD)
+
+
 def test_banned_index_and_minus_inf_entries(oracle):
     rng = np.random.default_rng(8)
     x = (rng.standard_normal((16, 200)) * 0.3).astype(np.float32)
