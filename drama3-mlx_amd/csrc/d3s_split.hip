@@ -26,6 +26,7 @@ namespace {
 
 constexpr int SPLIT_NW = 4;              /* waves per segment */
 constexpr int SPLIT_CPT = 8;             /* 16-byte chunks per lane */
+constexpr int SPLIT_CPT_WIDE = 10;       /* the wider form, when it fills the CUs more evenly */
 constexpr int SPLIT_T = SPLIT_NW * WAVE; /* threads per segment */
 constexpr int SCAP = SPLIT_T;            /* candidates a segment ranks (one per thread) */
 constexpr int SPLIT_MAX_SEG = 16;        /* segments per row */
@@ -540,14 +541,55 @@ bool try_split(const SampleArgs &a, int nseg, void *ws, size_t ws_bytes, hipStre
 
 size_t split_counter_bytes() { return SPLIT_CNT_BYTES; }
 
-int split_segments(const SampleArgs &a, Dtype dt) {
-  const int EPC = dt == DT_F32 ? 4 : 8;
-  const int cap = SPLIT_NW * SPLIT_CPT * WAVE;
-  const int nchunks = (EPC - 1 + a.vocab + EPC - 1) / EPC; /* any start offset */
-  const int nseg = (nchunks + cap - 1) / cap;
-  if (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG || (int64_t)a.n_rows * nseg > SPLIT_MAX_BLOCKS) return 0;
-  return nseg;
+namespace {
+
+/* compute units of the current device (queried once per device) */
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
 }
+
+struct SplitShape {
+  int cpt, nseg; /* nseg 0: the segmented kernel does not take the rows */
+};
+
+/* The segments' form for these rows: SPLIT_CPT chunks per lane, or
+ * SPLIT_CPT_WIDE when its launch (fewer, longer segments) fills whole rounds
+ * of the CUs more evenly and fits in one round (the bf16 form runs three
+ * workgroups per CU).  A row's merge waits for its slowest segment, and a CU
+ * holding one workgroup more than the others makes that segment slow. */
+SplitShape split_shape(const SampleArgs &a, Dtype dt) {
+  const int EPC = dt == DT_F32 ? 4 : 8;
+  const int nchunks = (EPC - 1 + a.vocab + EPC - 1) / EPC; /* any start offset */
+  const int cus = device_cus();
+  SplitShape best{SPLIT_CPT, 0};
+  double best_fill = -1.0;
+  for (const int cpt : {SPLIT_CPT, SPLIT_CPT_WIDE}) {
+    const int cap = SPLIT_NW * cpt * WAVE;
+    const int nseg = (nchunks + cap - 1) / cap;
+    const int64_t blocks = (int64_t)a.n_rows * nseg;
+    if (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG || blocks > SPLIT_MAX_BLOCKS) continue;
+    const int per_cu = cpt == SPLIT_CPT_WIDE && dt == DT_BF16 ? 3 : 4; /* registers */
+    if (cpt == SPLIT_CPT_WIDE && blocks > (int64_t)cus * per_cu) continue;
+    const int64_t rounds = (blocks + cus - 1) / cus;
+    const double fill = (double)blocks / (double)(rounds * cus);
+    if (fill > best_fill + 1e-9) {
+      best = SplitShape{cpt, nseg};
+      best_fill = fill;
+    }
+  }
+  return best;
+}
+
+}  // namespace
+
+int split_segments(const SampleArgs &a, Dtype dt) { return split_shape(a, dt).nseg; }
 
 size_t split_workspace_bytes(const SampleArgs &a, Dtype dt) {
   const int nseg = split_segments(a, dt);
@@ -556,10 +598,13 @@ size_t split_workspace_bytes(const SampleArgs &a, Dtype dt) {
 }
 
 bool launch_split(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
-  const int nseg = split_segments(a, dt);
-  if (!nseg) return false;
-  return dt == DT_F32 ? try_split<SPLIT_CPT, false>(a, nseg, ws, ws_bytes, s)
-                      : try_split<SPLIT_CPT, true>(a, nseg, ws, ws_bytes, s);
+  const SplitShape sh = split_shape(a, dt);
+  if (!sh.nseg) return false;
+  if (sh.cpt == SPLIT_CPT_WIDE)
+    return dt == DT_F32 ? try_split<SPLIT_CPT_WIDE, false>(a, sh.nseg, ws, ws_bytes, s)
+                        : try_split<SPLIT_CPT_WIDE, true>(a, sh.nseg, ws, ws_bytes, s);
+  return dt == DT_F32 ? try_split<SPLIT_CPT, false>(a, sh.nseg, ws, ws_bytes, s)
+                      : try_split<SPLIT_CPT, true>(a, sh.nseg, ws, ws_bytes, s);
 }
 
 }  // namespace d3s

@@ -379,16 +379,36 @@ def test_wide_kernel_on_many_rows(gpu, oracle, bf16):
     compare(oracle, gpu, xs, u, 0.8, 0.9, label=f"wide kernel, {N} rows bf16={bf16}")
 
 
-def split_bounds(V, bf16, row):
+def split_shape(V, bf16, N, cus=256):
+    """(chunks per lane, segments per row) the segmented kernel picks for N rows
+    of V (0 segments: it does not take them): 8 chunks per lane, or 10 when
+    that launch fills whole rounds of the CUs more evenly and fits in one
+    round (three bf16 workgroups per CU); segments of 4 waves x 64 lanes."""
+    EPC = 8 if bf16 else 4
+    nchunks = (EPC - 1 + V + EPC - 1) // EPC
+    best, fill_best = (8, 0), -1.0
+    for cpt in (8, 10):
+        nseg = -(-nchunks // (256 * cpt))
+        blocks = N * nseg
+        if not (2 <= nseg <= 16 and blocks <= 4096):
+            continue
+        if cpt == 10 and blocks > cus * (3 if bf16 else 4):
+            continue
+        fill = blocks / (-(-blocks // cus) * cus)
+        if fill > fill_best + 1e-9:
+            best, fill_best = (cpt, nseg), fill
+    return best
+
+
+def split_bounds(V, bf16, row, N):
     """Positions where the segmented kernel's segments of row `row` begin (rows
     contiguous from a 16-byte aligned base): the row's 16-byte chunks from the
-    aligned address at or below its start, in nseg equal parts of at most 2048
-    chunks; nseg from the chunk count at any start offset.  Empty when the
-    row is not cut (2 to 16 segments)."""
+    aligned address at or below its start, in nseg equal parts (split_shape).
+    Empty when the row is not cut."""
     EPC, ES = (8, 2) if bf16 else (4, 4)
     off = (row * V * ES) % 16 // ES
-    nseg = -(-((EPC - 1 + V + EPC - 1) // EPC) // 2048)
-    if not 2 <= nseg <= 16:
+    nseg = split_shape(V, bf16, N)[1]
+    if nseg == 0:
         return np.array([], np.int64)
     segc = -(-((off + V + EPC - 1) // EPC) // nseg)
     return np.array([s * segc * EPC - off for s in range(1, nseg)], np.int64)
@@ -396,10 +416,11 @@ def split_bounds(V, bf16, row):
 
 @pytest.mark.parametrize("V,bf16,N", [(8190, False, 20), (16381, False, 12), (16382, True, 9),
                                       (131069, False, 4), (262137, True, 3), (262138, True, 2),
-                                      (40000, True, 40), (151936, True, 6)])
+                                      (327674, True, 2), (40000, True, 40), (151936, True, 6),
+                                      (151936, True, 64)])
 def test_segmented_rows(gpu, oracle, V, bf16, N):
-    """Rows cut into equal segments of at most 2048 chunks (2 to 16 per row,
-    and one past the most: the generic kernel), with structure across
+    """Rows cut into equal segments of at most 2048 or 2560 chunks (2 to 16 per
+    row, and one past the most: the generic kernel), with structure across
     segments: the top k at segment bounds, a NaN in the last segment, a
     segment all -inf, the banned index at a bound, fewer finite elements than
     k, per-row T and top_p; against the oracle and the generic kernel."""
@@ -408,7 +429,7 @@ def test_segmented_rows(gpu, oracle, V, bf16, N):
     seg = 8192 * (2 if bf16 else 1)  # nominal bounds for rows that are not cut
 
     def bounds(r):
-        b = split_bounds(V, bf16, r)
+        b = split_bounds(V, bf16, r, N)
         return b if len(b) else np.arange(seg, V, seg)
 
     if N > 1 and len(bounds(1)):
