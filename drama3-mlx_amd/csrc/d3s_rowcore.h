@@ -192,12 +192,14 @@ struct Chunks {
   /* through a buffer resource spanning the row's chunks: a chunk past the
    * row's last reads as zeros (masked by the caller), and no per-chunk
    * address arithmetic is needed */
+  /* AUX: the loads' cache policy (2: nontemporal, for rows read once) */
+  template <int AUX = 0>
   __device__ __forceinline__ void load(const uint4 *src, int nchunks, int lane) {
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, nchunks * 16, BUFFER_FLAGS);
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane * 16, j * WAVE * 16, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane * 16, j * WAVE * 16, AUX);
       const uint4 q = make_uint4(v[0], v[1], v[2], v[3]);
       w[4 * j] = q.x;
       w[4 * j + 1] = q.y;

@@ -253,7 +253,11 @@ struct WaveRow {
 
   __device__ __forceinline__ void load() {
     setup();
-    c.load(src, nchunks, lane);
+    /* rows taken once (candidates from the registers) stream past the caches */
+    if (reg_cands)
+      c.template load<2>(src, nchunks, lane);
+    else
+      c.load(src, nchunks, lane);
     /* the partial chunk at the row start and every chunk row from the one
      * holding the row end on */
     const int jlast = (nchunks - 1) / WAVE;
