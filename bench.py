@@ -5,8 +5,9 @@ Headline (`value`): sampled rows/s on C3, the batched backbone head
 launches, `--batches-per-launch` batches of 256 rows per d3s_sample call
 (default 512: 131 072 rows), taken in turn by `--headline-streams` streams
 (default 3), so that one launch's last waves overlap the next one's first.
-A step is one such launch: `--warmup` untimed launches, then `--steps` timed
-ones (ms_per_step is per launch).  The launches cycle over
+A step is one such launch: 40 ms of untimed launches and `--warmup` more,
+back to back (sustained load runs slower for its first ~30 ms), then
+`--steps` timed ones (ms_per_step is per launch).  The launches cycle over
 a pool of `--pool-batches` batches in device memory (default 512 batches,
 2.2 GB, over eight times the 256 MB Infinity Cache, so every launch reads HBM;
 16 distinct generated contents, every batch with its own uniforms).  Beside it: one batch
@@ -80,16 +81,19 @@ class Pool:
                               ("ptr", self.top_p.ptr + r0 * 4), None, ids.ptr, stream=stream)
 
 
-def time_launches(pool, launches, warmup, g, n_streams):
-    """`warmup` untimed launches, then `launches` timed launches of g batches
-    each, round robin over n_streams streams, between a start event on the
-    first stream (the others wait on it) and a stop event after every
-    stream's last launch; returns (device ms between the events, host wall s,
-    launches timed)."""
+def time_launches(pool, launches, warmup, g, n_streams, settle=0):
+    """`settle` then `warmup` untimed launches, enqueued back to back, then
+    `launches` timed launches of g batches each, round robin over n_streams
+    streams, between a start event on the first stream (the others wait on
+    it) and a stop event after every stream's last launch; returns (device ms
+    between the events, host wall s, launches timed)."""
     import hiprt
     streams = [hiprt.Stream() for _ in range(n_streams)]
     ids = [hiprt.DeviceBuffer(4 * ROWS * g) for _ in range(n_streams)]
     windows = pool.n // g
+    for i in range(settle):
+        s = i % n_streams
+        assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
     for i in range(warmup):
         s = i % n_streams
         assert pool.launch((i % windows) * g, g, ids[s], streams[s].ptr) == 0
@@ -119,6 +123,19 @@ def time_launches(pool, launches, warmup, g, n_streams):
 
 
 PREWARM_S = 0.3
+# Sustained load that starts after more than a few ms of idle runs slower for
+# its first ~30 ms: per-launch events on one stream, headline launches back
+# to back, read 330 us, then rise to 400-460 us from the sixth launch on and
+# fall back to ~330 us over the next ~100 launches; 5 warm-up + 20 timed
+# launches after 10-200 ms idle read 383-405 us per launch, after 120
+# back-to-back launches 313-316 us.  Every timed phase therefore follows
+# SETTLE_S of the same launches, enqueued back to back with its warm-up.
+SETTLE_S = 0.04
+
+
+def settle_launches(t_launch):
+    """launches of t_launch seconds each that fill SETTLE_S"""
+    return int(SETTLE_S / max(t_launch, 5e-6)) + 1
 
 
 def prewarm(pool, g):
@@ -654,13 +671,15 @@ def main():
         return
     # clocks settle: headline launches for at least PREWARM_S seconds before
     # anything is timed (a fresh box runs its first ~10 ms of launches about
-    # 15 % slower), then --warmup untimed launches, then --steps timed ones
+    # 15 % slower); then each timed phase: SETTLE_S of untimed launches and
+    # --warmup more, back to back, a synchronisation, --steps timed launches
     prewarm_launches = prewarm(pool, G)
-    log(f"pre-warm: {prewarm_launches} launches over {PREWARM_S} s")
+    n_settle = settle_launches(PREWARM_S / prewarm_launches)
+    log(f"pre-warm: {prewarm_launches} launches over {PREWARM_S} s; {n_settle} settle launches per phase")
     # the dominant kernel alone: G batches per launch, back to back on one
     # stream, HIP events on that stream (the roofline's launch duration)
     bytes_per_launch = G * ROWS * BYTES_PER_ROW
-    ms_k, _, lk = time_launches(pool, args.steps, args.warmup, G, 1)
+    ms_k, _, lk = time_launches(pool, args.steps, args.warmup, G, 1, n_settle)
     kmean = ms_k * 1e3 / lk
     achieved = bytes_per_launch / (kmean * 1e-6) / 1e9
     log(f"one stream: {lk} timed launches of {G} batches after {args.warmup} untimed, {kmean:.2f} us per "
@@ -668,7 +687,7 @@ def main():
     # headline: the same launches taken in turn by S streams, so that one
     # launch's last waves overlap the next launch's first
     S = args.headline_streams
-    ms, wall, launches = time_launches(pool, args.steps, args.warmup, G, S)
+    ms, wall, launches = time_launches(pool, args.steps, args.warmup, G, S, n_settle)
     batches = launches * G
     value = batches * ROWS / (ms * 1e-3)
     job_gbs = value * BYTES_PER_ROW / 1e9
@@ -676,10 +695,11 @@ def main():
         f"{ms:.2f} ms: {value:.3e} rows/s -> {job_gbs:.0f} GB/s (host wall {wall:.3f} s)")
     # one batch (256 rows) per launch, one stream and several
     n1 = 5000
-    ms1, _, l1 = time_launches(pool, n1, 100, 1, 1)
+    n1_settle = settle_launches(1e-5)
+    ms1, _, l1 = time_launches(pool, n1, 100, 1, 1, n1_settle)
     single = l1 * ROWS / (ms1 * 1e-3)
     log(f"one batch per launch, one stream: {single:.3e} rows/s ({ms1 * 1e3 / l1:.2f} us/launch)")
-    msS, _, lS = time_launches(pool, n1, 100, 1, args.streams)
+    msS, _, lS = time_launches(pool, n1, 100, 1, args.streams, n1_settle)
     multi = lS * ROWS / (msS * 1e-3)
     log(f"one batch per launch, {args.streams} streams: {multi:.3e} rows/s")
     floor_us = launch_floor(500)
@@ -728,7 +748,10 @@ def main():
                                    f"taken in turn by {S} streams",
                    "batches_per_launch": G, "streams": S,
                    "prewarm": f"{prewarm_launches} untimed launches over {PREWARM_S} s before the "
-                              f"--warmup launches (clocks settle)"},
+                              f"first phase (clocks settle)",
+                   "settle": f"{n_settle} untimed launches ({SETTLE_S * 1e3:.0f} ms) back to back with "
+                             f"the --warmup launches before each timed phase: sustained load runs "
+                             f"slower for its first ~30 ms"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel_us_mean": kmean, "bytes_per_launch": bytes_per_launch,
