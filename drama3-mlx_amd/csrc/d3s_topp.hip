@@ -222,7 +222,350 @@ __device__ __forceinline__ void block_argmax(float &s, int &r, TRed &R) {
   r = (int)uni_u32((uint32_t)r);
 }
 
-template <int EPT, bool BF16, int TBLOCK>
+/* The cut's certain bands (phase 4 below): ranks whose prefix Q_r of the terms
+ * fix40(e_r) reaches tdrop certainly drop, those below tkeep certainly stay.
+ * With G = exp(m - lse) and G' = 2^40 / S, |P_r - Q_r G'| <= eps' (Q_r + k) G'
+ * + k, P_r the exact prefix of the terms fix40(expf(x_r - lse)).  eps' is each
+ * term's relative error, its two argument roundings (2^-24 z on either side,
+ * z = lse - x_r <= min(lse - xmin, 30): terms with larger z are below one unit
+ * on both sides) and two expf ulps, plus G's against G' (the roundings of
+ * S 2^-40, of m + log S, and the log's ulp).  Tq: the smallest prefix that
+ * passes top_p; 0 < Tq <= k 2^41. */
+struct CutBands {
+  uint64_t tdrop, tkeep;
+};
+__device__ __forceinline__ CutBands topp_cut_bands(uint64_t Tq, uint64_t S, float lse, float lnS, float xmin, int k) {
+  /* in fp32: S' = RN(S 2^-40) = 1 / G' within 2^-24; every product and
+   * conversion below is within a relative 2^-23, inside the extra 2^-20 */
+  const float Sf = d3s_fixsum_to_f32(S);
+  const float zf = lse - xmin;
+  const float z = zf < 30.0f ? zf : 30.0f; /* NaN and inf too */
+  const float et = 0x1p-24f * 1.01f * 2.0f * z + 0x1p-22f;
+  const float ulp_ln = lnS > 0x1p-126f ? ldexpf(1.0f, ilogbf(lnS) - 23) : 0x1p-126f;
+  const float eg = 0x1p-24f * 1.01f * (fabsf(lse) + 1.0f) + 1.01f * ulp_ln;
+  const float ep = (et * 1.0001f + 1.01f * eg) * (1.0f + 1.01f * eg);
+  const float slack = ep * (float)k / Sf + (float)k;
+  const float Tqf = (float)Tq;
+  /* 1 / (1 - ep) <= 1 + 1.13 ep and 1 / (1 + ep) >= 1 - ep for ep < 1/16 */
+  const float dd = (Tqf + slack) * Sf * (1.0f + 1.13f * ep + 0x1p-20f);
+  const float dk = (Tqf - slack) * Sf * (1.0f - ep - 0x1p-20f);
+  /* (an lse so large that the band is wide leaves every rank to the exact
+   * prefixes: no rank certainly drops, none certainly stays) */
+  const bool wide = !(ep < 0x1p-4f);
+  CutBands c;
+  c.tdrop = wide || !(dd < 0x1p62f) ? ~0ull : (uint64_t)dd + 2ull;
+  c.tkeep = wide || !(dk > 2.0f) ? 0ull : (dk < 0x1p62f ? (uint64_t)dk - 1ull : (1ull << 62));
+  return c;
+}
+
+/* ---- The ids-only path (no probabilities or candidates asked for, k = V).
+ * The race reads every kept rank's uniform u[r], but a rank's bucket already
+ * bounds its probability (the bucket bounds m - x), and only the few ranks
+ * whose score's upper bound reaches the largest lower bound need their
+ * element.  No element is ranked but those of the buckets such ranks fall
+ * in and those of the group of buckets that holds the cut:
+ *  3'. bucket counts (as phase 3) and per-group sums of fix40(e), a group
+ *      being the PER buckets one thread scans; their exclusive scans give
+ *      each bucket's first rank and each group's prefix Q at its start; a map
+ *      from rank to bucket holds each non-empty bucket's id at its first rank.
+ *  4'. the cut as phase 4: the first group whose end reaches the certain drop
+ *      band holds the first certain drop; one wave ranks that group's
+ *      elements and sums their prefixes.  A cut that is not certain leaves
+ *      the row to the full path.
+ *  5'. each kept rank's score bounds from its bucket's bounds on e and its
+ *      uniform; the candidates (upper bound at least the largest lower bound)
+ *      are resolved: one wave ranks the elements of their buckets and each
+ *      candidate's element takes the exact score.  The first maximum of the
+ *      candidates' scores is the row's, as every rank whose exact score ties
+ *      or beats it is a candidate.
+ * Returns the id, or TOPP_FULL for the full path: a cut within the bands'
+ * uncertainty, a group or the candidates' buckets with more elements than a
+ * wave holds, no positive kept score.  Called by every thread; every return
+ * follows a barrier. */
+constexpr int TOPP_FULL = -2;
+constexpr int TF_CAP = WAVE; /* the elements one wave resolves */
+
+/* byte offsets in the dynamic LDS region: group sums (one per thread), the
+ * resolved elements' keys and values, counters, bucket and rank bitmaps, the
+ * rank -> bucket map */
+__host__ __device__ constexpr size_t tf_lkey(int tb) { return 8 * (size_t)tb; }
+__host__ __device__ constexpr size_t tf_lval(int tb) { return tf_lkey(tb) + 8 * TF_CAP; }
+__host__ __device__ constexpr size_t tf_misc(int tb) { return tf_lval(tb) + 8 * TF_CAP; }
+__host__ __device__ constexpr size_t tf_cbits(int tb) { return tf_misc(tb) + 64; }
+__host__ __device__ constexpr size_t tf_rbits(int tb, int nbk) { return tf_cbits(tb) + 4 * (size_t)(nbk / 32 + 4); }
+__host__ __device__ constexpr size_t tf_map(int tb, int nbk, int V) {
+  return tf_rbits(tb, nbk) + 16 * (size_t)((V + 127) / 128);
+}
+__host__ __device__ constexpr size_t tf_bytes(int tb, int nbk, int V) {
+  return tf_map(tb, nbk, V) + 2 * (size_t)((V + 7) & ~7);
+}
+
+/* 3' before the row is read: the bucket counts, group sums, map and bitmaps
+ * cleared (phase 1's barriers order this before the counting) */
+template <int TBLOCK, int NBK>
+__device__ __forceinline__ void topp_fast_clear(int V, uint32_t *bstart, char *dyn) {
+  const int tid = (int)threadIdx.x;
+#pragma unroll
+  for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
+  if (tid == 0) bstart[NBK] = 0u;
+  if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = 0u;
+  ((uint64_t *)dyn)[tid] = 0ull;
+  uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
+  uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
+  uint32_t *rmap = (uint32_t *)(dyn + tf_map(TBLOCK, NBK, V));
+  for (int w = tid; w < ((V + 7) & ~7) / 2; w += TBLOCK) rmap[w] = 0u;
+  for (int w = tid; w < NBK / 32 + 4; w += TBLOCK) cbits[w] = 0u;
+  for (int w = tid; w < 4 * ((V + 127) / 128); w += TBLOCK) rbits[w] = 0u;
+}
+
+/* the bucket of x (x <= m; NBK for -inf) */
+template <int NBK>
+__device__ __forceinline__ int topp_bucket(float x, float m, float scale) {
+  return x != -__builtin_inff() ? min((int)((m - x) * scale), NBK - 1) : NBK;
+}
+
+/* 3'-5' once the counts and group sums are in (bk: each element's bucket) */
+template <int EPT, int TBLOCK, int NBK>
+__device__ __forceinline__ int topp_fast(const SampleArgs &a, int row, const float (&x)[EPT], const int (&bk)[EPT],
+                                         float m, float xmin, float scale, uint64_t S, float lse, float lnS,
+                                         float top_p, uint32_t *bstart, char *dyn, TRed &R) {
+  constexpr int PER = NBK / TBLOCK;
+  static_assert(PER % 4 == 0, "whole 16-byte groups of buckets per thread");
+  const int V = a.vocab, k = a.k;
+  const int tid = (int)threadIdx.x, lane = lane_id();
+  uint64_t *gsum = (uint64_t *)dyn;
+  uint64_t *lkey = (uint64_t *)(dyn + tf_lkey(TBLOCK));
+  uint64_t *lval = (uint64_t *)(dyn + tf_lval(TBLOCK));
+  uint32_t *misc = (uint32_t *)(dyn + tf_misc(TBLOCK)); /* [0] list count, [1] cut, [2] id */
+  uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32); /* [0] a group's start, [1] Q at cut - 1 */
+  uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
+  uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
+  uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V));
+
+  /* this thread's ranks, for the race */
+  const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
+  const int r0 = tid * RPT;
+
+  {
+    /* bucket starts (exclusive scan, as phase 3); each non-empty bucket's id
+     * at its first rank in the map */
+    uint4 c[PER / 4];
+    uint32_t loc = 0u;
+#pragma unroll
+    for (int q = 0; q < PER / 4; q++) {
+      c[q] = *(const uint4 *)&bstart[tid * PER + 4 * q];
+      loc += c[q].x + c[q].y + c[q].z + c[q].w;
+    }
+    uint32_t tot;
+    uint32_t run = block_excl_scan_u32(loc, R, tot);
+#pragma unroll
+    for (int q = 0; q < PER / 4; q++) {
+      const uint32_t cc[4] = {c[q].x, c[q].y, c[q].z, c[q].w};
+      uint32_t st[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        st[e] = run;
+        if (cc[e] != 0u) rmap[run] = (uint16_t)(tid * PER + 4 * q + e);
+        run += cc[e];
+      }
+      *(uint4 *)&bstart[tid * PER + 4 * q] = make_uint4(st[0], st[1], st[2], st[3]);
+    }
+    if (tid == 0) {
+      bstart[NBK] = tot;
+      if (tot < (uint32_t)V) rmap[tot] = (uint16_t)NBK;
+    }
+  }
+  /* each group's prefix at its start (the scan's barriers also publish the
+   * starts and the map) */
+  const uint64_t gs = gsum[tid];
+  const uint64_t gst = block_excl_scan_u64(gs, R);
+
+  /* ---- 4'. the cut, and Q at the rank before it (the kept sum) */
+  const uint64_t Tq = d3s_fixsum_gt_threshold(top_p);
+  int cut;
+  uint64_t qlast;
+  if (Tq == 0ull) {
+    cut = 1; /* rank 0's term: e_0 = 1 */
+    qlast = 1ull << 40;
+  } else if (Tq > ((uint64_t)k << 41)) {
+    cut = k;
+    qlast = S;
+  } else {
+    const CutBands cb = topp_cut_bands(Tq, S, lse, lnS, xmin, k);
+    const int g = block_min_i32(gst + gs >= cb.tdrop ? tid : 0x7fffffff, R);
+    if (g == 0x7fffffff) {
+      cut = k; /* no rank certainly drops: the last must certainly stay */
+      qlast = S;
+    } else {
+      const uint32_t s0 = bstart[g * PER], n = bstart[g * PER + PER] - s0;
+      if (n > (uint32_t)TF_CAP) {
+        __syncthreads();
+        return TOPP_FULL;
+      }
+      if (tid == g) misc64[0] = gst;
+#pragma unroll
+      for (int j = 0; j < EPT; j++) {
+        const int i = j * TBLOCK + tid;
+        const bool in = i < V && bk[j] / PER == g; /* (the -inf bucket's is no group) */
+        const int slot = wave_append(in, (int *)&misc[0]);
+        if (in) lkey[slot] = composite_key(x[j], i);
+      }
+      __syncthreads();
+      if (tid < WAVE) {
+        /* lane t: element t of the group, its term fix40(e), rank and
+         * inclusive prefix */
+        const uint64_t q0 = misc64[0];
+        const bool mine = lane < (int)n;
+        const uint64_t mk = mine ? lkey[lane] : 0ull;
+        if (mine) lval[lane] = d3s_fix40_unit(d3s_expf_nonpos(key_x(mk) - m));
+        wave_lds_sync();
+        int rho = 0;
+        uint64_t inc = 0ull;
+        for (int t = 0; t < (int)n; t++) {
+          const uint64_t kk = lkey[t], vv = lval[t];
+          rho += kk > mk ? 1 : 0;
+          inc += kk >= mk ? vv : 0ull;
+        }
+        const int r = (int)s0 + rho;
+        const uint64_t qr = q0 + inc;
+        /* the first rank reaching the band (the group's last does); rank 0
+         * never drops */
+        const int r1 = wave_min_i32(mine && qr >= cb.tdrop ? r : 0x7fffffff);
+        const int c2 = min(max(r1, 1), k);
+        uint64_t ql = q0; /* c2 - 1 = s0 - 1: the prefix before the group */
+        if (c2 - 1 >= (int)s0) {
+          const uint64_t at = __ballot(mine && r == c2 - 1);
+          const int src = (int)__builtin_ctzll(at | (1ull << 63));
+          ql = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
+        }
+        if (lane == 0) {
+          misc[1] = (uint32_t)c2;
+          misc64[1] = ql;
+          misc[0] = 0u; /* the list is free again */
+        }
+      }
+      __syncthreads();
+      cut = (int)misc[1];
+      qlast = misc64[1];
+    }
+    if (cut > 1 && !(qlast < cb.tkeep)) {
+      __syncthreads();
+      return TOPP_FULL;
+    }
+  }
+  const float inv = 1.0f / d3s_fixsum_to_f32(qlast);
+
+  /* ---- 5'. score bounds per kept rank from its bucket: elements of finite
+   * bucket b < NBK - 1 have t = RN(RN(m - x) scale) in [b, b + 1), so
+   * RN(m - x) = x's distance d' lies in [b (1 - 2^-24), (b + 1) (1 + 2^-24)]
+   * / scale (the last finite bucket: up to RN(m - xmin)); z_lo and z_hi below
+   * are outside that with the roundings of 1 / scale and the products.  e =
+   * expf(-d') within an ulp; the hardware 2^(-z log2 e) is within 2^-21 and
+   * the product's rounding within 2^-16 for z <= 104 (below that e is 0 or
+   * subnormal), all inside the 2^-12 margins; e_hi is at least 2^-126 (above
+   * every subnormal), e_lo 0 far out.  p = RN(e inv) is monotone in e. */
+  /* the kept ranks' uniforms (the dropped ranks' are not read) */
+  float uv[EPT];
+#pragma unroll
+  for (int q = 0; q < EPT; q++) uv[q] = (q < RPT && r0 + q < cut) ? a.u[(size_t)row * k + r0 + q] : 0.0f;
+  int b = 0;
+  if (r0 < cut) {
+    int lo = 0, hi = NBK + 1; /* the largest b with start(b) <= r0 */
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (bstart[mid] <= (uint32_t)r0)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    b = lo;
+  }
+  const float rs = 1.0f / scale, dmax = m - xmin;
+  const int bfirst = b;
+  float hb[EPT];
+  float lbm = -1.0f;
+#pragma unroll
+  for (int q = 0; q < EPT; q++) {
+    const int r = r0 + q;
+    hb[q] = -__builtin_inff();
+    if (q < RPT && r < cut) {
+      if (q > 0) b = max(b, (int)rmap[r]);
+      float elo = 0.0f, ehi = 0.0f; /* the -inf bucket: e = 0 */
+      if (b < NBK) {
+        const float zlo = (float)b * rs * (1.0f - 0x1p-18f);
+        const float zhi = (b < NBK - 1 ? (float)(b + 1) * rs : dmax) * (1.0f + 0x1p-18f);
+        ehi = fmaxf(__builtin_amdgcn_exp2f(-zlo * 1.44269504f) * (1.0f + 0x1p-12f), 0x1p-126f);
+        elo = zhi < 87.0f ? __builtin_amdgcn_exp2f(-zhi * 1.44269504f) * (1.0f - 0x1p-12f) : 0.0f;
+      }
+      const float plo = elo * inv, phi = ehi * inv;
+      const float uu = uv[q];
+      /* the full path's bounds (phase 5) at p_lo and p_hi */
+      float lb = -1.0f, h = __builtin_inff();
+      if (uu >= 0x1p-24f && uu < 1.0f) {
+        lb = plo * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * (1.0f - 0x1p-18f);
+        if (uu > 0x1p-24f) h = phi * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * (1.0f + 0x1p-18f);
+      } else if (uu >= 1.0f) {
+        h = 0.0f;
+      }
+      hb[q] = h;
+      lbm = fmaxf(lbm, lb);
+    }
+  }
+  const float LB = block_max_f(lbm, R);
+  b = bfirst;
+#pragma unroll
+  for (int q = 0; q < EPT; q++) {
+    const int r = r0 + q;
+    if (q > 0 && q < RPT && r < cut) b = max(b, (int)rmap[r]);
+    if (hb[q] >= LB) { /* only kept ranks: the others hold -inf */
+      atomicOr(&rbits[r >> 5], 1u << (r & 31));
+      atomicOr(&cbits[b >> 5], 1u << (b & 31));
+    }
+  }
+  __syncthreads();
+  /* the elements of the candidates' buckets */
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    const int bb = bk[j];
+    const bool in = i < V && ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u;
+    const int slot = wave_append(in, (int *)&misc[0]);
+    if (in && slot < TF_CAP) {
+      lkey[slot] = composite_key(x[j], i);
+      lval[slot] = (uint64_t)bb;
+    }
+  }
+  __syncthreads();
+  const uint32_t n2 = misc[0];
+  if (n2 > (uint32_t)TF_CAP) return TOPP_FULL; /* (after the barrier above) */
+  if (tid < WAVE) {
+    const bool mine = lane < (int)n2;
+    const uint64_t mk = mine ? lkey[lane] : 0ull;
+    const uint64_t mb = mine ? lval[lane] : ~0ull;
+    int rho = 0;
+    for (int t = 0; t < (int)n2; t++) rho += (lval[t] == mb && lkey[t] > mk) ? 1 : 0;
+    float bs = -2.0f;
+    int br = 0x7fffffff;
+    if (mine) {
+      const int r = (int)bstart[(int)mb] + rho;
+      if (r < cut && ((rbits[r >> 5] >> (r & 31)) & 1u) != 0u) {
+        const float e = d3s_expf_nonpos(key_x(mk) - m);
+        bs = topp_score(e * inv, a.u[(size_t)row * k + r]);
+        br = r;
+      }
+    }
+    const int myr = br;
+    wave_argmax(bs, br);
+    const uint64_t at = __ballot(mine && myr == br);
+    const int src = (int)__builtin_ctzll(at | (1ull << 63));
+    const int id = key_idx(((uint64_t)readlane_u((uint32_t)(mk >> 32), src) << 32) | readlane_u((uint32_t)mk, src));
+    if (lane == 0) misc[2] = bs > 0.0f ? (uint32_t)id : (uint32_t)TOPP_FULL;
+  }
+  __syncthreads();
+  return (int)misc[2];
+}
+
+template <int EPT, bool BF16, int TBLOCK, bool FAST>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
     SampleArgs a) {
   constexpr int NBK = topp_buckets(EPT * TBLOCK, TBLOCK);
@@ -248,6 +591,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   const bool t_finite = T < __builtin_inff();
   const float y = 1.0f / T;
   const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  if (FAST) topp_fast_clear<TBLOCK, NBK>(V, bstart, (char *)keys);
 
   /* ---- 1. x, classification, max and smallest finite x */
   float x[EPT];
@@ -282,22 +626,56 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   }
   const float xmin = -nxl;
 
+  const float dmax = m - xmin;
+  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
+
   /* ---- 2. e = exp(x - m) and the exact row sum and lse (x = -inf, and
    * i >= V, add 0); e is also each element's softmax term (x_0 = m) */
   float ev[EPT];
-  uint64_t acc = 0;
+  uint64_t S;
+  float lnS, lse;
+  if (FAST && scale > 0.0f) {
+    /* the ids-only path: each element's term also goes to its bucket's
+     * count and its group's sum, and e is not kept */
+    constexpr int PER = NBK / TBLOCK;
+    int bk[EPT];
+    uint64_t acc = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    ev[j] = d3s_expf_nonpos(x[j] - m); /* in [0, 1] */
-    acc += d3s_fix40_unit(ev[j]);
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const uint64_t f = d3s_fix40_unit(d3s_expf_nonpos(x[j] - m));
+      acc += f;
+      const int b = topp_bucket<NBK>(x[j], m, scale);
+      bk[j] = b;
+      if (i < V) {
+        atomicAdd(&bstart[b], 1u);
+        if (b < NBK) atomicAdd((unsigned long long *)&keys[b / PER], (unsigned long long)f);
+      }
+    }
+    S = block_sum_u64(acc, R); /* (its barriers also close the counting) */
+    lnS = d3s_logf(d3s_fixsum_to_f32(S));
+    lse = m + lnS;
+    const int id = topp_fast<EPT, TBLOCK, NBK>(a, row, x, bk, m, xmin, scale, S, lse, lnS, rp.top_p, bstart,
+                                               (char *)keys, R);
+    if (id != TOPP_FULL) {
+      if (tid == 0) a.ids[row] = id;
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; j++) ev[j] = d3s_expf_nonpos(x[j] - m);
+  } else {
+    uint64_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      ev[j] = d3s_expf_nonpos(x[j] - m); /* in [0, 1] */
+      acc += d3s_fix40_unit(ev[j]);
+    }
+    S = block_sum_u64(acc, R);
+    lnS = d3s_logf(d3s_fixsum_to_f32(S));
+    lse = m + lnS;
   }
-  const uint64_t S = block_sum_u64(acc, R);
-  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
-  const float lse = m + lnS;
 
   /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
-  const float dmax = m - xmin;
-  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
 #pragma unroll
   for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) bstart[NBK] = 0u;
@@ -384,15 +762,9 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
 
   /* ---- 4. the cut: the first r > 0 whose exact prefix P_r of the terms
    * fix40(expf(x_r - lse)) passes top_p (fixsum_to_f32(P) > top_p is P >=
-   * Tq).  First from the prefixes Q_r of fix40(e_r): with G = exp(m - lse)
-   * and G' = 2^40 / S, |P_r - Q_r G'| <= eps' (Q_r + k) G' + k.  eps' is
-   * each term's relative error, its two argument roundings (2^-24 z on
-   * either side, z = lse - x_r <= min(lse - xmin, 30): terms with larger z
-   * are below one unit on both sides) and two expf ulps, plus G's against
-   * G' (the roundings of S 2^-40, of m + log S, and the log's ulp).  Ranks
-   * with Q_r >= Tdrop certainly drop, those with Q_r < Tkeep certainly stay;
-   * if the rank before the first certain drop does not certainly stay, the
-   * exact prefixes decide. */
+   * Tq).  First from the prefixes Q_r of fix40(e_r) and the certain bands
+   * (topp_cut_bands): if the rank before the first certain drop does not
+   * certainly stay, the exact prefixes decide. */
   const uint64_t Tq = d3s_fixsum_gt_threshold(rp.top_p);
   uint64_t qt[EPT];
   uint64_t qloc = 0;
@@ -410,25 +782,8 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   } else if (Tq > ((uint64_t)k << 41)) {
     cut = k; /* no prefix of at most k terms below 1 reaches it */
   } else {
-    /* in fp32: S' = RN(S 2^-40) = 1 / G' within 2^-24; every product and
-     * conversion below is within a relative 2^-23, inside the extra 2^-20 */
-    const float Sf = d3s_fixsum_to_f32(S);
-    const float zf = lse - xmin;
-    const float z = zf < 30.0f ? zf : 30.0f; /* NaN and inf too */
-    const float et = 0x1p-24f * 1.01f * 2.0f * z + 0x1p-22f;
-    const float ulp_ln = lnS > 0x1p-126f ? ldexpf(1.0f, ilogbf(lnS) - 23) : 0x1p-126f;
-    const float eg = 0x1p-24f * 1.01f * (fabsf(lse) + 1.0f) + 1.01f * ulp_ln;
-    const float ep = (et * 1.0001f + 1.01f * eg) * (1.0f + 1.01f * eg);
-    const float slack = ep * (float)k / Sf + (float)k;
-    const float Tqf = (float)Tq;
-    /* 1 / (1 - ep) <= 1 + 1.13 ep and 1 / (1 + ep) >= 1 - ep for ep < 1/16 */
-    const float dd = (Tqf + slack) * Sf * (1.0f + 1.13f * ep + 0x1p-20f);
-    const float dk = (Tqf - slack) * Sf * (1.0f - ep - 0x1p-20f);
-    /* (an lse so large that the band is wide leaves every rank to the exact
-     * prefixes: no rank certainly drops, none certainly stays) */
-    const bool wide = !(ep < 0x1p-4f);
-    const uint64_t Tdrop = wide || !(dd < 0x1p62f) ? ~0ull : (uint64_t)dd + 2ull;
-    const uint64_t Tkeep = wide || !(dk > 2.0f) ? 0ull : (dk < 0x1p62f ? (uint64_t)dk - 1ull : (1ull << 62));
+    const CutBands cb = topp_cut_bands(Tq, S, lse, lnS, xmin, k);
+    const uint64_t Tdrop = cb.tdrop, Tkeep = cb.tkeep;
     int drop = k;
     uint64_t Q = Qp;
 #pragma unroll
@@ -584,8 +939,16 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
 template <int EPT, bool BF16, int TBLOCK>
 bool try_topp(const SampleArgs &a, hipStream_t s) {
   if (a.vocab > EPT * TBLOCK) return false;
-  hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), (size_t)a.vocab * sizeof(uint64_t), s,
-                     a);
+  /* ids only, k = V (top-k disabled): the ids-only path first */
+  const bool fast = !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
+  /* the ranked keys, or the ids-only path's arrays */
+  const size_t ranked = (size_t)a.vocab * sizeof(uint64_t);
+  const size_t arrays = tf_bytes(TBLOCK, topp_buckets(EPT * TBLOCK, TBLOCK), a.vocab);
+  const size_t lds = ranked > arrays ? ranked : arrays;
+  if (fast)
+    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK, true>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
+  else
+    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK, false>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
   return true;
 }
 

@@ -56,6 +56,13 @@ def compare(oracle, gpu, logits, u, T, top_p, banned=None, flags=0, label="", ro
     both_nan = np.isnan(got["probs"]) & np.isnan(exp["probs"])
     assert np.array_equal(got["probs"][~both_nan], exp["probs"][~both_nan])
     np.testing.assert_allclose(got["probs"][~both_nan], exp["probs"][~both_nan], rtol=RTOL)
+    # the same call asking for ids only (the nucleus kernel then skips the
+    # ranking it needs only for probabilities and candidates)
+    ids_only = gpu.sample(logits, u, T, top_p, banned=banned, flags=flags, row_stride=row_stride,
+                          vocab=vocab, want_probs=False)
+    assert ids_only["rc"] == 0, ids_only["rc"]
+    bad = np.nonzero(ids_only["ids"] != exp["ids"])[0]
+    assert len(bad) == 0, ("ids only", bad[:10], ids_only["ids"][bad[:10]], exp["ids"][bad[:10]])
     return got, exp
 
 
