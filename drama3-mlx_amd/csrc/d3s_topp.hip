@@ -258,39 +258,43 @@ __device__ __forceinline__ CutBands topp_cut_bands(uint64_t Tq, uint64_t S, floa
   return c;
 }
 
-/* ---- The ids-only path (no probabilities or candidates asked for, k = V).
- * The race reads every kept rank's uniform u[r], but a rank's bucket already
- * bounds its probability (the bucket bounds m - x), and only the few ranks
- * whose score's upper bound reaches the largest lower bound need their
- * element.  No element is ranked but those of the buckets such ranks fall
- * in and those of the group of buckets that holds the cut:
- *  3'. bucket counts (as phase 3) and per-group sums of fix40(e), a group
- *      being the PER buckets one thread scans; their exclusive scans give
- *      each bucket's first rank and each group's prefix Q at its start; a map
- *      from rank to bucket holds each non-empty bucket's id at its first rank.
- *  4'. the cut as phase 4: the first group whose end reaches the certain drop
- *      band holds the first certain drop; one wave ranks that group's
- *      elements and sums their prefixes.  A cut that is not certain leaves
- *      the row to the full path.
- *  5'. each kept rank's score bounds from its bucket's bounds on e and its
- *      uniform; the candidates (upper bound at least the largest lower bound)
- *      are resolved: one wave ranks the elements of their buckets and each
- *      candidate's element takes the exact score.  The first maximum of the
- *      candidates' scores is the row's, as every rank whose exact score ties
- *      or beats it is a candidate.
- * Returns the id, or TOPP_FULL for the full path: a cut within the bands'
- * uncertainty, a group or the candidates' buckets with more elements than a
- * wave holds, no positive kept score.  Called by every thread; every return
- * follows a barrier. */
+/* ---- The ids-only path (k_topp_ids: no probabilities or candidates asked
+ * for, k = V).  The race reads every kept rank's uniform u[r], but a rank's
+ * bucket bounds its probability (the bucket bounds m - x), and only the few
+ * ranks whose score's upper bound reaches the largest lower bound need their
+ * element.  So no element is ranked but those of the group of buckets that
+ * holds the cut and those of the buckets such ranks fall in:
+ *  2'. with the row sum, each element's bucket count and its group's sum of
+ *      fix40(e) (a group: the PER buckets one thread scans); one scan gives
+ *      each bucket's first rank and each group's prefix Q at its start.
+ *  4'. the first group whose end reaches the certain drop band (phase 4's
+ *      bands) holds the first certain drop, so the cut lies in [klo, khi]:
+ *      the ranks before the group are kept, those after it dropped.
+ *  5'. scores are bounded in units of inv = 1 / (kept sum), which cancels
+ *      from every comparison: per rank, e <= 1 for the ranks that may be kept
+ *      and e >= emin (a bucket bound) for those certainly kept give the first
+ *      bounds and their largest lower bound LB1; the ranks whose upper bound
+ *      reaches LB1 (a handful) take their bucket's bounds on e (bucket found
+ *      by binary search over the starts), whose largest lower bound LB2 picks
+ *      the candidates.  One gather brings one wave the cut group's elements
+ *      and the candidates' buckets' elements; it ranks them, sums the cut
+ *      group's prefixes (the cut, and the kept sum), and takes the candidates'
+ *      exact scores: their first maximum is the row's (every rank whose exact
+ *      score reaches it is a candidate).
+ * A row takes the full path (phases 3-5) when its cut is within the bands'
+ * uncertainty, when more elements than a wave holds would go to that wave, or
+ * when no kept score is positive. */
 constexpr int TOPP_FULL = -2;
-constexpr int TF_CAP = WAVE; /* the elements one wave resolves */
+constexpr int TF_CAP = WAVE; /* the elements (and refined ranks) one wave takes */
 
-/* byte offsets in the dynamic LDS region: group sums (one per thread), the
- * resolved elements' keys and values, counters, bucket and rank bitmaps, the
- * rank -> bucket map */
+/* byte offsets in the dynamic LDS region: group sums (one per thread); the
+ * gathered elements' keys and buckets; the refined ranks and their uniforms;
+ * counters; candidate bucket and rank bitmaps; the rank map */
 __host__ __device__ constexpr size_t tf_lkey(int tb) { return 8 * (size_t)tb; }
 __host__ __device__ constexpr size_t tf_lval(int tb) { return tf_lkey(tb) + 8 * TF_CAP; }
-__host__ __device__ constexpr size_t tf_misc(int tb) { return tf_lval(tb) + 8 * TF_CAP; }
+__host__ __device__ constexpr size_t tf_rr(int tb) { return tf_lval(tb) + 8 * TF_CAP; }
+__host__ __device__ constexpr size_t tf_ru(int tb) { return tf_rr(tb) + 4 * TF_CAP; }
+__host__ __device__ constexpr size_t tf_misc(int tb) { return tf_ru(tb) + 4 * TF_CAP; }
 __host__ __device__ constexpr size_t tf_cbits(int tb) { return tf_misc(tb) + 64; }
 __host__ __device__ constexpr size_t tf_rbits(int tb, int nbk) { return tf_cbits(tb) + 4 * (size_t)(nbk / 32 + 4); }
 __host__ __device__ constexpr size_t tf_map(int tb, int nbk, int V) {
@@ -300,55 +304,163 @@ __host__ __device__ constexpr size_t tf_bytes(int tb, int nbk, int V) {
   return tf_map(tb, nbk, V) + 2 * (size_t)((V + 7) & ~7);
 }
 
-/* 3' before the row is read: the bucket counts, group sums, map and bitmaps
- * cleared (phase 1's barriers order this before the counting) */
-template <int TBLOCK, int NBK>
-__device__ __forceinline__ void topp_fast_clear(int V, uint32_t *bstart, char *dyn) {
-  const int tid = (int)threadIdx.x;
-#pragma unroll
-  for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
-  if (tid == 0) bstart[NBK] = 0u;
-  if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = 0u;
-  ((uint64_t *)dyn)[tid] = 0ull;
-  uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
-  uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
-  uint32_t *rmap = (uint32_t *)(dyn + tf_map(TBLOCK, NBK, V));
-  for (int w = tid; w < ((V + 7) & ~7) / 2; w += TBLOCK) rmap[w] = 0u;
-  for (int w = tid; w < NBK / 32 + 4; w += TBLOCK) cbits[w] = 0u;
-  for (int w = tid; w < 4 * ((V + 127) / 128); w += TBLOCK) rbits[w] = 0u;
+/* uint64 -> fp32 within a relative 2^-22 (two conversions and a sum) */
+__device__ __forceinline__ float u64_to_f32_near(uint64_t v) {
+  return __builtin_fmaf((float)(uint32_t)(v >> 32), 0x1p32f, (float)(uint32_t)v);
+}
+/* floor(v) for 0 <= v < 2^56 (v's bits split exactly at 2^32) */
+__device__ __forceinline__ uint64_t f32_to_u64_small(float v) {
+  const uint32_t hi = (uint32_t)(v * 0x1p-32f);
+  const uint32_t lo = (uint32_t)(v - (float)hi * 0x1p32f);
+  return ((uint64_t)hi << 32) | lo;
 }
 
-/* the bucket of x (x <= m; NBK for -inf) */
+/* topp_cut_bands with cheaper conversions: every conversion within 2^-22
+ * (inside the extra 2^-20), the log's ulp rounded up to a power of two at
+ * least 2^-126, and the band ends capped at 2^56 (wider bands: safe) */
+__device__ __forceinline__ CutBands topp_cut_bands_lean(uint64_t Tq, uint64_t S, float lse, float lnS, float xmin,
+                                                        int k) {
+  const float Sf = u64_to_f32_near(S) * 0x1p-40f;
+  const float zf = lse - xmin;
+  const float z = zf < 30.0f ? zf : 30.0f;
+  const float et = 0x1p-24f * 1.01f * 2.0f * z + 0x1p-22f;
+  const float ulp_ln = lnS >= 0x1p-103f ? d3s_u2f((d3s_f2u(lnS) & 0x7f800000u) - (23u << 23)) : 0x1p-126f;
+  const float eg = 0x1p-24f * 1.01f * (fabsf(lse) + 1.0f) + 1.01f * ulp_ln;
+  const float ep = (et * 1.0001f + 1.01f * eg) * (1.0f + 1.01f * eg);
+  const float slack = ep * (float)k / Sf + (float)k;
+  const float Tqf = u64_to_f32_near(Tq);
+  const float dd = (Tqf + slack) * Sf * (1.0f + 1.13f * ep + 0x1p-20f);
+  const float dk = (Tqf - slack) * Sf * (1.0f - ep - 0x1p-20f);
+  const bool wide = !(ep < 0x1p-4f);
+  CutBands c;
+  c.tdrop = wide || !(dd < 0x1p56f) ? ~0ull : f32_to_u64_small(dd) + 2ull;
+  c.tkeep = wide || !(dk > 2.0f) ? 0ull : (dk < 0x1p56f ? f32_to_u64_small(dk) - 1ull : (1ull << 56));
+  return c;
+}
+
+/* Bounds on e = expf(x - m) over bucket b's elements (b < NBK finite; the
+ * -inf bucket's e is 0).  Elements of bucket b < NBK - 1 have t =
+ * RN(RN(m - x) scale) in [b, b + 1), so x's distance d' = RN(m - x) lies in
+ * [b (1 - 2^-24), (b + 1) (1 + 2^-24)] / scale (the last finite bucket: up to
+ * dmax = RN(m - xmin)); z_lo and z_hi below lie outside that with the
+ * roundings of rs = RN(1 / scale) and of the products.  e = expf(-d') is
+ * within an ulp; the hardware 2^(-z log2 e) is within 2^-21 and the
+ * exponent's rounding within 2^-16 for z <= 104 (beyond, e is 0 or
+ * subnormal): all inside the 2^-12 margins; e_hi is at least 2^-126 (above
+ * every subnormal), e_lo 0 far out. */
 template <int NBK>
-__device__ __forceinline__ int topp_bucket(float x, float m, float scale) {
-  return x != -__builtin_inff() ? min((int)((m - x) * scale), NBK - 1) : NBK;
+__device__ __forceinline__ void topp_ebounds(int b, float rs, float dmax, float &elo, float &ehi) {
+  elo = 0.0f;
+  ehi = 0.0f;
+  if (b < NBK) {
+    const float zlo = (float)b * rs * (1.0f - 0x1p-18f);
+    const float zhi = (b < NBK - 1 ? (float)(b + 1) * rs : dmax) * (1.0f + 0x1p-18f);
+    ehi = fmaxf(__builtin_amdgcn_exp2f(-zlo * 1.44269504f) * (1.0f + 0x1p-12f), 0x1p-126f);
+    elo = zhi < 87.0f ? __builtin_amdgcn_exp2f(-zhi * 1.44269504f) * (1.0f - 0x1p-12f) : 0.0f;
+  }
 }
 
-/* 3'-5' once the counts and group sums are in (bk: each element's bucket) */
+/* Score bounds in units of inv from bounds on e, as phase 5's for exact p:
+ * p = RN(e inv) lies in [e_lo inv (1 - 2^-24), e_hi inv (1 + 2^-24)], inside
+ * the extra 2^-20 margins.  lb: -1 when u gives no bound (every score is at
+ * least -1); h: +inf likewise, 0 for u >= 1 (noise +inf or NaN: score 0 or
+ * -1). */
+__device__ __forceinline__ void topp_sbounds(float elo, float ehi, float uu, float &lb, float &h) {
+  lb = -1.0f;
+  h = __builtin_inff();
+  if (uu >= 0x1p-24f && uu < 1.0f) {
+    lb = elo * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * ((1.0f - 0x1p-18f) * (1.0f - 0x1p-20f));
+    if (uu > 0x1p-24f) h = ehi * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * ((1.0f + 0x1p-18f) * (1.0f + 0x1p-20f));
+  } else if (uu >= 1.0f) {
+    h = 0.0f;
+  }
+}
+
+/* exclusive scans, in thread order, of a count and a fixed-point sum (below
+ * 2^56 in total), and their totals, in one round */
+__device__ __forceinline__ void block_excl_scan2(uint32_t c, uint64_t v, TRed &R, uint32_t &cx, uint32_t &ctot,
+                                                 uint64_t &vx, uint64_t &vtot) {
+  const int lane = lane_id(), wid = threadIdx.x / WAVE;
+  const uint32_t ic = wave_scan_add_u32(c);
+  const uint32_t lo = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t hi = wave_scan_add_u32((uint32_t)(v >> 24));
+  const uint64_t iv = ((uint64_t)hi << 24) + lo;
+  __syncthreads();
+  if (lane == WAVE - 1) {
+    R.a[wid] = ic;
+    R.s[wid] = iv;
+  }
+  __syncthreads();
+  const uint32_t xc = R.a[lane & 15];
+  const uint64_t xv = R.s[lane & 15];
+  ctot = uni_u32(row16_sum_u32(xc));
+  vtot = uni_u64(row16_sum_u64(xv));
+  cx = row16_sum_u32((lane & 15) < wid ? xc : 0u) + ic - c;
+  vx = row16_sum_u64((lane & 15) < wid ? xv : 0ull) + iv - v;
+}
+
+/* a wave's append of popc(mask) items per lane with one atomic: this lane's
+ * first slot (every lane of the wave calls it) */
+__device__ __forceinline__ int wave_append_mask(uint32_t mask, int *counter) {
+  const uint32_t cnt = (uint32_t)__popc(mask);
+  const uint32_t incl = wave_scan_add_u32(cnt);
+  const uint32_t total = readlane_u(incl, WAVE - 1);
+  int base = 0;
+  if (total != 0u) {
+    if (lane_id() == WAVE - 1) base = atomicAdd(counter, (int)total);
+    base = (int)readlane_u((uint32_t)base, WAVE - 1);
+  }
+  return base + (int)(incl - cnt);
+}
+
+/* x's bucket: t = RN(m - x) scale, t <= RN(dmax scale) < NBK for finite x,
+ * +inf for -inf (bucket NBK) */
+template <int NBK>
+__device__ __forceinline__ int topp_bucket_of(float x, float m, float scale) {
+  return (int)fminf((m - x) * scale, (float)NBK);
+}
+
+/* the largest bucket b with start(b) <= r (bucket of rank r < V) */
+template <int NBK>
+__device__ __forceinline__ int topp_bucket_of_rank(const uint32_t *bstart, int r) {
+  int lo = 0, hi = NBK + 1;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (bstart[mid] <= (uint32_t)r)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+/* 4'-5' once the bucket counts and group sums are in LDS.  Returns the id or
+ * TOPP_FULL; every thread calls it and every return follows a barrier. */
 template <int EPT, int TBLOCK, int NBK>
-__device__ __forceinline__ int topp_fast(const SampleArgs &a, int row, const float (&x)[EPT], const int (&bk)[EPT],
-                                         float m, float xmin, float scale, uint64_t S, float lse, float lnS,
-                                         float top_p, uint32_t *bstart, char *dyn, TRed &R) {
+__device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const float (&x)[EPT],
+                                             const float (&uv)[EPT], float m, float xmin, float scale, float top_p,
+                                             uint32_t *bstart, char *dyn, TRed &R) {
   constexpr int PER = NBK / TBLOCK;
   static_assert(PER % 4 == 0, "whole 16-byte groups of buckets per thread");
   const int V = a.vocab, k = a.k;
   const int tid = (int)threadIdx.x, lane = lane_id();
   uint64_t *gsum = (uint64_t *)dyn;
   uint64_t *lkey = (uint64_t *)(dyn + tf_lkey(TBLOCK));
-  uint64_t *lval = (uint64_t *)(dyn + tf_lval(TBLOCK));
-  uint32_t *misc = (uint32_t *)(dyn + tf_misc(TBLOCK)); /* [0] list count, [1] cut, [2] id */
-  uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32); /* [0] a group's start, [1] Q at cut - 1 */
+  uint64_t *lval = (uint64_t *)(dyn + tf_lval(TBLOCK)); /* bucket */
+  int *rr = (int *)(dyn + tf_rr(TBLOCK));
+  float *ru = (float *)(dyn + tf_ru(TBLOCK));
+  /* [0] elements, [1] flag, [2] id, [3] refined ranks, [4] the cut group */
+  uint32_t *misc = (uint32_t *)(dyn + tf_misc(TBLOCK));
+  uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32); /* [0] the cut group's prefix, [1] P before it */
   uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
   uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
-  uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V));
-
-  /* this thread's ranks, for the race */
+  uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V)); /* bucket + 1 at each bucket's first rank */
   const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
   const int r0 = tid * RPT;
 
+  /* ---- bucket starts, group prefixes and the row sum S, one scan */
+  uint64_t gst, gs, S;
   {
-    /* bucket starts (exclusive scan, as phase 3); each non-empty bucket's id
-     * at its first rank in the map */
     uint4 c[PER / 4];
     uint32_t loc = 0u;
 #pragma unroll
@@ -356,8 +468,9 @@ __device__ __forceinline__ int topp_fast(const SampleArgs &a, int row, const flo
       c[q] = *(const uint4 *)&bstart[tid * PER + 4 * q];
       loc += c[q].x + c[q].y + c[q].z + c[q].w;
     }
-    uint32_t tot;
-    uint32_t run = block_excl_scan_u32(loc, R, tot);
+    gs = gsum[tid];
+    uint32_t run, tot;
+    block_excl_scan2(loc, gs, R, run, tot, gst, S);
 #pragma unroll
     for (int q = 0; q < PER / 4; q++) {
       const uint32_t cc[4] = {c[q].x, c[q].y, c[q].z, c[q].w};
@@ -365,198 +478,248 @@ __device__ __forceinline__ int topp_fast(const SampleArgs &a, int row, const flo
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         st[e] = run;
-        if (cc[e] != 0u) rmap[run] = (uint16_t)(tid * PER + 4 * q + e);
+        if (cc[e] != 0u) rmap[run] = (uint16_t)(tid * PER + 4 * q + e + 1);
         run += cc[e];
       }
       *(uint4 *)&bstart[tid * PER + 4 * q] = make_uint4(st[0], st[1], st[2], st[3]);
     }
     if (tid == 0) {
       bstart[NBK] = tot;
-      if (tot < (uint32_t)V) rmap[tot] = (uint16_t)NBK;
+      if (tot < (uint32_t)V) rmap[tot] = (uint16_t)(NBK + 1);
     }
   }
-  /* each group's prefix at its start (the scan's barriers also publish the
-   * starts and the map) */
-  const uint64_t gs = gsum[tid];
-  const uint64_t gst = block_excl_scan_u64(gs, R);
+  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
+  const float lse = m + lnS;
 
-  /* ---- 4'. the cut, and Q at the rank before it (the kept sum) */
+  /* ---- 4'. the cut's range [klo, khi]: the group whose prefix crosses the
+   * certain drop band (one thread's: the prefixes only grow) */
   const uint64_t Tq = d3s_fixsum_gt_threshold(top_p);
-  int cut;
-  uint64_t qlast;
-  if (Tq == 0ull) {
-    cut = 1; /* rank 0's term: e_0 = 1 */
-    qlast = 1ull << 40;
-  } else if (Tq > ((uint64_t)k << 41)) {
-    cut = k;
-    qlast = S;
+  const bool settled1 = Tq == 0ull;                     /* every prefix passes: cut 1 */
+  const bool settledk = Tq > ((uint64_t)k << 41);      /* none reaches it: cut k */
+  uint64_t tdrop = ~0ull, tkeep = 0ull;
+  if (!settled1 && !settledk) {
+    const CutBands cb = topp_cut_bands_lean(Tq, S, lse, lnS, xmin, k);
+    tdrop = cb.tdrop;
+    tkeep = cb.tkeep;
+    if (gst < tdrop && tdrop <= gst + gs) {
+      misc[4] = (uint32_t)tid;
+      misc64[0] = gst;
+    }
+  }
+  __syncthreads(); /* the starts, the map, the cut group */
+  const int g = settled1 || settledk ? -1 : (int)misc[4]; /* -1: no group (cleared to ~0) */
+  uint32_t s0 = 0u;
+  int klo, khi;
+  if (settled1) {
+    klo = khi = 1;
+  } else if (g < 0) {
+    klo = khi = k; /* no rank certainly drops (when not settled: the last must certainly stay) */
   } else {
-    const CutBands cb = topp_cut_bands(Tq, S, lse, lnS, xmin, k);
-    const int g = block_min_i32(gst + gs >= cb.tdrop ? tid : 0x7fffffff, R);
-    if (g == 0x7fffffff) {
-      cut = k; /* no rank certainly drops: the last must certainly stay */
-      qlast = S;
-    } else {
-      const uint32_t s0 = bstart[g * PER], n = bstart[g * PER + PER] - s0;
-      if (n > (uint32_t)TF_CAP) {
-        __syncthreads();
-        return TOPP_FULL;
-      }
-      if (tid == g) misc64[0] = gst;
-#pragma unroll
-      for (int j = 0; j < EPT; j++) {
-        const int i = j * TBLOCK + tid;
-        const bool in = i < V && bk[j] / PER == g; /* (the -inf bucket's is no group) */
-        const int slot = wave_append(in, (int *)&misc[0]);
-        if (in) lkey[slot] = composite_key(x[j], i);
-      }
-      __syncthreads();
-      if (tid < WAVE) {
-        /* lane t: element t of the group, its term fix40(e), rank and
-         * inclusive prefix */
-        const uint64_t q0 = misc64[0];
-        const bool mine = lane < (int)n;
-        const uint64_t mk = mine ? lkey[lane] : 0ull;
-        if (mine) lval[lane] = d3s_fix40_unit(d3s_expf_nonpos(key_x(mk) - m));
-        wave_lds_sync();
-        int rho = 0;
-        uint64_t inc = 0ull;
-        for (int t = 0; t < (int)n; t++) {
-          const uint64_t kk = lkey[t], vv = lval[t];
-          rho += kk > mk ? 1 : 0;
-          inc += kk >= mk ? vv : 0ull;
-        }
-        const int r = (int)s0 + rho;
-        const uint64_t qr = q0 + inc;
-        /* the first rank reaching the band (the group's last does); rank 0
-         * never drops */
-        const int r1 = wave_min_i32(mine && qr >= cb.tdrop ? r : 0x7fffffff);
-        const int c2 = min(max(r1, 1), k);
-        uint64_t ql = q0; /* c2 - 1 = s0 - 1: the prefix before the group */
-        if (c2 - 1 >= (int)s0) {
-          const uint64_t at = __ballot(mine && r == c2 - 1);
-          const int src = (int)__builtin_ctzll(at | (1ull << 63));
-          ql = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
-        }
-        if (lane == 0) {
-          misc[1] = (uint32_t)c2;
-          misc64[1] = ql;
-          misc[0] = 0u; /* the list is free again */
-        }
-      }
-      __syncthreads();
-      cut = (int)misc[1];
-      qlast = misc64[1];
-    }
-    if (cut > 1 && !(qlast < cb.tkeep)) {
-      __syncthreads();
-      return TOPP_FULL;
-    }
+    s0 = bstart[g * PER];
+    const uint32_t n = bstart[g * PER + PER] - s0;
+    if (n > (uint32_t)TF_CAP) return TOPP_FULL; /* (after the barrier above) */
+    klo = max((int)s0, 1); /* cut = max(r1, 1), r1 the group's first rank reaching tdrop */
+    khi = max((int)(s0 + n) - 1, 1);
   }
-  const float inv = 1.0f / d3s_fixsum_to_f32(qlast);
 
-  /* ---- 5'. score bounds per kept rank from its bucket: elements of finite
-   * bucket b < NBK - 1 have t = RN(RN(m - x) scale) in [b, b + 1), so
-   * RN(m - x) = x's distance d' lies in [b (1 - 2^-24), (b + 1) (1 + 2^-24)]
-   * / scale (the last finite bucket: up to RN(m - xmin)); z_lo and z_hi below
-   * are outside that with the roundings of 1 / scale and the products.  e =
-   * expf(-d') within an ulp; the hardware 2^(-z log2 e) is within 2^-21 and
-   * the product's rounding within 2^-16 for z <= 104 (below that e is 0 or
-   * subnormal), all inside the 2^-12 margins; e_hi is at least 2^-126 (above
-   * every subnormal), e_lo 0 far out.  p = RN(e inv) is monotone in e. */
-  /* the kept ranks' uniforms (the dropped ranks' are not read) */
-  float uv[EPT];
-#pragma unroll
-  for (int q = 0; q < EPT; q++) uv[q] = (q < RPT && r0 + q < cut) ? a.u[(size_t)row * k + r0 + q] : 0.0f;
-  int b = 0;
-  if (r0 < cut) {
-    int lo = 0, hi = NBK + 1; /* the largest b with start(b) <= r0 */
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (bstart[mid] <= (uint32_t)r0)
-        lo = mid;
-      else
-        hi = mid;
-    }
-    b = lo;
-  }
+  /* ---- 5'. first bounds, in units of inv: e <= 1 on every rank that may
+   * be kept (r < khi); e >= emin on those certainly kept (r < klo) */
   const float rs = 1.0f / scale, dmax = m - xmin;
-  const int bfirst = b;
-  float hb[EPT];
+  float emin = 1.0f; /* klo = 1: rank 0 alone, e_0 = 1 */
+  if (klo > 1) {
+    float eh;
+    if (g >= 0)
+      topp_ebounds<NBK>(g * PER - 1, rs, dmax, emin, eh); /* the ranks before the group */
+    else
+      topp_ebounds<NBK>(bstart[NBK] < (uint32_t)V ? NBK : NBK - 1, rs, dmax, emin, eh); /* every rank */
+  }
+  float hb0[EPT];
   float lbm = -1.0f;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
     const int r = r0 + q;
-    hb[q] = -__builtin_inff();
-    if (q < RPT && r < cut) {
-      if (q > 0) b = max(b, (int)rmap[r]);
-      float elo = 0.0f, ehi = 0.0f; /* the -inf bucket: e = 0 */
-      if (b < NBK) {
-        const float zlo = (float)b * rs * (1.0f - 0x1p-18f);
-        const float zhi = (b < NBK - 1 ? (float)(b + 1) * rs : dmax) * (1.0f + 0x1p-18f);
-        ehi = fmaxf(__builtin_amdgcn_exp2f(-zlo * 1.44269504f) * (1.0f + 0x1p-12f), 0x1p-126f);
-        elo = zhi < 87.0f ? __builtin_amdgcn_exp2f(-zhi * 1.44269504f) * (1.0f - 0x1p-12f) : 0.0f;
-      }
-      const float plo = elo * inv, phi = ehi * inv;
-      const float uu = uv[q];
-      /* the full path's bounds (phase 5) at p_lo and p_hi */
-      float lb = -1.0f, h = __builtin_inff();
-      if (uu >= 0x1p-24f && uu < 1.0f) {
-        lb = plo * __builtin_amdgcn_rcpf(uu * __builtin_amdgcn_rcpf(1.0f - uu) + 0x1p-22f) * (1.0f - 0x1p-18f);
-        if (uu > 0x1p-24f) h = phi * __builtin_amdgcn_rcpf(uu - 0x1p-24f) * (1.0f + 0x1p-18f);
-      } else if (uu >= 1.0f) {
-        h = 0.0f;
-      }
-      hb[q] = h;
-      lbm = fmaxf(lbm, lb);
+    hb0[q] = -__builtin_inff();
+    if (q < RPT && r < khi) {
+      float lb, h;
+      topp_sbounds(emin, 1.0f, uv[q], lb, h);
+      hb0[q] = h;
+      if (r < klo) lbm = fmaxf(lbm, lb);
     }
   }
-  const float LB = block_max_f(lbm, R);
-  b = bfirst;
+  const float LB1 = block_max_f(lbm, R);
+  /* the ranks whose first upper bound reaches LB1, to one wave */
+  {
+    uint32_t pm = 0u;
 #pragma unroll
-  for (int q = 0; q < EPT; q++) {
-    const int r = r0 + q;
-    if (q > 0 && q < RPT && r < cut) b = max(b, (int)rmap[r]);
-    if (hb[q] >= LB) { /* only kept ranks: the others hold -inf */
-      atomicOr(&rbits[r >> 5], 1u << (r & 31));
+    for (int q = 0; q < EPT; q++) pm |= (hb0[q] >= LB1 ? 1u : 0u) << q;
+    int slot = wave_append_mask(pm, (int *)&misc[3]);
+#pragma unroll
+    for (int q = 0; q < EPT; q++)
+      if ((pm >> q) & 1u) {
+        if (slot < TF_CAP) {
+          rr[slot] = r0 + q;
+          ru[slot] = uv[q];
+        }
+        slot++;
+      }
+  }
+  __syncthreads();
+  const uint32_t nref = misc[3];
+  if (nref > (uint32_t)TF_CAP) return TOPP_FULL; /* (after the barrier above) */
+  /* wave 0 keeps the refined ranks in registers (lane t: rank t) */
+  int my_rr = 0;
+  float my_ru = 0.0f;
+  if (tid < WAVE) {
+    /* their buckets' bounds; LB2 and the candidates */
+    const bool mine = lane < (int)nref;
+    my_rr = mine ? rr[lane] : 0x7fffffff;
+    my_ru = mine ? ru[lane] : 0.0f;
+    int b = 0;
+    if (mine) {
+      /* the bucket holding rank r: the nearest first rank at or below it */
+      int p = my_rr, v = (int)rmap[p];
+      while (v == 0) v = (int)rmap[--p]; /* (rmap[0] = 1: bucket 0 holds rank 0) */
+      b = v - 1;
+    }
+    float lb = -1.0f, h = -__builtin_inff();
+    if (mine) {
+      float elo, ehi, l2;
+      topp_ebounds<NBK>(b, rs, dmax, elo, ehi);
+      topp_sbounds(elo, ehi, my_ru, l2, h);
+      if (my_rr < klo) lb = l2;
+    }
+    const float LB2 = fmaxf(LB1, wave_max_f(lb));
+    if (mine && h >= LB2) {
+      atomicOr(&rbits[my_rr >> 5], 1u << (my_rr & 31));
       atomicOr(&cbits[b >> 5], 1u << (b & 31));
     }
   }
   __syncthreads();
-  /* the elements of the candidates' buckets */
+  /* ---- one gather: the cut group's elements and the candidates' buckets' */
+  {
+    uint32_t gm = 0u;
 #pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int i = j * TBLOCK + tid;
-    const int bb = bk[j];
-    const bool in = i < V && ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u;
-    const int slot = wave_append(in, (int *)&misc[0]);
-    if (in && slot < TF_CAP) {
-      lkey[slot] = composite_key(x[j], i);
-      lval[slot] = (uint64_t)bb;
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const int bb = topp_bucket_of<NBK>(x[j], m, scale);
+      const bool in = i < V && ((uint32_t)bb / PER == (uint32_t)g || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
+      gm |= (in ? 1u : 0u) << j;
     }
+    int slot = wave_append_mask(gm, (int *)&misc[0]);
+#pragma unroll
+    for (int j = 0; j < EPT; j++)
+      if ((gm >> j) & 1u) {
+        if (slot < TF_CAP) {
+          lkey[slot] = composite_key(x[j], j * TBLOCK + tid);
+          lval[slot] = (uint64_t)(uint32_t)topp_bucket_of<NBK>(x[j], m, scale);
+        }
+        slot++;
+      }
   }
   __syncthreads();
   const uint32_t n2 = misc[0];
   if (n2 > (uint32_t)TF_CAP) return TOPP_FULL; /* (after the barrier above) */
+  /* ---- wave 0: rank the gathered elements; the cut from the group's
+   * prefixes (lane t: element t; the others' keys by readlane) */
+  bool mine = false, ing = false;
+  uint64_t mk = 0ull, qr = 0ull;
+  int r = 0x7fffffff, cut = 0;
+  uint64_t qlast = 0ull;
   if (tid < WAVE) {
-    const bool mine = lane < (int)n2;
-    const uint64_t mk = mine ? lkey[lane] : 0ull;
-    const uint64_t mb = mine ? lval[lane] : ~0ull;
+    mine = lane < (int)n2;
+    mk = mine ? lkey[lane] : 0ull;
+    const uint32_t mb = mine ? (uint32_t)lval[lane] : 0xffffffffu;
+    ing = mine && mb / PER == (uint32_t)g;
+    const uint64_t f = ing ? d3s_fix40_exp(key_x(mk) - m) : 0ull;
     int rho = 0;
-    for (int t = 0; t < (int)n2; t++) rho += (lval[t] == mb && lkey[t] > mk) ? 1 : 0;
+    uint64_t inc = 0ull;
+    for (int t = 0; t < (int)n2; t++) {
+      const uint64_t kt = ((uint64_t)readlane_u((uint32_t)(mk >> 32), t) << 32) | readlane_u((uint32_t)mk, t);
+      const uint32_t bt = readlane_u(mb, t);
+      const uint64_t ft = ((uint64_t)readlane_u((uint32_t)(f >> 32), t) << 32) | readlane_u((uint32_t)f, t);
+      rho += (bt == mb && kt > mk) ? 1 : 0;
+      inc += kt >= mk ? ft : 0ull; /* (0 outside the group) */
+    }
+    r = mine ? (int)bstart[mb] + rho : 0x7fffffff;
+    bool certain;
+    if (g >= 0) {
+      const uint64_t q0 = misc64[0];
+      qr = q0 + inc;
+      /* the first rank reaching tdrop (the group's last does); rank 0 never drops */
+      const int r1 = wave_min_i32(ing && qr >= tdrop ? r : 0x7fffffff);
+      cut = min(max(r1, 1), k);
+      qlast = q0; /* cut - 1 = s0 - 1: the prefix before the group */
+      if (cut - 1 >= (int)s0) {
+        const uint64_t at = __ballot(ing && r == cut - 1);
+        const int src = (int)__builtin_ctzll(at | (1ull << 63));
+        qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
+      }
+      certain = cut <= 1 || qlast < tkeep;
+    } else {
+      cut = klo;
+      qlast = cut == 1 ? (1ull << 40) : S; /* rank 0's term, or every term */
+      certain = cut <= 1 || settledk || qlast < tkeep;
+    }
+    if (lane == 0) misc[1] = certain ? 0u : (g >= 0 ? 1u : 2u);
+  }
+  __syncthreads();
+  const uint32_t how = misc[1];
+  if (how == 2u) return TOPP_FULL; /* an uncertain last rank: the full path */
+  if (how == 1u) {
+    /* the cut within the bands' uncertainty: the exact prefix P before the
+     * group (block sum of fix40(expf(x - lse)) over the elements of the
+     * buckets before it), then the group's exact prefixes */
+    uint64_t part = 0ull;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const int bb = topp_bucket_of<NBK>(x[j], m, scale);
+      if (i < V && bb < g * PER) part += d3s_fix40_exp(x[j] - lse);
+    }
+    const uint64_t p0 = block_sum_u64(part, R);
+    if (tid < WAVE) {
+      const uint64_t pt = ing ? d3s_fix40_exp(key_x(mk) - lse) : 0ull;
+      uint64_t pinc = 0ull;
+      for (int t = 0; t < (int)n2; t++) {
+        const uint64_t kt = ((uint64_t)readlane_u((uint32_t)(mk >> 32), t) << 32) | readlane_u((uint32_t)mk, t);
+        const uint64_t ftt = ((uint64_t)readlane_u((uint32_t)(pt >> 32), t) << 32) | readlane_u((uint32_t)pt, t);
+        pinc += kt >= mk ? ftt : 0ull;
+      }
+      /* the first rank whose exact prefix reaches Tq; before the group when
+       * p0 does already (then the full path) */
+      const int re = wave_min_i32(ing && p0 + pinc >= Tq ? r : 0x7fffffff);
+      cut = min(max(re, 1), k);
+      qlast = misc64[0];
+      if (cut - 1 >= (int)s0) {
+        const uint64_t at = __ballot(ing && r == cut - 1);
+        const int src = (int)__builtin_ctzll(at | (1ull << 63));
+        qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
+      }
+      if (lane == 0 && (p0 >= Tq || re == 0x7fffffff)) misc[2] = (uint32_t)TOPP_FULL;
+    }
+    __syncthreads();
+    if (misc[2] == (uint32_t)TOPP_FULL) return TOPP_FULL; /* (after the barrier above) */
+  }
+  /* ---- the candidates' exact scores and their first maximum */
+  if (tid < WAVE) {
     float bs = -2.0f;
     int br = 0x7fffffff;
-    if (mine) {
-      const int r = (int)bstart[(int)mb] + rho;
-      if (r < cut && ((rbits[r >> 5] >> (r & 31)) & 1u) != 0u) {
-        const float e = d3s_expf_nonpos(key_x(mk) - m);
-        bs = topp_score(e * inv, a.u[(size_t)row * k + r]);
-        br = r;
-      }
+    const float inv = 1.0f / d3s_fixsum_to_f32(qlast);
+    const bool cand = mine && r < cut && ((rbits[r >> 5] >> (r & 31)) & 1u) != 0u;
+    /* (every candidate is a refined rank: its uniform is in wave 0's lanes) */
+    float uu = 0.0f;
+    for (int t = 0; t < (int)nref; t++) {
+      const int rt = (int)readlane_u((uint32_t)my_rr, t);
+      const float ut = d3s_u2f(readlane_u(d3s_f2u(my_ru), t));
+      uu = rt == r ? ut : uu;
+    }
+    if (cand) {
+      bs = topp_score(d3s_expf_nonpos(key_x(mk) - m) * inv, uu);
+      br = r;
     }
     const int myr = br;
     wave_argmax(bs, br);
-    const uint64_t at = __ballot(mine && myr == br);
+    const uint64_t at = __ballot(cand && myr == br);
     const int src = (int)__builtin_ctzll(at | (1ull << 63));
     const int id = key_idx(((uint64_t)readlane_u((uint32_t)(mk >> 32), src) << 32) | readlane_u((uint32_t)mk, src));
     if (lane == 0) misc[2] = bs > 0.0f ? (uint32_t)id : (uint32_t)TOPP_FULL;
@@ -565,115 +728,18 @@ __device__ __forceinline__ int topp_fast(const SampleArgs &a, int row, const flo
   return (int)misc[2];
 }
 
-template <int EPT, bool BF16, int TBLOCK, bool FAST>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
-    SampleArgs a) {
+/* Phases 3-5 (the full path) from x and e = expf(x - m). */
+template <int EPT, bool BF16, int TBLOCK>
+__device__ __forceinline__ void topp_full(const SampleArgs &a, int row, const RowP &rp, const char *rowp,
+                                          const float (&x)[EPT], const float (&ev)[EPT], float m, float xmin,
+                                          float scale, uint64_t S, float lnS, float lse, uint32_t *bstart,
+                                          uint64_t *keys, TRed &R) {
   constexpr int NBK = topp_buckets(EPT * TBLOCK, TBLOCK);
-  constexpr int NW = TBLOCK / WAVE;
-  static_assert(NW <= TNW, "one reduction entry per wave");
-  extern __shared__ uint64_t keys[]; /* V slots: by bucket, then by rank */
-  static_assert(NBK % (4 * TBLOCK) == 0, "whole 16-byte groups of buckets per thread");
-  __shared__ __align__(16) uint32_t bstart[NBK + 4]; /* bucket counts, first slots, then ends */
-  __shared__ TRed R;
-
-  const int row = (int)blockIdx.x;
-  const int tid = (int)threadIdx.x;
-  if (NW < TNW && tid >= NW && tid < TNW) {
-    /* the reduction entries of absent waves: identities, never overwritten */
-    R.f[tid] = R.g[tid] = R.h[tid] = -__builtin_inff();
-    R.s[tid] = 0ull;
-    R.a[tid] = 0u;
-    R.r[tid] = 0x7fffffff;
-  }
   const int V = a.vocab, k = a.k;
-  const RowP rp = row_params(a, row);
+  const int tid = (int)threadIdx.x;
   const float T = rp.T;
   const bool t_finite = T < __builtin_inff();
   const float y = 1.0f / T;
-  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
-  if (FAST) topp_fast_clear<TBLOCK, NBK>(V, bstart, (char *)keys);
-
-  /* ---- 1. x, classification, max and smallest finite x */
-  float x[EPT];
-  float xm = -__builtin_inff(), xl = __builtin_inff();
-  /* every load in flight before the first use (past the row's end, the last
-   * element is read again and ignored) */
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int i = j * TBLOCK + tid;
-    x[j] = load_logit<BF16>(rowp, i < V ? i : V - 1, rp.banned);
-  }
-  /* xm: the maximum with NaN propagated, so NaN or +inf anywhere shows in it;
-   * xl: the least x above -inf */
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int i = j * TBLOCK + tid;
-    const float xi = i < V ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
-    x[j] = xi;
-    xm = __builtin_elementwise_maximum(xm, xi);
-    xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
-  }
-  const bool refused = !(xm < __builtin_inff()); /* NaN or +inf */
-  float m = refused ? 0.0f : xm, nxl = -xl, bad = refused ? 1.0f : 0.0f;
-  block_max3_f(m, nxl, bad, R);
-  if (bad > 0.0f) {
-    write_special(a, row, false);
-    return;
-  }
-  if (m == -__builtin_inff()) {
-    write_special(a, row, true);
-    return;
-  }
-  const float xmin = -nxl;
-
-  const float dmax = m - xmin;
-  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
-
-  /* ---- 2. e = exp(x - m) and the exact row sum and lse (x = -inf, and
-   * i >= V, add 0); e is also each element's softmax term (x_0 = m) */
-  float ev[EPT];
-  uint64_t S;
-  float lnS, lse;
-  if (FAST && scale > 0.0f) {
-    /* the ids-only path: each element's term also goes to its bucket's
-     * count and its group's sum, and e is not kept */
-    constexpr int PER = NBK / TBLOCK;
-    int bk[EPT];
-    uint64_t acc = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
-      const uint64_t f = d3s_fix40_unit(d3s_expf_nonpos(x[j] - m));
-      acc += f;
-      const int b = topp_bucket<NBK>(x[j], m, scale);
-      bk[j] = b;
-      if (i < V) {
-        atomicAdd(&bstart[b], 1u);
-        if (b < NBK) atomicAdd((unsigned long long *)&keys[b / PER], (unsigned long long)f);
-      }
-    }
-    S = block_sum_u64(acc, R); /* (its barriers also close the counting) */
-    lnS = d3s_logf(d3s_fixsum_to_f32(S));
-    lse = m + lnS;
-    const int id = topp_fast<EPT, TBLOCK, NBK>(a, row, x, bk, m, xmin, scale, S, lse, lnS, rp.top_p, bstart,
-                                               (char *)keys, R);
-    if (id != TOPP_FULL) {
-      if (tid == 0) a.ids[row] = id;
-      return;
-    }
-#pragma unroll
-    for (int j = 0; j < EPT; j++) ev[j] = d3s_expf_nonpos(x[j] - m);
-  } else {
-    uint64_t acc = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; j++) {
-      ev[j] = d3s_expf_nonpos(x[j] - m); /* in [0, 1] */
-      acc += d3s_fix40_unit(ev[j]);
-    }
-    S = block_sum_u64(acc, R);
-    lnS = d3s_logf(d3s_fixsum_to_f32(S));
-    lse = m + lnS;
-  }
 
   /* ---- 3. ranks: counting sort over buckets of m - x, exact within buckets */
 #pragma unroll
@@ -936,19 +1002,217 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   }
 }
 
+/* the block's shared arrays and the reduction entries of absent waves */
+#define D3S_TOPP_SHARED                                                                         \
+  constexpr int NBK = topp_buckets(EPT * TBLOCK, TBLOCK);                                       \
+  constexpr int NW = TBLOCK / WAVE;                                                             \
+  static_assert(NW <= TNW, "one reduction entry per wave");                                     \
+  extern __shared__ uint64_t keys[]; /* V slots: by bucket, then by rank (or the ids path's) */ \
+  static_assert(NBK % (4 * TBLOCK) == 0, "whole 16-byte groups of buckets per thread");         \
+  __shared__ __align__(16) uint32_t bstart[NBK + 4]; /* bucket counts, first slots, then ends */ \
+  __shared__ TRed R;                                                                            \
+  const int tid = (int)threadIdx.x;                                                             \
+  if (NW < TNW && tid >= NW && tid < TNW) {                                                     \
+    /* the reduction entries of absent waves: identities, never overwritten */                  \
+    R.f[tid] = R.g[tid] = R.h[tid] = -__builtin_inff();                                         \
+    R.s[tid] = 0ull;                                                                            \
+    R.a[tid] = 0u;                                                                              \
+    R.r[tid] = 0x7fffffff;                                                                      \
+  }
+
+/* phase 1's ending: the row's max m (NaN or +inf: refused) and least finite
+ * x; false when the row was written as a special case */
+template <int EPT>
+__device__ __forceinline__ bool topp_max_min(const SampleArgs &a, int row, float xm, float xl, float &m, float &xmin,
+                                             TRed &R) {
+  const bool refused = !(xm < __builtin_inff()); /* NaN or +inf */
+  float nxl = -xl, bad = refused ? 1.0f : 0.0f;
+  m = refused ? 0.0f : xm;
+  block_max3_f(m, nxl, bad, R);
+  if (bad > 0.0f) {
+    write_special(a, row, false);
+    return false;
+  }
+  if (m == -__builtin_inff()) {
+    write_special(a, row, true);
+    return false;
+  }
+  xmin = -nxl;
+  return true;
+}
+
+/* k_topp: every output (ids, probabilities, candidates) by the full path */
+template <int EPT, bool BF16, int TBLOCK>
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
+    SampleArgs a) {
+  D3S_TOPP_SHARED
+  const int row = (int)blockIdx.x;
+  const int V = a.vocab;
+  const RowP rp = row_params(a, row);
+  const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+
+  /* ---- 1. x, classification, max and smallest finite x */
+  float x[EPT];
+  float xm = -__builtin_inff(), xl = __builtin_inff();
+  /* every load in flight before the first use (past the row's end, the last
+   * element is read again and ignored) */
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    x[j] = load_logit<BF16>(rowp, i < V ? i : V - 1, rp.banned);
+  }
+  /* xm: the maximum with NaN propagated, so NaN or +inf anywhere shows in it;
+   * xl: the least x above -inf */
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    const float xi = i < V ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
+    x[j] = xi;
+    xm = __builtin_elementwise_maximum(xm, xi);
+    xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
+  }
+  float m, xmin;
+  if (!topp_max_min<EPT>(a, row, xm, xl, m, xmin, R)) return;
+  const float dmax = m - xmin;
+  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
+
+  /* ---- 2. e = exp(x - m) and the exact row sum and lse (x = -inf, and
+   * i >= V, add 0); e is also each element's softmax term (x_0 = m) */
+  float ev[EPT];
+  uint64_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    ev[j] = d3s_expf_nonpos(x[j] - m); /* in [0, 1] */
+    acc += d3s_fix40_unit(ev[j]);
+  }
+  const uint64_t S = block_sum_u64(acc, R);
+  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
+  const float lse = m + lnS;
+  topp_full<EPT, BF16, TBLOCK>(a, row, rp, rowp, x, ev, m, xmin, scale, S, lnS, lse, bstart, keys, R);
+}
+
+/* k_topp_ids: ids only, k = V; the ids-only path, the full path for the rows
+ * it leaves */
+template <int EPT, bool BF16, int TBLOCK>
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp_ids(
+    SampleArgs a) {
+  D3S_TOPP_SHARED
+  constexpr int PER = NBK / TBLOCK;
+  char *dyn = (char *)keys;
+  const int row = (int)blockIdx.x;
+  const int V = a.vocab;
+  const RowP rp = row_params(a, row);
+  const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  {
+    /* bucket counts, group sums, counters and bitmaps cleared (phase 1's
+     * barriers order this before the counting) */
+#pragma unroll
+    for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < 4) bstart[NBK + tid] = 0u;
+    if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = tid == 4 ? ~0u : 0u;
+    ((uint64_t *)dyn)[tid] = 0ull;
+    uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
+    uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
+    for (int w = tid; w < NBK / 32 + 4; w += TBLOCK) cbits[w] = 0u;
+    for (int w = tid; w < 4 * ((V + 127) / 128); w += TBLOCK) rbits[w] = 0u;
+    uint32_t *rmap = (uint32_t *)(dyn + tf_map(TBLOCK, NBK, V));
+    for (int w = tid; w < ((V + 7) & ~7) / 2; w += TBLOCK) rmap[w] = 0u;
+  }
+
+  /* ---- 1. x (with T = 1, x = L: RN(L / 1) = L), max and least finite x;
+   * the uniforms of this thread's ranks in flight with the row */
+  float x[EPT], uv[EPT];
+  float xm = -__builtin_inff(), xl = __builtin_inff();
+  {
+    const int RPT = (V + TBLOCK - 1) / TBLOCK, r0 = tid * RPT;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const int ii = i < V ? i : V - 1;
+      x[j] = BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[ii]) : ((const float *)rowp)[ii];
+      uv[j] = (j < RPT && r0 + j < V) ? a.u[(size_t)row * V + r0 + j] : 0.0f;
+    }
+  }
+  if (T == 1.0f) {
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const float xi = i < V && i != rp.banned ? x[j] : -__builtin_inff();
+      x[j] = xi;
+      xm = __builtin_elementwise_maximum(xm, xi);
+      xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const float xi = i < V && i != rp.banned ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
+      x[j] = xi;
+      xm = __builtin_elementwise_maximum(xm, xi);
+      xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
+    }
+  }
+  float m, xmin;
+  if (!topp_max_min<EPT>(a, row, xm, xl, m, xmin, R)) return;
+  const float dmax = m - xmin;
+  const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
+
+  /* ---- 2'. each element's bucket count and its group's sum of fix40(e)
+   * (elements past the row count in the spare slot NBK + 1 and add 0 to a
+   * sum past the groups') */
+  if (scale > 0.0f) {
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = j * TBLOCK + tid;
+      const uint64_t f = d3s_fix40_exp(x[j] - m); /* fix40(expf(x - m)), 0 for -inf */
+      const int b = topp_bucket_of<NBK>(x[j], m, scale);
+      atomicAdd(&bstart[i < V ? b : NBK + 1], 1u);
+      atomicAdd((unsigned long long *)&((uint64_t *)dyn)[(uint32_t)b / PER], (unsigned long long)f);
+    }
+    __syncthreads(); /* the counts and sums in (the row sum S is their total) */
+    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, uv, m, xmin, scale, rp.top_p, bstart, dyn, R);
+    if (id != TOPP_FULL) {
+      if (tid == 0) a.ids[row] = id;
+      return;
+    }
+  }
+  /* the full path, the row read again (nothing of the ids path's stays
+   * live into it): x, e and the row sum */
+  float x2[EPT], ev[EPT];
+  uint64_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = j * TBLOCK + tid;
+    x2[j] = i < V ? scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite) : -__builtin_inff();
+    ev[j] = d3s_expf_nonpos(x2[j] - m);
+    acc += d3s_fix40_unit(ev[j]);
+  }
+  const uint64_t S = block_sum_u64(acc, R);
+  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
+  const float lse = m + lnS;
+  topp_full<EPT, BF16, TBLOCK>(a, row, rp, rowp, x2, ev, m, xmin, scale, S, lnS, lse, bstart, keys, R);
+}
+#undef D3S_TOPP_SHARED
+
 template <int EPT, bool BF16, int TBLOCK>
 bool try_topp(const SampleArgs &a, hipStream_t s) {
   if (a.vocab > EPT * TBLOCK) return false;
   /* ids only, k = V (top-k disabled): the ids-only path first */
-  const bool fast = !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
+  const bool ids = !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
   /* the ranked keys, or the ids-only path's arrays */
   const size_t ranked = (size_t)a.vocab * sizeof(uint64_t);
   const size_t arrays = tf_bytes(TBLOCK, topp_buckets(EPT * TBLOCK, TBLOCK), a.vocab);
   const size_t lds = ranked > arrays ? ranked : arrays;
-  if (fast)
-    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK, true>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
+  if (ids)
+    hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
   else
-    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK, false>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
+    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
   return true;
 }
 
