@@ -399,10 +399,12 @@ def ras_latency(reps):
 
 def head_latency(reps):
     """The backbone head (src/backbone.c:1213-1215) and its sample: bf16 hidden
-    [1, 2048] x lm_head [4097, 2048]^T (d3s_linear_bf16), then one draw
-    (d3s_sample).  p50 of events around the two launches, and around one replay
-    of a HIP graph holding both (one weight copy for both, as a graph fixes its
-    pointers).  The gemv alone rotates over 32 weight copies (537 MB, over twice
+    [1, 2048] x lm_head [4097, 2048]^T, then one draw.  p50 of events around
+    one d3s_linear_sample_bf16 launch with D3S_FLAG_ONE_LAUNCH (gemv and sample
+    fused), around the two launches d3s_linear_bf16 + d3s_sample (the entry
+    point's default), and around one replay of a HIP graph holding those two
+    (one weight copy, as a graph fixes its pointers).  Each of the first two,
+    and the gemv alone, also rotating over 32 weight copies (537 MB, over twice
     the Infinity Cache) so each call reads them from HBM."""
     import ctypes
     import d3s
@@ -429,19 +431,37 @@ def head_latency(reps):
         assert L.d3s_linear_bf16(bx.ptr, wp, 1, K, Vh, y.ptr, s.ptr) == 0
         assert d3s.sample_raw(y.ptr, d3s.DTYPE_BF16, 1, Vh, Vh, u.ptr, K_SAMPLE, 0.7, 0.7, None, ids.ptr,
                               stream=s.ptr) == 0
+    def fused(wp):
+        assert L.d3s_linear_sample_bf16(bx.ptr, wp, 1, K, Vh, y.ptr, u.ptr, K_SAMPLE, None, None, 0.7, 0.7,
+                                        ids.ptr, None, None, None, d3s.FLAG_ONE_LAUNCH, s.ptr) == 0
     graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
     hiprt.check(H.hipStreamBeginCapture(s.ptr, 0), "begin capture")
     both(bw.ptr)
     hiprt.check(H.hipStreamEndCapture(s.ptr, ctypes.byref(graph)), "end capture")
     hiprt.check(H.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "instantiate")
     a, b = hiprt.Event(), hiprt.Event()
-    two, replay, gemv = [], [], []
+    two, two_hbm, replay, gemv, one, one_hbm = [], [], [], [], [], []
     for i in range(reps + 20):
         a.record(s)
         both(bw.ptr)
         b.record(s)
         b.synchronize()
         t2 = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        both(bw.ptr + ((i + 7) % copies) * w.nbytes)
+        b.record(s)
+        b.synchronize()
+        t2h = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        fused(bw.ptr)
+        b.record(s)
+        b.synchronize()
+        t1 = a.elapsed_ms(b) * 1e3
+        a.record(s)
+        fused(bw.ptr + (i % copies) * w.nbytes)
+        b.record(s)
+        b.synchronize()
+        t1h = a.elapsed_ms(b) * 1e3
         a.record(s)
         hiprt.check(H.hipGraphLaunch(exe, s.ptr), "graph launch")
         b.record(s)
@@ -453,6 +473,9 @@ def head_latency(reps):
         b.synchronize()
         if i >= 20:
             two.append(t2)
+            two_hbm.append(t2h)
+            one.append(t1)
+            one_hbm.append(t1h)
             replay.append(tg)
             gemv.append(a.elapsed_ms(b) * 1e3)
     H.hipGraphExecDestroy(exe)
@@ -460,9 +483,13 @@ def head_latency(reps):
     s.destroy()
     g = float(np.median(gemv))
     res = {"shape": [[1, K], [Vh, K]], "dtype": "bf16", "k": K_SAMPLE,
-           "two_launches_p50_us": float(np.median(two)), "graph_replay_p50_us": float(np.median(replay)),
+           "fused_p50_us": float(np.median(one)), "fused_hbm_p50_us": float(np.median(one_hbm)),
+           "two_launches_p50_us": float(np.median(two)), "two_launches_hbm_p50_us": float(np.median(two_hbm)),
+           "graph_replay_p50_us": float(np.median(replay)),
            "gemv_p50_us": g, "gemv_weight_GBs": w.nbytes / (g * 1e-6) / 1e9}
-    log(f"head gemv + sample, [1, {K}] x [{Vh}, {K}] bf16: two launches p50 {res['two_launches_p50_us']:.2f} us, "
+    log(f"head gemv + sample, [1, {K}] x [{Vh}, {K}] bf16: one fused launch p50 {res['fused_p50_us']:.2f} us "
+        f"({res['fused_hbm_p50_us']:.2f} us with the weights from HBM), "
+        f"two launches p50 {res['two_launches_p50_us']:.2f} us ({res['two_launches_hbm_p50_us']:.2f} us from HBM), "
         f"one graph replay p50 {res['graph_replay_p50_us']:.2f} us; gemv alone (HBM) {g:.2f} us "
         f"({res['gemv_weight_GBs']:.0f} GB/s of weights)")
     return res

@@ -272,6 +272,73 @@ int d3s_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_
   return launched();
 }
 
+int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
+                           uint16_t *y, const float *u, int k, const float *temperature, const float *top_p,
+                           float temperature_scalar, float top_p_scalar, int32_t *ids, float *probs,
+                           int32_t *cand, uint32_t *counters, unsigned flags, void *stream) {
+  if (n_rows < 0 || n_rows > 65535 || K < 128 || K % 128 != 0 || K > (1 << 20) || V < 1 || V > (1 << 24) ||
+      k < 1 || k > V)
+    return D3S_ERR_ARG;
+  if (k > d3s::generic_max_k()) return D3S_ERR_UNSUPPORTED;
+  if (n_rows == 0) return D3S_OK;
+  if (!x || !w || !u || !ids) return D3S_ERR_ARG;
+  if ((uintptr_t)x % 8u != 0u || (uintptr_t)w % 8u != 0u || (uintptr_t)y % 2u != 0u) return D3S_ERR_ARG;
+  if ((flags & ~(D3S_FLAG_GENERIC | D3S_FLAG_EXACT_LSE | D3S_FLAG_EXACT_SELECT | D3S_FLAG_OP_GRAPH |
+                 D3S_FLAG_ONE_LAUNCH)) != 0u)
+    return D3S_ERR_ARG;
+  const bool one_launch = (flags & D3S_FLAG_ONE_LAUNCH) != 0u;
+  flags &= ~D3S_FLAG_ONE_LAUNCH;
+  d3s::LinearArgs la;
+  la.x = x;
+  la.w = w;
+  la.K = (int)K;
+  la.V = (int)V;
+  la.n_rows = (int)n_rows;
+  la.y = y;
+  d3s::SampleArgs a;
+  a.logits = y;
+  a.row_stride = V;
+  a.vocab = (int)V;
+  a.k = k;
+  a.n_rows = (int)n_rows;
+  a.u = u;
+  a.temperature = temperature;
+  a.top_p = top_p;
+  a.temperature_scalar = temperature_scalar;
+  a.top_p_scalar = top_p_scalar;
+  a.banned = nullptr;
+  a.ids = ids;
+  a.probs = probs;
+  a.cand = cand;
+  a.counters = counters;
+  a.flags = flags;
+  a.opgraph = d3s::op_graph_order(a.vocab, k, (flags & D3S_FLAG_OP_GRAPH) || env_no_fused());
+  hipStream_t s = (hipStream_t)stream;
+  if (one_launch && !(flags & D3S_FLAG_GENERIC) && k <= 64 && V <= d3s::head_max_vocab() &&
+      n_rows <= d3s::head_max_rows()) {
+    const size_t need = d3s::head_workspace_bytes(la);
+    void *ws = d3s::stream_workspace(s, need);
+    if (!ws) return D3S_ERR_NOMEM;
+    if (d3s::launch_head(la, a, ws, need, s)) return launched();
+  }
+  /* the gemv, then the routed sample on its logits (into y, or else the
+   * stream's workspace after the segmented kernel's counters and records) */
+  size_t split_bytes = d3s::split_workspace_bytes(a, d3s::DT_BF16);
+  if (split_bytes < d3s::split_counter_bytes()) split_bytes = d3s::split_counter_bytes();
+  split_bytes = (split_bytes + 255) & ~(size_t)255;
+  const size_t total = split_bytes + (y ? 0 : (size_t)n_rows * (size_t)V * 2);
+  void *ws = d3s::stream_workspace(s, total);
+  if (!ws) return D3S_ERR_NOMEM;
+  if (!y) {
+    la.y = (uint16_t *)((char *)ws + split_bytes);
+    a.logits = la.y;
+  }
+  d3s::launch_linear(la, s);
+  const int rc = launched();
+  if (rc != D3S_OK) return rc;
+  return sample_routed(a, d3s::DT_BF16, s, ws, split_bytes, false);
+}
+
 int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream) {
   if (n < 0 || (n > 0 && !u)) return D3S_ERR_ARG;
   d3s::launch_uniform(u, n, seed, draw, (hipStream_t)stream);

@@ -75,11 +75,12 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 }
 
 /* Row `row` by the whole BLOCK-thread workgroup (BLOCK a multiple of 256);
- * glist: LDS for kpow >= k composite keys (kpow a power of two).  Every thread
- * of the workgroup calls it and returns from it. */
-template <bool BF16, int BLOCK = GBLOCK>
-__device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, const int kpow,
-                                            uint64_t *glist) {
+ * glist: LDS for kpow >= k composite keys (kpow a power of two); src(i): the
+ * row's logit i as fp32, -inf at the banned index.  Every thread of the
+ * workgroup calls it and returns from it. */
+template <int BLOCK, class Src>
+__device__ __forceinline__ void generic_row_src(const SampleArgs &a, const int row, const int kpow,
+                                                uint64_t *glist, Src &&src) {
   constexpr int GBLOCK = BLOCK, GNW = BLOCK / WAVE;
   __shared__ uint32_t hist[NB];
   __shared__ float sh_max[GNW];
@@ -95,8 +96,7 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
   const float T = rp.T;
   const bool t_finite = T < __builtin_inff();
   const float y = 1.0f / T;
-  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
-  auto xat = [&](int i) { return scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite); };
+  auto xat = [&](int i) { return scale_logit(src(i), T, y, t_finite); };
 
   /* ---- pass 1: max and classification */
   float xm = -__builtin_inff();
@@ -299,6 +299,15 @@ __device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, 
       }
     a.ids[row] = key_idx(glist[r]);
   }
+}
+
+/* generic_row_src over row `row` of a.logits */
+template <bool BF16, int BLOCK = GBLOCK>
+__device__ __forceinline__ void generic_row(const SampleArgs &a, const int row, const int kpow,
+                                            uint64_t *glist) {
+  const int banned = row_params(a, row).banned;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  generic_row_src<BLOCK>(a, row, kpow, glist, [&](int i) { return load_logit<BF16>(rowp, i, banned); });
 }
 
 }  // namespace

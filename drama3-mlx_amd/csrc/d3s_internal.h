@@ -99,6 +99,16 @@ void launch_ras_select(const RasArgs &r, const int32_t *first, const int32_t *re
 void *stream_workspace(hipStream_t s, size_t bytes);
 /* Launch the head's gemv. */
 void launch_linear(const LinearArgs &la, hipStream_t s);
+/* Launch the fused head: the gemv's logits and their sample in one launch
+ * (k <= 64, V <= head_max_vocab(), at most head_max_rows() rows).  ws: device memory of
+ * ws_bytes (at least head_workspace_bytes) whose first split_counter_bytes()
+ * are the arrival counters (zero on entry; the kernel leaves them zero).
+ * a: the sample's arguments (vocab = la.V).  Returns false (nothing
+ * launched) when the call does not fit. */
+bool launch_head(const LinearArgs &la, const SampleArgs &a, void *ws, size_t ws_bytes, hipStream_t s);
+int head_max_vocab();
+int head_max_rows();
+size_t head_workspace_bytes(const LinearArgs &la);
 /* out[i] = the hardware 2^in[i] (v_exp_f32) the wave kernel's fast row sum uses */
 void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s);
 /* out[i] = the hardware log2(in[i]) (v_log_f32) the fast row sum's log uses */

@@ -179,6 +179,49 @@ __device__ __forceinline__ int wave_write_special(const SampleArgs &a, int row, 
   return masked ? 0 : -1;
 }
 
+/* relaxed agent-scope stores and loads (global_store / global_load with sc1):
+ * coherent across the XCDs' L2s without a whole-cache write-back */
+__device__ __forceinline__ void st_agent(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* rank the n keys of list (n + 2 entries of room): every key counts the keys
+ * above its own; those below k land in ranked by rank.  Keys are distinct.
+ * G adjacent lanes share a key (G = 4 when n <= NT / 4, 2 when n <=
+ * NT / 2), each counting a share of the list; quad DPP adds the shares.
+ * Called by every thread of an NT-thread workgroup. */
+template <int NT>
+__device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k, uint64_t *ranked) {
+  if (threadIdx.x == 0) {
+    list[n] = 0ull; /* pads below every key */
+    list[n + 1] = 0ull;
+  }
+  __syncthreads();
+  const ulonglong2 *k2 = (const ulonglong2 *)list;
+  const uint32_t lg = n <= NT / 4 ? 2u : n <= NT / 2 ? 1u : 0u; /* log2 G */
+  const uint32_t np = (n + 1) / 2;                                         /* pairs */
+  const uint32_t share = (np + (1u << lg) - 1) >> lg;
+  const uint32_t part = threadIdx.x & ((1u << lg) - 1);
+  const uint32_t p0 = min(np, part * share), p1 = min(np, p0 + share);
+  for (uint32_t base = 0; base < n; base += NT >> lg) {
+    const uint32_t t = base + (threadIdx.x >> lg);
+    const uint64_t my = t < n ? list[t] : ~0ull;
+    uint32_t rank = 0u;
+#pragma unroll 4
+    for (uint32_t j2 = p0; j2 < p1; j2++) {
+      const ulonglong2 q = k2[j2];
+      rank += (q.x > my ? 1u : 0u) + (q.y > my ? 1u : 0u);
+    }
+    if (lg >= 1) rank += dpp_u<0xb1, 0xf>(0u, rank); /* quad_perm [1,0,3,2] */
+    if (lg >= 2) rank += dpp_u<0x4e, 0xf>(0u, rank); /* quad_perm [2,3,0,1] */
+    if (part == 0 && t < n && rank < (uint32_t)k) ranked[rank] = my;
+  }
+  __syncthreads();
+}
+
 /* A row in registers: CPT 16-byte chunks per lane (chunk j * 64 + lane, from
  * the aligned address at or below the row start), 4 words each: fp32 bits or
  * two bf16 halves.  Element i of a lane is chunk row i / EPC, lane-in-chunk

@@ -60,13 +60,6 @@ struct __align__(16) SplitLds {
   uint32_t slo[SPLIT_NW], shi[SPLIT_NW];
 };
 
-__device__ __forceinline__ void st_agent(uint64_t *p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_agent(const uint64_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 /* The exact lse of the row (the oracle's: 2^-40 fixed point of d3s_expf(x -
  * M)), by the whole workgroup streaming the row once. */
 template <bool BF16>
@@ -88,39 +81,6 @@ __device__ __forceinline__ float split_exact_lse(const SampleArgs &a, int row, f
 #pragma unroll
   for (int q = 0; q < SPLIT_NW; q++) tot += ((uint64_t)S.shi[q] << 32) | S.slo[q];
   return M + d3s_logf(d3s_fixsum_to_f32(tot));
-}
-
-/* rank the n keys of list (n + 2 entries of room): every key counts the keys
- * above its own; those below k land in ranked by rank.  Keys are distinct.
- * G adjacent lanes share a key (G = 4 when n <= SPLIT_T / 4, 2 when n <=
- * SPLIT_T / 2), each counting a share of the list; quad DPP adds the shares.
- * Called by every thread. */
-__device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k, uint64_t *ranked) {
-  if (threadIdx.x == 0) {
-    list[n] = 0ull; /* pads below every key */
-    list[n + 1] = 0ull;
-  }
-  __syncthreads();
-  const ulonglong2 *k2 = (const ulonglong2 *)list;
-  const uint32_t lg = n <= SPLIT_T / 4 ? 2u : n <= SPLIT_T / 2 ? 1u : 0u; /* log2 G */
-  const uint32_t np = (n + 1) / 2;                                         /* pairs */
-  const uint32_t share = (np + (1u << lg) - 1) >> lg;
-  const uint32_t part = threadIdx.x & ((1u << lg) - 1);
-  const uint32_t p0 = min(np, part * share), p1 = min(np, p0 + share);
-  for (uint32_t base = 0; base < n; base += SPLIT_T >> lg) {
-    const uint32_t t = base + (threadIdx.x >> lg);
-    const uint64_t my = t < n ? list[t] : ~0ull;
-    uint32_t rank = 0u;
-#pragma unroll 4
-    for (uint32_t j2 = p0; j2 < p1; j2++) {
-      const ulonglong2 q = k2[j2];
-      rank += (q.x > my ? 1u : 0u) + (q.y > my ? 1u : 0u);
-    }
-    if (lg >= 1) rank += dpp_u<0xb1, 0xf>(0u, rank); /* quad_perm [1,0,3,2] */
-    if (lg >= 2) rank += dpp_u<0x4e, 0xf>(0u, rank); /* quad_perm [2,3,0,1] */
-    if (part == 0 && t < n && rank < (uint32_t)k) ranked[rank] = my;
-  }
-  __syncthreads();
 }
 
 /* wave_kth_prefix over the SPLIT_T keys of a workgroup held in LDS, by
@@ -369,7 +329,7 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
         const uint64_t lp = S.raw[w * WAVE + t];
         S.keys[threadIdx.x] = composite_key(scale_logit(d3s_u2f((uint32_t)(lp >> 32)), T, y, true), (int)(uint32_t)lp);
       }
-      rank_by_count(S.keys, tot, k, S.ranked);
+      rank_by_count<SPLIT_T>(S.keys, tot, k, S.ranked);
       nfiled = min(tot, (uint32_t)k);
     }
   }
@@ -500,7 +460,7 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
       if (take) S.keys[at] = kv[q];
     }
     __syncthreads();
-    rank_by_count(S.keys, S.mcount, k, S.ranked);
+    rank_by_count<SPLIT_T>(S.keys, S.mcount, k, S.ranked);
     /* the top k reach x = -inf: ties the segments did not file */
     generic = key_x(S.ranked[k - 1]) == ninf;
   }

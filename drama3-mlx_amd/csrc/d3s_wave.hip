@@ -30,6 +30,7 @@
  * k_wide (below) runs the same passes on rows spread over a workgroup.
  */
 #include "d3s_rowcore.h"
+#include "d3s_gemv.h"
 
 #pragma clang fp contract(off)
 
@@ -531,13 +532,8 @@ constexpr int wave_occupancy() {
 
 /* k_linear: the backbone head's logits (src/backbone.c:1213-1215).  Each
  * half-wave takes one logit r and follows the reference's single-row gemv
- * (src/mlxu.c:365-400): its 32 lanes accumulate in fp32, lane l the products
- * of elements c*128 + 4l + t in block order, fused (fma); a shuffle-down tree
- * over 16, 8, 4, 2, 1 lanes adds them; the sum is rounded to bf16.  Sampling
- * the logits is a second launch (d3s_sample): handing a row's logits from
- * the workgroups that wrote them to one that samples them, inside one launch,
- * needs an agent-scope release per workgroup (an L2 write-back on every XCD)
- * and measured slower than the second launch. */
+ * (gemv_half_wave); the sum is rounded to bf16.  k_head (d3s_head.hip) runs
+ * the same gemv and samples its logits in the same launch. */
 constexpr int LIN_WAVES = 4;
 constexpr int LIN_PER_WG = 2 * LIN_WAVES; /* logits per workgroup */
 
@@ -546,34 +542,7 @@ __global__ __launch_bounds__(WAVE *LIN_WAVES) void k_linear(LinearArgs la) {
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id(), hl = lane & 31;
   const int r = ((int)blockIdx.x * LIN_WAVES + wid) * 2 + (lane >> 5);
-  const int KB = la.K / 128;
-  float acc = 0.0f;
-  if (r < la.V) {
-    const uint2 *wp = (const uint2 *)(la.w + (size_t)r * la.K) + hl;
-    const uint2 *xp = (const uint2 *)(la.x + (size_t)n * la.K) + hl;
-    for (int c0 = 0; c0 < KB; c0 += 16) {
-      uint2 wv[16], xv[16];
-#pragma unroll
-      for (int c = 0; c < 16; c++)
-        if (c0 + c < KB) {
-          wv[c] = wp[(c0 + c) * 32];
-          xv[c] = xp[(c0 + c) * 32];
-        }
-#pragma unroll
-      for (int c = 0; c < 16; c++)
-        if (c0 + c < KB) {
-          const uint32_t wq[2] = {wv[c].x, wv[c].y}, xq[2] = {xv[c].x, xv[c].y};
-#pragma unroll
-          for (int t = 0; t < 4; t++) {
-            const float wf = d3s_u2f(t & 1 ? wq[t / 2] & 0xffff0000u : wq[t / 2] << 16);
-            const float xf = d3s_u2f(t & 1 ? xq[t / 2] & 0xffff0000u : xq[t / 2] << 16);
-            acc = __builtin_fmaf(wf, xf, acc);
-          }
-        }
-    }
-  }
-#pragma unroll
-  for (int sn = 16; sn >= 1; sn >>= 1) acc = acc + __shfl_down(acc, sn, 32);
+  const float acc = gemv_half_wave(la, n, r, hl);
   if (hl == 0 && r < la.V) la.y[(size_t)n * la.V + r] = d3s_f32_to_bf16_rn(acc);
 }
 

@@ -18,6 +18,7 @@ FLAG_GENERIC = 1
 FLAG_EXACT_LSE = 2
 FLAG_EXACT_SELECT = 4
 FLAG_OP_GRAPH = 8
+FLAG_ONE_LAUNCH = 16
 COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
 NUM_COUNTERS = 4
 OK = 0
@@ -64,6 +65,9 @@ def lib():
         L.d3s_sample_ras.restype = i32
         L.d3s_linear_bf16.argtypes = [vp, vp, i64, i64, i64, vp, vp]
         L.d3s_linear_bf16.restype = i32
+        L.d3s_linear_sample_bf16.argtypes = [vp, vp, i64, i64, i64, vp, vp, i32, vp, vp, f32, f32, vp, vp,
+                                             vp, vp, u32, vp]
+        L.d3s_linear_sample_bf16.restype = i32
         L.d3s_uniform_fill.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
         L.d3s_uniform_fill.restype = i32
         L.d3s_max_k.argtypes = []
@@ -279,3 +283,52 @@ def linear_bf16(x, w):
         b.free()
     return rc, out
 
+
+
+def linear_sample_bf16(x, w, u, temperature, top_p, flags=0, want_probs=True, keep_logits=True, stream=None):
+    """Host helper for d3s_linear_sample_bf16: x uint16 [N, K], w uint16 [V, K]
+    (bf16 bits), u float32 [N, k]; temperature / top_p scalars or float32 [N].
+    Returns dict(rc, ids, probs, cand, counters, y) (y: the logits, uint16
+    [N, V], when keep_logits)."""
+    import hiprt
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    u = np.ascontiguousarray(u, np.float32)
+    N, K = x.shape
+    V = w.shape[0]
+    k = u.shape[1]
+    bufs = dict(x=hiprt.to_device(x), w=hiprt.to_device(w), u=hiprt.to_device(u), ids=hiprt.DeviceBuffer(4 * N),
+                counters=hiprt.DeviceBuffer(4 * NUM_COUNTERS).zero())
+    if keep_logits:
+        bufs["y"] = hiprt.DeviceBuffer(2 * N * V)
+    if want_probs:
+        bufs["probs"] = hiprt.DeviceBuffer(4 * N * k)
+        bufs["cand"] = hiprt.DeviceBuffer(4 * N * k)
+    t_ptr, t_s, p_ptr, p_s = None, 0.0, None, 0.0
+    if np.ndim(temperature):
+        bufs["T"] = hiprt.to_device(np.asarray(temperature, np.float32))
+        t_ptr = bufs["T"].ptr
+    else:
+        t_s = float(temperature)
+    if np.ndim(top_p):
+        bufs["P"] = hiprt.to_device(np.asarray(top_p, np.float32))
+        p_ptr = bufs["P"].ptr
+    else:
+        p_s = float(top_p)
+    g = lambda name: bufs[name].ptr if name in bufs else None
+    rc = lib().d3s_linear_sample_bf16(g("x"), g("w"), N, K, V, g("y"), g("u"), k, t_ptr, p_ptr, t_s, p_s,
+                                      g("ids"), g("probs"), g("cand"), g("counters"), flags,
+                                      stream.ptr if stream else None)
+    out = dict(rc=rc)
+    if rc == OK:
+        hiprt.synchronize()
+        out["ids"] = bufs["ids"].download((N,), np.int32)
+        out["counters"] = bufs["counters"].download((NUM_COUNTERS,), np.uint32)
+        if keep_logits:
+            out["y"] = bufs["y"].download((N, V), np.uint16)
+        if want_probs:
+            out["probs"] = bufs["probs"].download((N, k), np.float32)
+            out["cand"] = bufs["cand"].download((N, k), np.int32)
+    for b in bufs.values():
+        b.free()
+    return out

@@ -46,6 +46,8 @@ extern "C" {
                                     reference computes it with D3_NO_FUSED_SAMPLER
                                     set (src/sampling.c:197); the environment
                                     variable has the same effect */
+#define D3S_FLAG_ONE_LAUNCH 16u  /* d3s_linear_sample_bf16 only: the gemv and the
+                                    sample in one launch where it fits */
 
 /* counters[] slots, when a counters array is given (atomic per-row increments) */
 #define D3S_COUNTER_REFUSED 0      /* rows with a NaN / +inf x: id -1 */
@@ -156,6 +158,30 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
  * gemv_row (src/mlxu.c:454-496). */
 int d3s_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
                     uint16_t *y, void *stream);
+
+/* A head's logits and their sample: y = d3s_linear_bf16(x, w) (the
+ * reference's single-row gemv order, bit for bit), then ids = d3s_sample on y
+ * as bf16 logits [n_rows, V] with u [n_rows, k], the same temperature / top_p
+ * / flags / outputs and the same result bits, including the choice of the
+ * reference kernel's or the op graph's order.  y [n_rows, V] receives the
+ * logits, or may be NULL when the caller does not keep them (they then go to
+ * the stream's workspace).  No banned index.
+ * By default the gemv and the sample are two launches on the stream, the
+ * faster form.  With D3S_FLAG_ONE_LAUNCH, calls with k <= 64, V <= 8192 and
+ * at most 62 rows take one launch instead: each workgroup computes 16 logits
+ * and files its part of the sample (max, fast sum, the logits) in the
+ * stream's workspace, and the last to arrive samples the row (one kernel node
+ * instead of two, about 3.5 us slower on [1, 2048] x [4097, 2048]); other
+ * calls take the two launches.  The workspace is the one d3s_sample keeps per
+ * stream, allocated on the stream's first call that needs it (D3S_ERR_NOMEM
+ * if it cannot).
+ * Replaces: m_linear through gemv_row (src/mlxu.c:454-496) followed by
+ * sample_with_noise on its logits: the backbone head (src/backbone.c:1213-1215)
+ * and the tower's codebook heads (src/tower.c:228-232,:264,:440-443). */
+int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
+                           uint16_t *y, const float *u, int k, const float *temperature, const float *top_p,
+                           float temperature_scalar, float top_p_scalar, int32_t *ids, float *probs,
+                           int32_t *cand, uint32_t *counters, unsigned flags, void *stream);
 
 /* u[i] = the i-th uniform of draw `draw` under `seed` (Philox4x32-10, counter
  * (i/4, draw), key seed, 24-bit values in [0, 1)), for i < n.
