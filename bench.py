@@ -343,6 +343,32 @@ def other_configs(reps):
         log(f"{name}: {us:.1f} us per launch of {N} rows, {gbs:.0f} GB/s "
             f"({100 * gbs / HBM_PEAK_GBS:.1f} % of HBM peak)")
         del lg, u
+    # C4's rows with top-k disabled (k = V, the op graph's full argsort,
+    # src/sampling.c:33-35): the sorting kernel
+    w = W.make("C4", seed=5, uniforms=False)
+    x = w["logits"]
+    N, Vc = x.shape
+    lg, u, ids = hiprt.to_device(x), hiprt.DeviceBuffer(N * Vc * 4), hiprt.DeviceBuffer(4 * N)
+    assert d3s.lib().d3s_uniform_fill(u.ptr, N * Vc, 42, 0, None) == 0
+    hiprt.synchronize()
+    for _ in range(2):
+        assert d3s.sample_raw(lg.ptr, d3s.DTYPE_BF16, N, Vc, Vc, u.ptr, Vc, 1.0, 0.9, None, ids.ptr,
+                              stream=s.ptr) == 0
+    n = 10
+    a.record(s)
+    for _ in range(n):
+        assert d3s.sample_raw(lg.ptr, d3s.DTYPE_BF16, N, Vc, Vc, u.ptr, Vc, 1.0, 0.9, None, ids.ptr,
+                              stream=s.ptr) == 0
+    b.record(s)
+    b.synchronize()
+    us = a.elapsed_ms(b) * 1e3 / n
+    per_launch = N * (Vc * 2 + Vc * 4 + 4 + 12)
+    out["C4_k_eq_V"] = {"shape": [N, Vc], "dtype": "bf16", "k": Vc, "us_per_launch": us,
+                        "rows_per_s": N / (us * 1e-6), "bytes_per_launch": per_launch,
+                        "achieved_GBs": per_launch / (us * 1e-6) / 1e9}
+    log(f"C4 with top-k disabled (k = V = {Vc}): {us:.1f} us per launch of {N} rows")
+    for buf in (lg, u, ids):
+        buf.free()
     s.destroy()
     return out
 

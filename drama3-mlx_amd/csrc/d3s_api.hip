@@ -84,6 +84,27 @@ bool env_no_fused() { return getenv("D3_NO_FUSED_SAMPLER") != nullptr; }
 
 int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
 
+/* the sorting kernel's keys per launch from the stream's workspace: every
+ * row, up to 256 MiB (then launches of fewer rows), at least one row */
+constexpr size_t BIGK_WS_CAP = (size_t)256 << 20;
+
+/* the workspace sample_routed takes from a stream for these rows: the
+ * segmented kernel's (counters and records), or the counters' block and the
+ * sorting kernel's keys after it; 0 when no kernel needs one */
+size_t routed_workspace_bytes(const d3s::SampleArgs &a, d3s::Dtype dt) {
+  const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
+  if (!generic && d3s::split_segments(a, dt) > 0) return d3s::split_workspace_bytes(a, dt);
+  /* the nucleus kernel takes k > 64 on rows up to topp_max_vocab() */
+  const bool topp = !generic && a.k > 64 && a.vocab <= d3s::topp_max_vocab();
+  if (a.k > d3s::generic_max_k() && !topp) {
+    const size_t row = d3s::bigk_row_bytes(a);
+    size_t keys = row * (size_t)a.n_rows;
+    if (keys > BIGK_WS_CAP) keys = BIGK_WS_CAP > row ? BIGK_WS_CAP : row;
+    return d3s::split_counter_bytes() + keys;
+  }
+  return 0;
+}
+
 /* the first kernel that holds the row: one wave, the rows cut into segments
  * over many CUs (with a workspace), the fused workgroup (kernel order only),
  * the wide workgroup, the nucleus kernel, else the streaming one.  ws: the
@@ -104,6 +125,18 @@ int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s, void *
   if (!generic && !a.opgraph && d3s::launch_fused(a, dt, s)) return launched();
   if (!generic && d3s::launch_wide(a, dt, s)) return launched();
   if (!generic && d3s::launch_topp(a, dt, s)) return launched();
+  if (a.k > d3s::generic_max_k()) { /* the sorting kernel, its keys after the counters' block */
+    const size_t off = d3s::split_counter_bytes();
+    if (!ws && stream_ws) {
+      const size_t need = routed_workspace_bytes(a, dt);
+      ws = d3s::stream_workspace(s, need);
+      if (!ws) return D3S_ERR_NOMEM;
+      ws_bytes = need;
+    }
+    if (!ws || ws_bytes < off + d3s::bigk_row_bytes(a)) return stream_ws ? D3S_ERR_NOMEM : D3S_ERR_SCRATCH;
+    if (!d3s::launch_bigk(a, dt, (char *)ws + off, ws_bytes - off, s)) return D3S_ERR_SCRATCH;
+    return launched();
+  }
   if (!d3s::launch_generic(a, dt, s)) return D3S_ERR_UNSUPPORTED;
   return launched();
 }
@@ -118,7 +151,6 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   if (n_rows < 0 || n_rows > 0x7fffffff || vocab < 1 || vocab > (1 << 26) ||
       row_stride < vocab || k < 1 || k > vocab)
     return D3S_ERR_ARG;
-  if (k > d3s::generic_max_k()) return D3S_ERR_UNSUPPORTED;
   if (n_rows == 0) return D3S_OK;
   if (!logits || !u || !ids) return D3S_ERR_ARG;
   /* rows are addressed in whole elements */
@@ -146,8 +178,9 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
   if (!no_alloc) return sample_routed(a, dt, (hipStream_t)stream);
   void *ws = nullptr;
-  if (!(flags & D3S_FLAG_GENERIC) && d3s::split_segments(a, dt) > 0) { /* the segmented kernel takes it */
-    if (d3s::split_workspace_bytes(a, dt) > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
+  const size_t need = routed_workspace_bytes(a, dt);
+  if (need > 0) { /* the segmented kernel, or the sorting kernel one row at a time */
+    if (d3s::split_segments(a, dt) > 0 && need > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
     ws = device_scratch();
     if (!ws) return D3S_ERR_LAUNCH;
   }
@@ -230,12 +263,12 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
    * registers): the two draws as routed launches, then the pick.  The first
    * draw's indices go to first_idx or else main_tok (the pick reads each row's
    * before it writes it); the retry's to retry_idx or else the workspace. */
-  if (r.first.k > d3s_max_k() || r.retry.k > d3s_max_k()) return D3S_ERR_UNSUPPORTED;
-  /* one workspace block: the segmented kernel's counters and records first
-   * (both draws use them in turn), then the retry's indices, never on the
-   * counters (which must stay zero for later launches on this stream) */
-  size_t split_bytes = d3s::split_workspace_bytes(r.first, dt);
-  const size_t split_retry = d3s::split_workspace_bytes(r.retry, dt);
+  /* one workspace block: the segmented kernel's counters and records, or the
+   * sorting kernel's keys, first (both draws use them in turn), then the
+   * retry's indices, never on the counters (which must stay zero for later
+   * launches on this stream) */
+  size_t split_bytes = routed_workspace_bytes(r.first, dt);
+  const size_t split_retry = routed_workspace_bytes(r.retry, dt);
   if (split_retry > split_bytes) split_bytes = split_retry;
   if (split_bytes < d3s::split_counter_bytes()) split_bytes = d3s::split_counter_bytes();
   split_bytes = (split_bytes + 255) & ~(size_t)255;
@@ -279,7 +312,6 @@ int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows,
   if (n_rows < 0 || n_rows > 65535 || K < 128 || K % 128 != 0 || K > (1 << 20) || V < 1 || V > (1 << 24) ||
       k < 1 || k > V)
     return D3S_ERR_ARG;
-  if (k > d3s::generic_max_k()) return D3S_ERR_UNSUPPORTED;
   if (n_rows == 0) return D3S_OK;
   if (!x || !w || !u || !ids) return D3S_ERR_ARG;
   if ((uintptr_t)x % 8u != 0u || (uintptr_t)w % 8u != 0u || (uintptr_t)y % 2u != 0u) return D3S_ERR_ARG;
@@ -323,7 +355,7 @@ int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows,
   }
   /* the gemv, then the routed sample on its logits (into y, or else the
    * stream's workspace after the segmented kernel's counters and records) */
-  size_t split_bytes = d3s::split_workspace_bytes(a, d3s::DT_BF16);
+  size_t split_bytes = routed_workspace_bytes(a, d3s::DT_BF16);
   if (split_bytes < d3s::split_counter_bytes()) split_bytes = d3s::split_counter_bytes();
   split_bytes = (split_bytes + 255) & ~(size_t)255;
   const size_t total = split_bytes + (y ? 0 : (size_t)n_rows * (size_t)V * 2);
@@ -345,7 +377,7 @@ int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *st
   return n > 0 ? launched() : D3S_OK;
 }
 
-int d3s_max_k(void) { return d3s::generic_max_k(); }
+int d3s_max_k(void) { return 1 << 26; }
 
 int d3s_fused_max_vocab(int dtype) {
   if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;

@@ -74,6 +74,97 @@ __device__ __forceinline__ int wave_min_i32(int v) {
   return (int)readlane_u((uint32_t)v, 63);
 }
 
+/* The op graph's order over the k ranked keys of glist (composite keys, rank
+ * order; LDS or global memory): exact prefix sums of fix40(d3s_expf(x_r -
+ * lse)) over ranks (its cumsum, rounded once, src/sampling.c:39-42), the cut
+ * (the first r > 0 whose prefix exceeds top_p), the kept sum of
+ * fix40(d3s_expf(x_r - x_0)), the probabilities and the race over every rank
+ * (:43-48), each thread owning R consecutive ranks.  Every thread of the
+ * BLOCK-thread workgroup calls it. */
+template <int BLOCK>
+__device__ __forceinline__ void generic_tail_opgraph(const SampleArgs &a, const int row, const float lse,
+                                                     const float top_p, const uint64_t *glist) {
+  constexpr int GBLOCK = BLOCK, GNW = BLOCK / WAVE;
+  __shared__ uint32_t sh_u32[GNW], sh_lo[GNW], sh_hi[GNW];
+  __shared__ float sh_best[GNW];
+  __shared__ int sh_bestr[GNW];
+  const int tid = threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int k = a.k;
+  const int R = (k + GBLOCK - 1) / GBLOCK;
+  const int r0 = tid * R;
+  const float v0 = key_x(glist[0]);
+  uint64_t loc = 0;
+  for (int q = 0; q < R; q++) {
+    const int r = r0 + q;
+    if (r < k) loc += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
+  }
+  uint64_t P = block_excl_scan_u64<GNW>(loc, sh_lo, sh_hi);
+  int cut_local = k;
+  for (int q = 0; q < R; q++) {
+    const int r = r0 + q;
+    if (r < k) {
+      P += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
+      if (r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > top_p) cut_local = r;
+    }
+  }
+  const int cm = wave_min_i32(cut_local);
+  if (lane == 0) sh_u32[wid] = (uint32_t)cm;
+  __syncthreads();
+  int cut = k;
+  for (int w = 0; w < GNW; w++) cut = min(cut, (int)sh_u32[w]);
+  uint64_t ks = 0;
+  for (int q = 0; q < R; q++) {
+    const int r = r0 + q;
+    if (r < k && r < cut) ks += d3s_fix40(d3s_expf(key_x(glist[r]) - v0));
+  }
+  {
+    const uint64_t w = wave_sum_u64(ks);
+    __syncthreads();
+    if (lane == 0) {
+      sh_lo[wid] = (uint32_t)w;
+      sh_hi[wid] = (uint32_t)(w >> 32);
+    }
+  }
+  __syncthreads();
+  uint64_t KS = 0;
+  for (int w = 0; w < GNW; w++) KS += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
+  const float inv = 1.0f / d3s_fixsum_to_f32(KS);
+  float bs = -1.0f;
+  int br = 0x7fffffff;
+  for (int q = 0; q < R; q++) {
+    const int r = r0 + q;
+    if (r < k) {
+      const uint64_t key = glist[r];
+      const float p = r < cut ? d3s_expf(key_x(key) - v0) * inv : 0.0f;
+      const float noise = -d3s_logf(1.0f - a.u[(size_t)row * k + r]);
+      const float score = p / noise;
+      const float sc = score > -1.0f ? score : -1.0f;
+      if (sc > bs || br == 0x7fffffff) { /* first maximum within the thread's ranks */
+        bs = sc;
+        br = r;
+      }
+      if (a.probs) a.probs[(size_t)row * k + r] = p;
+      if (a.cand) a.cand[(size_t)row * k + r] = key_idx(key);
+    }
+  }
+  wave_argmax(bs, br);
+  if (lane == 0) {
+    sh_best[wid] = bs;
+    sh_bestr[wid] = br;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float b = sh_best[0];
+    int r = sh_bestr[0];
+    for (int w = 1; w < GNW; w++)
+      if (sh_best[w] > b || (sh_best[w] == b && sh_bestr[w] < r)) {
+        b = sh_best[w];
+        r = sh_bestr[w];
+      }
+    a.ids[row] = key_idx(glist[r]);
+  }
+}
+
 /* Row `row` by the whole BLOCK-thread workgroup (BLOCK a multiple of 256);
  * glist: LDS for kpow >= k composite keys (kpow a power of two); src(i): the
  * row's logit i as fp32, -inf at the banned index.  Every thread of the
@@ -86,8 +177,6 @@ __device__ __forceinline__ void generic_row_src(const SampleArgs &a, const int r
   __shared__ float sh_max[GNW];
   __shared__ uint32_t sh_flag[GNW], sh_u32[GNW], sh_lo[GNW], sh_hi[GNW];
   __shared__ int n_gather;
-  __shared__ float sh_best[GNW];
-  __shared__ int sh_bestr[GNW];
   __shared__ __align__(16) float wbuf[WAVE];
 
   const int tid = threadIdx.x, lane = lane_id(), wid = tid / WAVE;
@@ -224,81 +313,7 @@ __device__ __forceinline__ void generic_row_src(const SampleArgs &a, const int r
     return;
   }
 
-  /* ---- the op graph's order: exact prefix sums over ranks (its cumsum and
-   * softmax, src/sampling.c:39-44), each thread owning R consecutive ranks */
-  const int R = (k + GBLOCK - 1) / GBLOCK;
-  const int r0 = tid * R;
-  const float v0 = key_x(glist[0]);
-  uint64_t loc = 0;
-  for (int q = 0; q < R; q++) {
-    const int r = r0 + q;
-    if (r < k) loc += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
-  }
-  uint64_t P = block_excl_scan_u64<GNW>(loc, sh_lo, sh_hi);
-  int cut_local = k;
-  for (int q = 0; q < R; q++) {
-    const int r = r0 + q;
-    if (r < k) {
-      P += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
-      if (r > 0 && cut_local == k && d3s_fixsum_to_f32(P) > top_p) cut_local = r;
-    }
-  }
-  const int cm = wave_min_i32(cut_local);
-  if (lane == 0) sh_u32[wid] = (uint32_t)cm;
-  __syncthreads();
-  int cut = k;
-  for (int w = 0; w < GNW; w++) cut = min(cut, (int)sh_u32[w]);
-  uint64_t ks = 0;
-  for (int q = 0; q < R; q++) {
-    const int r = r0 + q;
-    if (r < k && r < cut) ks += d3s_fix40(d3s_expf(key_x(glist[r]) - v0));
-  }
-  {
-    const uint64_t w = wave_sum_u64(ks);
-    __syncthreads();
-    if (lane == 0) {
-      sh_lo[wid] = (uint32_t)w;
-      sh_hi[wid] = (uint32_t)(w >> 32);
-    }
-  }
-  __syncthreads();
-  uint64_t KS = 0;
-  for (int w = 0; w < GNW; w++) KS += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
-  const float inv = 1.0f / d3s_fixsum_to_f32(KS);
-  float bs = -1.0f;
-  int br = 0x7fffffff;
-  for (int q = 0; q < R; q++) {
-    const int r = r0 + q;
-    if (r < k) {
-      const uint64_t key = glist[r];
-      const float p = r < cut ? d3s_expf(key_x(key) - v0) * inv : 0.0f;
-      const float noise = -d3s_logf(1.0f - a.u[(size_t)row * k + r]);
-      const float score = p / noise;
-      const float sc = score > -1.0f ? score : -1.0f;
-      if (sc > bs || br == 0x7fffffff) { /* first maximum within the thread's ranks */
-        bs = sc;
-        br = r;
-      }
-      if (a.probs) a.probs[(size_t)row * k + r] = p;
-      if (a.cand) a.cand[(size_t)row * k + r] = key_idx(key);
-    }
-  }
-  wave_argmax(bs, br);
-  if (lane == 0) {
-    sh_best[wid] = bs;
-    sh_bestr[wid] = br;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float b = sh_best[0];
-    int r = sh_bestr[0];
-    for (int w = 1; w < GNW; w++)
-      if (sh_best[w] > b || (sh_best[w] == b && sh_bestr[w] < r)) {
-        b = sh_best[w];
-        r = sh_bestr[w];
-      }
-    a.ids[row] = key_idx(glist[r]);
-  }
+  generic_tail_opgraph<BLOCK>(a, row, lse, top_p, glist);
 }
 
 /* generic_row_src over row `row` of a.logits */

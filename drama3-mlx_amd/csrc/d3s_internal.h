@@ -142,6 +142,12 @@ int topp_max_vocab();
 /* Launch the streaming generic kernel (any V, k <= generic_max_k()). */
 bool launch_generic(const SampleArgs &a, Dtype dt, hipStream_t s);
 int generic_max_k();
+/* Launch the sorting kernel for k beyond generic_max_k() (any V, any k <= V):
+ * one workgroup per row sorts the row's keys in ws (bigk_row_bytes per row;
+ * rows go in launches of as many as ws holds).  Returns false when ws does
+ * not hold one row. */
+bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s);
+size_t bigk_row_bytes(const SampleArgs &a);
 /* u[i] = d3s_uniform(seed, stream_id, i), i < n */
 void launch_uniform(float *u, int64_t n, uint64_t seed, uint64_t stream_id, hipStream_t s);
 /* elementwise d3s_expf / d3s_logf / x / divisor / d3s_fix40 for the math self-test */

@@ -91,17 +91,19 @@ def lib():
 
 
 def sample_raw(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, banned, ids,
-               probs=None, cand=None, counters=None, flags=0, stream=None):
-    """d3s_sample on device pointers (ints).  temperature / top_p: a float
-    (scalar) or a device pointer wrapped as ("ptr", address)."""
+               probs=None, cand=None, counters=None, flags=0, stream=None, noalloc=False):
+    """d3s_sample (or d3s_sample_noalloc) on device pointers (ints).
+    temperature / top_p: a float (scalar) or a device pointer wrapped as
+    ("ptr", address)."""
     t_ptr, t_s = (temperature[1], 0.0) if isinstance(temperature, tuple) else (None, float(temperature))
     p_ptr, p_s = (top_p[1], 0.0) if isinstance(top_p, tuple) else (None, float(top_p))
-    return lib().d3s_sample(logits, dtype, n_rows, vocab, row_stride, u, k, t_ptr, p_ptr, t_s, p_s,
-                            banned, ids, probs, cand, counters, flags, stream)
+    fn = lib().d3s_sample_noalloc if noalloc else lib().d3s_sample
+    return fn(logits, dtype, n_rows, vocab, row_stride, u, k, t_ptr, p_ptr, t_s, p_s,
+              banned, ids, probs, cand, counters, flags, stream)
 
 
 def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True, row_stride=None,
-           vocab=None, stream=None):
+           vocab=None, stream=None, noalloc=False):
     """Host arrays in, host arrays out (copies through device memory).
     logits: float32 or uint16 (bf16 bits) [N, row_stride]; u: float32 [N, k];
     temperature / top_p: scalars or float32 [N].  Returns dict(ids, probs, cand,
@@ -136,7 +138,7 @@ def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True,
     rc = sample_raw(bufs["logits"].ptr, dtype, N, V, stride, bufs["u"].ptr, k, T, P, ban,
                     bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
                     bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
-                    stream.ptr if stream else None)
+                    stream.ptr if stream else None, noalloc=noalloc)
     out = dict(rc=rc)
     if rc != OK:
         return out
