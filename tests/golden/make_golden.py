@@ -9,7 +9,9 @@ the C oracle and of the kernels:
   closed_form_wide.npz     rows wider than one wave's registers (V 10000 to
                            151936, k <= 64; bf16 logits, also read widened to
                            fp32): the fused, wide and generic kernels, and rows
-                           past the reference kernel's V <= 65536.
+                           past the reference kernel's V <= 65536;
+  closed_form_sorted.npz   k beyond 16384 on rows of 16500 and 20000 (k up to
+                           V; bf16 values): the sorting kernel.
 
 The reference itself commits no vectors for this path (its pinning tests
 compute expectations at run time on Apple hardware), so these fixtures fix the
@@ -108,6 +110,25 @@ def wide_rows():
     return out
 
 
+def sorted_rows():
+    """k beyond 16384 on rows past the nucleus kernel's 8192 (top-k disabled
+    on a wide row): the sorting kernel.  bf16 values, as wide_rows."""
+    rng = np.random.default_rng(20261204)
+    out = []
+    for V, k, kind in [(16500, 16500, 0), (20000, 16400, 1)]:
+        x = (rng.standard_normal(V) * 1.5).astype(np.float32)
+        if kind == 0:
+            x[rng.integers(0, V, 12)] += np.float32(5.0)
+        else:  # ties, and a masked stretch
+            x = (np.round(x * 2) / 2).astype(np.float32)
+            x[3000:5000] = -np.inf
+        T = np.float32(1.0 if kind == 0 else 0.7)
+        top_p = np.float32(0.9 if kind == 0 else 0.95)
+        u = rng.random(k).astype(np.float32)
+        out.append((bf16_bits(x), u, T, top_p, k))
+    return out
+
+
 def write(name, rs, ragged=False):
     """rows (x, u, T, top_p, k) and their closed-form answers; ragged rows
     (different V) are stored flat with offsets"""
@@ -145,6 +166,7 @@ def main():
     write("closed_form_rows.npz", rows())
     write("closed_form_nucleus.npz", nucleus_rows(), ragged=True)
     write("closed_form_wide.npz", wide_rows(), ragged=True)
+    write("closed_form_sorted.npz", sorted_rows(), ragged=True)
 
 
 if __name__ == "__main__":

@@ -7,7 +7,8 @@ post-filter probabilities within 1e-5 relative where the kept set agrees.
 closed_form_rows.npz reaches the one-wave kernel (V = 257, k <= 40);
 closed_form_nucleus.npz the nucleus and generic kernels (k > 64 up to k = V);
 closed_form_wide.npz the fused, wide and generic kernels (V 10000 to 151936,
-bf16 values read as bf16 and widened to fp32)."""
+bf16 values read as bf16 and widened to fp32); closed_form_sorted.npz the
+sorting kernel (k beyond 16384 on rows of 16500 and 20000)."""
 import os
 
 import numpy as np
@@ -16,7 +17,7 @@ import pytest
 import closed_form as CF
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-FIXTURES = ["closed_form_rows.npz", "closed_form_nucleus.npz", "closed_form_wide.npz"]
+FIXTURES = ["closed_form_rows.npz", "closed_form_nucleus.npz", "closed_form_wide.npz", "closed_form_sorted.npz"]
 RTOL = 1e-5
 
 
@@ -71,7 +72,7 @@ def test_fixture_is_the_closed_form(name):
 
 
 @pytest.mark.parametrize("name,widen", [(FIXTURES[0], False), (FIXTURES[1], False), (FIXTURES[2], False),
-                                        (FIXTURES[2], True)])
+                                        (FIXTURES[2], True), (FIXTURES[3], False)])
 def test_oracle_matches_golden_rows(oracle, name, widen):
     check(lambda x, u, T, p: oracle.sample(x, u, T, p), "oracle", name, widen)
 
@@ -79,7 +80,7 @@ def test_oracle_matches_golden_rows(oracle, name, widen):
 @pytest.mark.gpu
 @pytest.mark.parametrize("flags", [0, 1])
 @pytest.mark.parametrize("name,widen", [(FIXTURES[0], False), (FIXTURES[1], False), (FIXTURES[2], False),
-                                        (FIXTURES[2], True)])
+                                        (FIXTURES[2], True), (FIXTURES[3], False), (FIXTURES[3], True)])
 def test_gpu_matches_golden_rows(name, widen, flags):
     """every route's kernels (flags 1: the generic kernel) against the fixtures"""
     import d3s
