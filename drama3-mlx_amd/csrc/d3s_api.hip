@@ -94,8 +94,10 @@ constexpr size_t BIGK_WS_CAP = (size_t)256 << 20;
 size_t routed_workspace_bytes(const d3s::SampleArgs &a, d3s::Dtype dt) {
   const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
   if (!generic && d3s::split_segments(a, dt) > 0) return d3s::split_workspace_bytes(a, dt);
-  /* the nucleus kernel takes k > 64 on rows up to topp_max_vocab() */
+  /* the nucleus kernel takes k > 64 on rows up to topp_max_vocab() (its
+   * ids-only form files the rows it leaves in the workspace) */
   const bool topp = !generic && a.k > 64 && a.vocab <= d3s::topp_max_vocab();
+  if (topp) return d3s::topp_workspace_bytes(a);
   if (a.k > d3s::generic_max_k() && !topp) {
     const size_t row = d3s::bigk_row_bytes(a);
     size_t keys = row * (size_t)a.n_rows;
@@ -124,7 +126,14 @@ int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s, void *
   }
   if (!generic && !a.opgraph && d3s::launch_fused(a, dt, s)) return launched();
   if (!generic && d3s::launch_wide(a, dt, s)) return launched();
-  if (!generic && d3s::launch_topp(a, dt, s)) return launched();
+  if (!generic && a.k > 64 && a.vocab <= d3s::topp_max_vocab()) {
+    const size_t need = d3s::topp_workspace_bytes(a);
+    if (need > 0 && !ws && stream_ws) {
+      ws = d3s::stream_workspace(s, need);
+      ws_bytes = ws ? need : 0; /* without one: the full path for every row */
+    }
+    if (d3s::launch_topp(a, dt, ws, ws_bytes, s)) return launched();
+  }
   if (a.k > d3s::generic_max_k()) { /* the sorting kernel, its keys after the counters' block */
     const size_t off = d3s::split_counter_bytes();
     if (!ws && stream_ws) {

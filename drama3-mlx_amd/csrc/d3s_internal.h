@@ -136,9 +136,14 @@ size_t split_counter_bytes();
 bool launch_fused(const SampleArgs &a, Dtype dt, hipStream_t s);
 /* Largest V the fused kernel accepts for this dtype. */
 int fused_max_vocab(Dtype dt);
-/* Launch the ranked-nucleus kernel (k > 64, V <= topp_max_vocab()). */
-bool launch_topp(const SampleArgs &a, Dtype dt, hipStream_t s);
+/* Launch the ranked-nucleus kernel (k > 64, V <= topp_max_vocab()).  Calls
+ * that ask for ids only with k = V take the ids-only kernel and a second
+ * launch for the rows it leaves to the full path, with ws (at least
+ * topp_workspace_bytes: the counter block, whose first two lines hold its
+ * counts, then a row list); without ws, the full path for every row. */
+bool launch_topp(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s);
 int topp_max_vocab();
+size_t topp_workspace_bytes(const SampleArgs &a);
 /* Launch the streaming generic kernel (any V, k <= generic_max_k()). */
 bool launch_generic(const SampleArgs &a, Dtype dt, hipStream_t s);
 int generic_max_k();

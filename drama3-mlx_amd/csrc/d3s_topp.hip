@@ -285,6 +285,8 @@ __device__ __forceinline__ CutBands topp_cut_bands(uint64_t Tq, uint64_t S, floa
  * uncertainty, when more elements than a wave holds would go to that wave, or
  * when no kept score is positive. */
 constexpr int TOPP_FULL = -2;
+constexpr int TOPP_RETRY = -3; /* the ids path's round 1 (internal) */
+constexpr int TOPP_REDO_WG = 64; /* k_topp_redo's workgroups (at most) */
 constexpr int TF_CAP = WAVE; /* the elements (and refined ranks) one wave takes */
 
 /* byte offsets in the dynamic LDS region: group sums (one per thread); the
@@ -434,12 +436,16 @@ __device__ __forceinline__ int topp_bucket_of_rank(const uint32_t *bstart, int r
   return lo;
 }
 
-/* 4'-5' once the bucket counts and group sums are in LDS.  Returns the id or
- * TOPP_FULL; every thread calls it and every return follows a barrier. */
+/* 4'-5' once the bucket counts and group sums are in LDS.  Returns the id,
+ * TOPP_FULL, or (round 0: the exact prefix puts the cut outside the group the
+ * bands chose) TOPP_RETRY, after which the caller runs the row again as round
+ * 1 (exact_grp): exact group sums of fix40(expf(x - lse)) then give the group
+ * holding the cut and the exact prefix before it.  Every thread calls it and
+ * every return follows a barrier. */
 template <int EPT, int TBLOCK, int NBK>
 __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const float (&x)[EPT],
-                                             const float (&uv)[EPT], float m, float xmin, float scale, float top_p,
-                                             uint32_t *bstart, char *dyn, TRed &R) {
+                                             const float (&uv_in)[EPT], float m, float xmin, float scale, float top_p,
+                                             uint32_t *bstart, char *dyn, TRed &R, const bool exact_grp) {
   constexpr int PER = NBK / TBLOCK;
   static_assert(PER % 4 == 0, "whole 16-byte groups of buckets per thread");
   const int V = a.vocab, k = a.k;
@@ -469,6 +475,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       loc += c[q].x + c[q].y + c[q].z + c[q].w;
     }
     gs = gsum[tid];
+    if (exact_grp) gsum[tid] = 0ull; /* (only this thread reads entry tid; the scan's barriers follow) */
     uint32_t run, tot;
     block_excl_scan2(loc, gs, R, run, tot, gst, S);
 #pragma unroll
@@ -497,17 +504,39 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   const bool settled1 = Tq == 0ull;                     /* every prefix passes: cut 1 */
   const bool settledk = Tq > ((uint64_t)k << 41);      /* none reaches it: cut k */
   uint64_t tdrop = ~0ull, tkeep = 0ull;
-  if (!settled1 && !settledk) {
-    const CutBands cb = topp_cut_bands_lean(Tq, S, lse, lnS, xmin, k);
-    tdrop = cb.tdrop;
-    tkeep = cb.tkeep;
-    if (gst < tdrop && tdrop <= gst + gs) {
+  uint64_t pg0 = 0ull; /* round 1: the exact prefix before the group */
+  if (!exact_grp) {
+    if (!settled1 && !settledk) {
+      const CutBands cb = topp_cut_bands_lean(Tq, S, lse, lnS, xmin, k);
+      tdrop = cb.tdrop;
+      tkeep = cb.tkeep;
+      if (gst < tdrop && tdrop <= gst + gs) {
+        misc[4] = (uint32_t)tid;
+        misc64[0] = gst;
+      }
+    }
+  } else {
+    /* round 1: exact group sums (the scan's barriers ordered the clearing
+     * before these), their prefixes, the first group reaching Tq */
+#pragma unroll
+    for (int j = 0; j < EPT; j++) { /* (-inf and past the row: 0, into a slot past the groups') */
+      const int b = topp_bucket_of<NBK>(x[j], m, scale);
+      atomicAdd((unsigned long long *)&gsum[(uint32_t)b / PER], (unsigned long long)d3s_fix40_exp(x[j] - lse));
+    }
+    __syncthreads();
+    const uint64_t E = gsum[tid];
+    uint32_t cx, ctot;
+    uint64_t Ex, Etot;
+    block_excl_scan2(0u, E, R, cx, ctot, Ex, Etot);
+    if (!settled1 && Ex < Tq && Tq <= Ex + E) {
       misc[4] = (uint32_t)tid;
       misc64[0] = gst;
+      misc64[1] = Ex;
     }
   }
   __syncthreads(); /* the starts, the map, the cut group */
-  const int g = settled1 || settledk ? -1 : (int)misc[4]; /* -1: no group (cleared to ~0) */
+  const int g = settled1 || (settledk && !exact_grp) ? -1 : (int)misc[4]; /* -1: no group (cleared to ~0) */
+  if (exact_grp && g >= 0) pg0 = misc64[1];
   uint32_t s0 = 0u;
   int klo, khi;
   if (settled1) {
@@ -533,6 +562,12 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     else
       topp_ebounds<NBK>(bstart[NBK] < (uint32_t)V ? NBK : NBK - 1, rs, dmax, emin, eh); /* every rank */
   }
+  /* this thread's ranks' uniforms: in flight with the row in round 0, read
+   * here in round 1 (fewer registers live through its group sums) */
+  float uv[EPT];
+#pragma unroll
+  for (int q = 0; q < EPT; q++)
+    uv[q] = !exact_grp ? uv_in[q] : (q < RPT && r0 + q < k) ? a.u[(size_t)row * k + r0 + q] : 0.0f;
   float hb0[EPT];
   float lbm = -1.0f;
 #pragma unroll
@@ -654,11 +689,12 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
         const int src = (int)__builtin_ctzll(at | (1ull << 63));
         qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
       }
-      certain = cut <= 1 || qlast < tkeep;
+      /* (round 1: the cut from the group's exact prefixes below) */
+      certain = !exact_grp && (cut <= 1 || qlast < tkeep);
     } else {
       cut = klo;
       qlast = cut == 1 ? (1ull << 40) : S; /* rank 0's term, or every term */
-      certain = cut <= 1 || settledk || qlast < tkeep;
+      certain = exact_grp || cut <= 1 || settledk || qlast < tkeep;
     }
     if (lane == 0) misc[1] = certain ? 0u : (g >= 0 ? 1u : 2u);
   }
@@ -669,14 +705,17 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     /* the cut within the bands' uncertainty: the exact prefix P before the
      * group (block sum of fix40(expf(x - lse)) over the elements of the
      * buckets before it), then the group's exact prefixes */
-    uint64_t part = 0ull;
+    uint64_t p0 = pg0;
+    if (!exact_grp) {
+      uint64_t part = 0ull;
 #pragma unroll
-    for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
-      const int bb = topp_bucket_of<NBK>(x[j], m, scale);
-      if (i < V && bb < g * PER) part += d3s_fix40_exp(x[j] - lse);
+      for (int j = 0; j < EPT; j++) {
+        const int i = j * TBLOCK + tid;
+        const int bb = topp_bucket_of<NBK>(x[j], m, scale);
+        if (i < V && bb < g * PER) part += d3s_fix40_exp(x[j] - lse);
+      }
+      p0 = block_sum_u64(part, R);
     }
-    const uint64_t p0 = block_sum_u64(part, R);
     if (tid < WAVE) {
       const uint64_t pt = ing ? d3s_fix40_exp(key_x(mk) - lse) : 0ull;
       uint64_t pinc = 0ull;
@@ -695,10 +734,12 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
         const int src = (int)__builtin_ctzll(at | (1ull << 63));
         qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
       }
-      if (lane == 0 && (p0 >= Tq || re == 0x7fffffff)) misc[2] = (uint32_t)TOPP_FULL;
+      /* the cut outside the group: round 1 (after round 0), the full path */
+      if (lane == 0 && (p0 >= Tq || re == 0x7fffffff)) misc[2] = (uint32_t)(exact_grp ? TOPP_FULL : TOPP_RETRY);
     }
     __syncthreads();
-    if (misc[2] == (uint32_t)TOPP_FULL) return TOPP_FULL; /* (after the barrier above) */
+    const uint32_t m2 = misc[2];
+    if (m2 == (uint32_t)TOPP_FULL || m2 == (uint32_t)TOPP_RETRY) return (int)m2; /* (after the barrier above) */
   }
   /* ---- the candidates' exact scores and their first maximum */
   if (tid < WAVE) {
@@ -1041,12 +1082,12 @@ __device__ __forceinline__ bool topp_max_min(const SampleArgs &a, int row, float
   return true;
 }
 
-/* k_topp: every output (ids, probabilities, candidates) by the full path */
-template <int EPT, bool BF16, int TBLOCK>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
-    SampleArgs a) {
-  D3S_TOPP_SHARED
-  const int row = (int)blockIdx.x;
+/* The full path for row `row` (every output: ids, probabilities,
+ * candidates), by the whole workgroup; keys: V slots of LDS. */
+template <int EPT, bool BF16, int TBLOCK, int NBK>
+__device__ __forceinline__ void topp_full_row(const SampleArgs &a, const int row, uint64_t *keys, uint32_t *bstart,
+                                              TRed &R) {
+  const int tid = (int)threadIdx.x;
   const int V = a.vocab;
   const RowP rp = row_params(a, row);
   const float T = rp.T;
@@ -1094,15 +1135,38 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
   topp_full<EPT, BF16, TBLOCK>(a, row, rp, rowp, x, ev, m, xmin, scale, S, lnS, lse, bstart, keys, R);
 }
 
-/* k_topp_ids: ids only, k = V; the ids-only path, the full path for the rows
- * it leaves */
+/* k_topp: every output (ids, probabilities, candidates) by the full path */
 template <int EPT, bool BF16, int TBLOCK>
-__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp_ids(
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_waves(EPT, TBLOCK)))) void k_topp(
     SampleArgs a) {
   D3S_TOPP_SHARED
+  topp_full_row<EPT, BF16, TBLOCK, NBK>(a, (int)blockIdx.x, keys, bstart, R);
+}
+
+/* The rows the ids-only path leaves to the full path: a count and the rows,
+ * filed by k_topp_ids and taken by k_topp_redo, which leaves the count (and
+ * its own arrival count) zero again.  The counts sit in the first two
+ * 128-byte lines of the stream workspace's counter block (every kernel that
+ * counts there leaves its counters zero); the rows after the block. */
+struct ToppRedo {
+  uint32_t *count; /* rows filed */
+  uint32_t *done;  /* k_topp_redo's workgroups finished */
+  int32_t *rows;   /* [n_rows] */
+};
+
+/* waves per SIMD of the ids-only kernel: its LDS (the bucket bounds and the
+ * ids path's arrays, without the full path's keys) fits four 512-thread
+ * workgroups per CU */
+constexpr int topp_ids_waves(int ept, int tb) { return tb == 512 ? 8 : topp_waves(ept, tb); }
+
+/* The ids-only path for row `row` (ids only, k = V), by the whole workgroup;
+ * dyn: its LDS arrays.  Returns true when the row's id is written, false when
+ * the row needs another round (the full path after round 1, exact_grp). */
+template <int EPT, bool BF16, int TBLOCK, int NBK>
+__device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row, char *dyn, uint32_t *bstart,
+                                             TRed &R, const bool exact_grp) {
   constexpr int PER = NBK / TBLOCK;
-  char *dyn = (char *)keys;
-  const int row = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
   const int V = a.vocab;
   const RowP rp = row_params(a, row);
   const float T = rp.T;
@@ -1136,7 +1200,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
       const int i = j * TBLOCK + tid;
       const int ii = i < V ? i : V - 1;
       x[j] = BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[ii]) : ((const float *)rowp)[ii];
-      uv[j] = (j < RPT && r0 + j < V) ? a.u[(size_t)row * V + r0 + j] : 0.0f;
+      uv[j] = (!exact_grp && j < RPT && r0 + j < V) ? a.u[(size_t)row * V + r0 + j] : 0.0f; /* (round 1: later) */
     }
   }
   if (T == 1.0f) {
@@ -1159,7 +1223,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
     }
   }
   float m, xmin;
-  if (!topp_max_min<EPT>(a, row, xm, xl, m, xmin, R)) return;
+  if (!topp_max_min<EPT>(a, row, xm, xl, m, xmin, R)) return true; /* (id written) */
   const float dmax = m - xmin;
   const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
 
@@ -1176,43 +1240,87 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_wav
       atomicAdd((unsigned long long *)&((uint64_t *)dyn)[(uint32_t)b / PER], (unsigned long long)f);
     }
     __syncthreads(); /* the counts and sums in (the row sum S is their total) */
-    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, uv, m, xmin, scale, rp.top_p, bstart, dyn, R);
-    if (id != TOPP_FULL) {
+    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, uv, m, xmin, scale, rp.top_p, bstart, dyn, R, exact_grp);
+    if (id >= 0) {
       if (tid == 0) a.ids[row] = id;
-      return;
+      return true;
     }
   }
-  /* the full path, the row read again (nothing of the ids path's stays
-   * live into it): x, e and the row sum */
-  float x2[EPT], ev[EPT];
-  uint64_t acc = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int i = j * TBLOCK + tid;
-    x2[j] = i < V ? scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite) : -__builtin_inff();
-    ev[j] = d3s_expf_nonpos(x2[j] - m);
-    acc += d3s_fix40_unit(ev[j]);
-  }
-  const uint64_t S = block_sum_u64(acc, R);
-  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
-  const float lse = m + lnS;
-  topp_full<EPT, BF16, TBLOCK>(a, row, rp, rowp, x2, ev, m, xmin, scale, S, lnS, lse, bstart, keys, R);
+  return false; /* TOPP_FULL, TOPP_RETRY, or scale 0 (a single finite x, or a row of equal ones) */
 }
+
+/* k_topp_ids: ids only, k = V; the ids-only path, the rows it leaves (round 1
+ * or the full path) filed for k_topp_redo */
+template <int EPT, bool BF16, int TBLOCK>
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids_waves(EPT, TBLOCK)))) void k_topp_ids(
+    SampleArgs a, ToppRedo rd) {
+  D3S_TOPP_SHARED
+  const int row = (int)blockIdx.x;
+  if (!topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, false) && tid == 0)
+    rd.rows[atomicAdd(rd.count, 1u)] = row;
+}
+
+/* k_topp_redo: each filed row again, the ids-only path's round 1 and, where
+ * that leaves it, the full path (TOPP_REDO_WG workgroups take the rows in
+ * turn; a few rows per launch, so registers are given room: the loop around
+ * the row must not spill); the last workgroup to finish clears the counts.
+ * No waiting: a workgroup that finds no row left ends.  LDS: the larger of
+ * the two paths' arrays. */
+template <int EPT, bool BF16, int TBLOCK>
+__global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) void k_topp_redo(
+    SampleArgs a, ToppRedo rd) {
+  D3S_TOPP_SHARED
+  const uint32_t n = __hip_atomic_load(rd.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 1
+  for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
+    const int row = rd.rows[i];
+    __syncthreads(); /* the previous row's LDS reads done */
+    if (!topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, true)) {
+      __syncthreads();
+      topp_full_row<EPT, BF16, TBLOCK, NBK>(a, row, keys, bstart, R);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(rd.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == gridDim.x - 1u) { /* every workgroup has read the count */
+      __hip_atomic_store(rd.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(rd.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 #undef D3S_TOPP_SHARED
 
+/* the ids-only path takes calls with k = V and neither probabilities nor
+ * candidates */
+bool topp_ids_call(const SampleArgs &a) {
+  return !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
+}
+
 template <int EPT, bool BF16, int TBLOCK>
-bool try_topp(const SampleArgs &a, hipStream_t s) {
+bool try_topp(const SampleArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
   if (a.vocab > EPT * TBLOCK) return false;
-  /* ids only, k = V (top-k disabled): the ids-only path first */
-  const bool ids = !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
-  /* the ranked keys, or the ids-only path's arrays */
-  const size_t ranked = (size_t)a.vocab * sizeof(uint64_t);
-  const size_t arrays = tf_bytes(TBLOCK, topp_buckets(EPT * TBLOCK, TBLOCK), a.vocab);
-  const size_t lds = ranked > arrays ? ranked : arrays;
-  if (ids)
-    hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
-  else
-    hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), lds, s, a);
+  const size_t ranked = (size_t)a.vocab * sizeof(uint64_t); /* the full path's keys */
+  /* (rows past 5120 elements: the redo kernel's loop would need scratch at
+   * 1024 threads a workgroup, so those take the full path) */
+  if constexpr (EPT * TBLOCK <= 5120) {
+    if (topp_ids_call(a) && ws && ws_bytes >= topp_workspace_bytes(a)) {
+      /* ids only, k = V (top-k disabled): the ids-only path with its own LDS,
+       * then the full path for the rows it files */
+      const size_t arrays = tf_bytes(TBLOCK, topp_buckets(EPT * TBLOCK, TBLOCK), a.vocab);
+      ToppRedo rd;
+      rd.count = (uint32_t *)ws;
+      rd.done = (uint32_t *)((char *)ws + 128);
+      rd.rows = (int32_t *)((char *)ws + split_counter_bytes());
+      hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), arrays, s, a, rd);
+      const int grid = a.n_rows < TOPP_REDO_WG ? a.n_rows : TOPP_REDO_WG;
+      hipLaunchKernelGGL((k_topp_redo<EPT, BF16, TBLOCK>), dim3(grid), dim3(TBLOCK), ranked > arrays ? ranked : arrays,
+                         s, a, rd);
+      return true;
+    }
+  }
+  hipLaunchKernelGGL((k_topp<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), ranked, s, a);
   return true;
 }
 
@@ -1220,14 +1328,22 @@ bool try_topp(const SampleArgs &a, hipStream_t s) {
 
 int topp_max_vocab() { return 8 * 1024; }
 
-bool launch_topp(const SampleArgs &a, Dtype dt, hipStream_t s) {
+size_t topp_workspace_bytes(const SampleArgs &a) {
+  return a.k > KF && a.vocab <= 5120 && topp_ids_call(a)
+             ? split_counter_bytes() + (size_t)a.n_rows * sizeof(int32_t)
+             : 0;
+}
+
+bool launch_topp(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
   if (a.k <= KF) return false;
   /* rows up to 4608 elements: 512 threads, three workgroups per CU (the
    * per-wave share of the reductions and the row's scalar arithmetic is
    * paid by 8 waves instead of 16); longer rows: 1024 threads */
   if (dt == DT_F32)
-    return try_topp<9, false, 512>(a, s) || try_topp<5, false, 1024>(a, s) || try_topp<8, false, 1024>(a, s);
-  return try_topp<9, true, 512>(a, s) || try_topp<5, true, 1024>(a, s) || try_topp<8, true, 1024>(a, s);
+    return try_topp<9, false, 512>(a, ws, ws_bytes, s) || try_topp<5, false, 1024>(a, ws, ws_bytes, s) ||
+           try_topp<8, false, 1024>(a, ws, ws_bytes, s);
+  return try_topp<9, true, 512>(a, ws, ws_bytes, s) || try_topp<5, true, 1024>(a, ws, ws_bytes, s) ||
+         try_topp<8, true, 1024>(a, ws, ws_bytes, s);
 }
 
 }  // namespace d3s
