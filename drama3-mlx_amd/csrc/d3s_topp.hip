@@ -455,9 +455,12 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   uint64_t *lval = (uint64_t *)(dyn + tf_lval(TBLOCK)); /* bucket */
   int *rr = (int *)(dyn + tf_rr(TBLOCK));
   float *ru = (float *)(dyn + tf_ru(TBLOCK));
-  /* [0] elements, [1] flag, [2] id, [3] refined ranks, [4] the cut group */
+  /* [0] elements, [1] flag, [2] id, [3] refined ranks, [4] the cut group,
+   * [5] (round 0) the group holding the certain keep band's end */
   uint32_t *misc = (uint32_t *)(dyn + tf_misc(TBLOCK));
-  uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32); /* [0] the cut group's prefix, [1] P before it */
+  /* [0] the cut group's prefix Q; [1] round 0: group [5]'s Q, round 1: the
+   * exact prefix before the cut group */
+  uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32);
   uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
   uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
   uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V)); /* bucket + 1 at each bucket's first rank */
@@ -514,6 +517,10 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
         misc[4] = (uint32_t)tid;
         misc64[0] = gst;
       }
+      if (gst < tkeep && tkeep <= gst + gs) {
+        misc[5] = (uint32_t)tid;
+        misc64[1] = gst;
+      }
     }
   } else {
     /* round 1: exact group sums (the scan's barriers ordered the clearing
@@ -536,7 +543,20 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   }
   __syncthreads(); /* the starts, the map, the cut group */
   const int g = settled1 || (settledk && !exact_grp) ? -1 : (int)misc[4]; /* -1: no group (cleared to ~0) */
-  if (exact_grp && g >= 0) pg0 = misc64[1];
+  /* the cut lies in groups [gl, g]: round 0 widens the range back to the
+   * group where the bands' keep end falls when the elements fit one wave
+   * (the bands straddling a group boundary would otherwise leave a cut
+   * before the group to round 1) */
+  int gl = g;
+  if (g >= 0) {
+    if (exact_grp) {
+      pg0 = misc64[1];
+    } else {
+      const uint32_t l = misc[5]; /* (~0: tkeep 0, no group) */
+      if (l < (uint32_t)g && bstart[g * PER + PER] - bstart[l * PER] <= (uint32_t)TF_CAP) gl = (int)l;
+    }
+  }
+  const uint64_t qg = gl < g ? misc64[1] : misc64[0]; /* Q before the range */
   uint32_t s0 = 0u;
   int klo, khi;
   if (settled1) {
@@ -544,7 +564,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   } else if (g < 0) {
     klo = khi = k; /* no rank certainly drops (when not settled: the last must certainly stay) */
   } else {
-    s0 = bstart[g * PER];
+    s0 = bstart[gl * PER];
     const uint32_t n = bstart[g * PER + PER] - s0;
     if (n > (uint32_t)TF_CAP) return TOPP_FULL; /* (after the barrier above) */
     klo = max((int)s0, 1); /* cut = max(r1, 1), r1 the group's first rank reaching tdrop */
@@ -558,7 +578,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   if (klo > 1) {
     float eh;
     if (g >= 0)
-      topp_ebounds<NBK>(g * PER - 1, rs, dmax, emin, eh); /* the ranks before the group */
+      topp_ebounds<NBK>(gl * PER - 1, rs, dmax, emin, eh); /* the ranks before the range */
     else
       topp_ebounds<NBK>(bstart[NBK] < (uint32_t)V ? NBK : NBK - 1, rs, dmax, emin, eh); /* every rank */
   }
@@ -637,7 +657,8 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     for (int j = 0; j < EPT; j++) {
       const int i = j * TBLOCK + tid;
       const int bb = topp_bucket_of<NBK>(x[j], m, scale);
-      const bool in = i < V && ((uint32_t)bb / PER == (uint32_t)g || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
+      const int gb = bb / PER;
+      const bool in = i < V && ((gb >= gl && gb <= g) || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
       gm |= (in ? 1u : 0u) << j;
     }
     int slot = wave_append_mask(gm, (int *)&misc[0]);
@@ -664,7 +685,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     mine = lane < (int)n2;
     mk = mine ? lkey[lane] : 0ull;
     const uint32_t mb = mine ? (uint32_t)lval[lane] : 0xffffffffu;
-    ing = mine && mb / PER == (uint32_t)g;
+    ing = mine && (int)(mb / PER) >= gl && (int)(mb / PER) <= g; /* (mb / PER < 2^28) */
     const uint64_t f = ing ? d3s_fix40_exp(key_x(mk) - m) : 0ull;
     int rho = 0;
     uint64_t inc = 0ull;
@@ -678,7 +699,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     r = mine ? (int)bstart[mb] + rho : 0x7fffffff;
     bool certain;
     if (g >= 0) {
-      const uint64_t q0 = misc64[0];
+      const uint64_t q0 = qg;
       qr = q0 + inc;
       /* the first rank reaching tdrop (the group's last does); rank 0 never drops */
       const int r1 = wave_min_i32(ing && qr >= tdrop ? r : 0x7fffffff);
@@ -712,7 +733,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       for (int j = 0; j < EPT; j++) {
         const int i = j * TBLOCK + tid;
         const int bb = topp_bucket_of<NBK>(x[j], m, scale);
-        if (i < V && bb < g * PER) part += d3s_fix40_exp(x[j] - lse);
+        if (i < V && bb < gl * PER) part += d3s_fix40_exp(x[j] - lse);
       }
       p0 = block_sum_u64(part, R);
     }
@@ -728,7 +749,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
        * p0 does already (then the full path) */
       const int re = wave_min_i32(ing && p0 + pinc >= Tq ? r : 0x7fffffff);
       cut = min(max(re, 1), k);
-      qlast = misc64[0];
+      qlast = qg;
       if (cut - 1 >= (int)s0) {
         const uint64_t at = __ballot(ing && r == cut - 1);
         const int src = (int)__builtin_ctzll(at | (1ull << 63));
@@ -1179,7 +1200,7 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
 #pragma unroll
     for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < 4) bstart[NBK + tid] = 0u;
-    if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = tid == 4 ? ~0u : 0u;
+    if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = tid == 4 || tid == 5 ? ~0u : 0u;
     ((uint64_t *)dyn)[tid] = 0ull;
     uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
     uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
