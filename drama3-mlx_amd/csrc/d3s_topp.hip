@@ -444,7 +444,7 @@ __device__ __forceinline__ int topp_bucket_of_rank(const uint32_t *bstart, int r
  * every return follows a barrier. */
 template <int EPT, int TBLOCK, int NBK>
 __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const float (&x)[EPT],
-                                             const float (&uv_in)[EPT], float m, float xmin, float scale, float top_p,
+                                             float m, float xmin, float scale, float top_p,
                                              uint32_t *bstart, char *dyn, TRed &R, const bool exact_grp) {
   constexpr int PER = NBK / TBLOCK;
   static_assert(PER % 4 == 0, "whole 16-byte groups of buckets per thread");
@@ -464,8 +464,8 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
   uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
   uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V)); /* bucket + 1 at each bucket's first rank */
-  const int RPT = (k + TBLOCK - 1) / TBLOCK; /* <= EPT */
-  const int r0 = tid * RPT;
+  /* thread t takes the uniforms of ranks q TBLOCK + t (q < EPT): read
+   * coalesced */
 
   /* ---- bucket starts, group prefixes and the row sum S, one scan */
   uint64_t gst, gs, S;
@@ -582,19 +582,21 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     else
       topp_ebounds<NBK>(bstart[NBK] < (uint32_t)V ? NBK : NBK - 1, rs, dmax, emin, eh); /* every rank */
   }
-  /* this thread's ranks' uniforms: in flight with the row in round 0, read
-   * here in round 1 (fewer registers live through its group sums) */
+  /* this thread's ranks' uniforms, read here (not with the row: fewer
+   * registers live through the counting; other workgroups hide the wait) */
   float uv[EPT];
 #pragma unroll
-  for (int q = 0; q < EPT; q++)
-    uv[q] = !exact_grp ? uv_in[q] : (q < RPT && r0 + q < k) ? a.u[(size_t)row * k + r0 + q] : 0.0f;
+  for (int q = 0; q < EPT; q++) {
+    const int r = q * TBLOCK + tid;
+    uv[q] = a.u[(size_t)row * k + (r < k ? r : k - 1)]; /* (r >= k: unused) */
+  }
   float hb0[EPT];
   float lbm = -1.0f;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
-    const int r = r0 + q;
+    const int r = q * TBLOCK + tid;
     hb0[q] = -__builtin_inff();
-    if (q < RPT && r < khi) {
+    if (r < khi) {
       float lb, h;
       topp_sbounds(emin, 1.0f, uv[q], lb, h);
       hb0[q] = h;
@@ -612,7 +614,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     for (int q = 0; q < EPT; q++)
       if ((pm >> q) & 1u) {
         if (slot < TF_CAP) {
-          rr[slot] = r0 + q;
+          rr[slot] = q * TBLOCK + tid;
           ru[slot] = uv[q];
         }
         slot++;
@@ -1210,18 +1212,15 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
     for (int w = tid; w < ((V + 7) & ~7) / 2; w += TBLOCK) rmap[w] = 0u;
   }
 
-  /* ---- 1. x (with T = 1, x = L: RN(L / 1) = L), max and least finite x;
-   * the uniforms of this thread's ranks in flight with the row */
-  float x[EPT], uv[EPT];
+  /* ---- 1. x (with T = 1, x = L: RN(L / 1) = L), max and least finite x */
+  float x[EPT];
   float xm = -__builtin_inff(), xl = __builtin_inff();
   {
-    const int RPT = (V + TBLOCK - 1) / TBLOCK, r0 = tid * RPT;
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
       const int i = j * TBLOCK + tid;
       const int ii = i < V ? i : V - 1;
       x[j] = BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[ii]) : ((const float *)rowp)[ii];
-      uv[j] = (!exact_grp && j < RPT && r0 + j < V) ? a.u[(size_t)row * V + r0 + j] : 0.0f; /* (round 1: later) */
     }
   }
   if (T == 1.0f) {
@@ -1261,7 +1260,7 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
       atomicAdd((unsigned long long *)&((uint64_t *)dyn)[(uint32_t)b / PER], (unsigned long long)f);
     }
     __syncthreads(); /* the counts and sums in (the row sum S is their total) */
-    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, uv, m, xmin, scale, rp.top_p, bstart, dyn, R, exact_grp);
+    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, m, xmin, scale, rp.top_p, bstart, dyn, R, exact_grp);
     if (id >= 0) {
       if (tid == 0) a.ids[row] = id;
       return true;
