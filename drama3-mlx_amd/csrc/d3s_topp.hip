@@ -1291,6 +1291,10 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) voi
     SampleArgs a, ToppRedo rd) {
   D3S_TOPP_SHARED
   const uint32_t n = __hip_atomic_load(rd.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  /* every workgroup reads the same count (nothing changes it before the
+   * last arrival below); none filed: the counts are zero already, and no
+   * workgroup arrives */
+  if (n == 0u) return;
 #pragma unroll 1
   for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
     const int row = rd.rows[i];
