@@ -188,7 +188,8 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   if (!no_alloc) return sample_routed(a, dt, (hipStream_t)stream);
   void *ws = nullptr;
   const size_t need = routed_workspace_bytes(a, dt);
-  if (need > 0) { /* the segmented kernel, or the sorting kernel one row at a time */
+  if (need > 0) { /* the segmented kernel, the sorting kernel one row at a time, or the nucleus
+                     ids path's filed rows (more rows than the scratch lists: the full path) */
     if (d3s::split_segments(a, dt) > 0 && need > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
     ws = device_scratch();
     if (!ws) return D3S_ERR_LAUNCH;
