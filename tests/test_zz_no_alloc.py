@@ -1,8 +1,9 @@
 """d3s_sample_noalloc (the entry point that allocates nothing: its scratch is
 one fixed block of static device memory per GPU) against d3s_sample, through
 the C-ABI, on two calls in a row, the second with a smaller input: rows the
-segmented kernel spreads over several CUs (the calls that use the scratch),
-then one-wave rows (no scratch); every id, probability and candidate equal."""
+segmented kernel spreads over several CUs and the nucleus kernel's ids-only
+rows (the calls that use the scratch), then one-wave rows (no scratch); every
+id, probability and candidate equal."""
 import numpy as np
 import pytest
 
@@ -21,21 +22,27 @@ def gpu():
     return d3s
 
 
-def run(gpu, fn, x, u, T, top_p, k):
+def run(gpu, fn, x, u, T, top_p, k, banned=None, want_probs=True):
     """one call of fn (d3s_sample or d3s_sample_noalloc) on device copies"""
     import hiprt
     N, V = x.shape
     dt = gpu.DTYPE_BF16 if x.dtype == np.uint16 else gpu.DTYPE_F32
     bl, bu = hiprt.to_device(x), hiprt.to_device(u)
-    ids, probs, cand = hiprt.DeviceBuffer(4 * N), hiprt.DeviceBuffer(4 * N * k), hiprt.DeviceBuffer(4 * N * k)
+    bb = hiprt.to_device(banned) if banned is not None else None
+    ids = hiprt.DeviceBuffer(4 * N)
+    probs = hiprt.DeviceBuffer(4 * N * k) if want_probs else None
+    cand = hiprt.DeviceBuffer(4 * N * k) if want_probs else None
     cnt = hiprt.DeviceBuffer(16).zero()
-    rc = fn(bl.ptr, dt, N, V, V, bu.ptr, k, None, None, T, top_p, None, ids.ptr, probs.ptr, cand.ptr,
-            cnt.ptr, 0, None)
+    rc = fn(bl.ptr, dt, N, V, V, bu.ptr, k, None, None, T, top_p, bb.ptr if bb else None, ids.ptr,
+            probs.ptr if probs else None, cand.ptr if cand else None, cnt.ptr, 0, None)
     assert rc == 0, rc
     hiprt.synchronize()
-    out = (ids.download((N,), np.int32), probs.download((N, k), np.float32), cand.download((N, k), np.int32))
-    for b in (bl, bu, ids, probs, cand, cnt):
-        b.free()
+    out = (ids.download((N,), np.int32),)
+    if want_probs:
+        out += (probs.download((N, k), np.float32), cand.download((N, k), np.int32))
+    for b in (bl, bu, bb, ids, probs, cand, cnt):
+        if b is not None:
+            b.free()
     return out
 
 
@@ -58,6 +65,26 @@ def test_no_alloc_equals_sample_twice(gpu, oracle, case):
         for p, q in zip(a, b):
             assert np.array_equal(p, q)
         assert np.array_equal(b[0], oracle.sample(x, u, T, top_p, n_threads=8)["ids"])
+
+
+def test_no_alloc_nucleus_ids_only(gpu, oracle):
+    """k = V, ids only: the nucleus kernel's ids path files the rows it cannot
+    settle in the scratch (rows of one value, heavy ties) for its second
+    kernel; two calls, the second smaller."""
+    L = gpu.lib()
+    w = W.make("C5", rows=256, seed=73, uniforms=False)
+    big, ban = w["logits"].copy(), w["banned"]
+    big[3, :] = 0.5                      # one value: the full path
+    big[7, :] = np.round(big[7] * 2)     # a few values, heavy ties
+    big[11, :] = np.round(big[11] * 8)
+    for n in (256, 13):  # two calls in a row, the second smaller
+        x, b_ = big[:n], ban[:n]
+        u = oracle.uniform(73, n, n, x.shape[1])
+        a = run(gpu, L.d3s_sample, x, u, 1.0, 0.95, x.shape[1], banned=b_, want_probs=False)
+        b = run(gpu, L.d3s_sample_noalloc, x, u, 1.0, 0.95, x.shape[1], banned=b_, want_probs=False)
+        print(f"[no-alloc] nucleus ids only rows={n}", flush=True)
+        assert np.array_equal(a[0], b[0])
+        assert np.array_equal(b[0], oracle.sample(x, u, 1.0, 0.95, banned=b_, n_threads=8)["ids"])
 
 
 def test_no_alloc_one_wave_rows(gpu, oracle):
