@@ -668,7 +668,37 @@ def cpu_baseline(seconds):
     return dict(value=n * ROWS / dt, unit="rows/s", cores=int(threads), kind="port",
                 sample=f"{n} batches x {ROWS} rows of C3 (fp32 [256,4097], k=30), C oracle "
                        f"({flags}, OpenMP over rows, ids only) on {threads} threads, {dt:.1f} s",
-                cpu_model=cpu_model(), c1_row_us_1_thread=c1_us)
+                cpu_model=cpu_model(), c1_row_us_1_thread=c1_us,
+                configs=cpu_configs(threads))
+
+
+def cpu_configs(threads, min_seconds=0.5):
+    """The oracle on every configuration at its own shape: rows/s on one
+    thread and on `threads` (C2: the nine rows; C4 and C5: their full row
+    counts), each timed over repeated calls for at least `min_seconds`."""
+    import d3s_oracle
+    import d3s_workloads as W
+    out = {}
+    for name in ("C2", "C3", "C4", "C5"):
+        w = W.make(name, seed=9, uniforms=False)
+        x = w["logits"]
+        N = x.shape[0]
+        u = d3s_oracle.uniform(42, 2, N, w["k"])
+        rates = {}
+        for nt in (1, threads):
+            rows_timed, t0 = 0, time.perf_counter()
+            while True:
+                d3s_oracle.sample(x, u, w["temperature"], w["top_p"], banned=w["banned"], n_threads=nt,
+                                  detail=False)
+                rows_timed += N
+                dt = time.perf_counter() - t0
+                if dt >= min_seconds:
+                    break
+            rates[nt] = rows_timed / dt
+        out[name] = {"rows": N, "vocab": int(x.shape[1]), "k": int(w["k"]),
+                     "rows_per_s_1_thread": rates[1], f"rows_per_s_{threads}_threads": rates[threads],
+                     "us_per_row_1_thread": 1e6 / rates[1]}
+    return out
 
 
 def main():

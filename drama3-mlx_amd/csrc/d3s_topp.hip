@@ -1299,7 +1299,9 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) voi
   for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
     const int row = rd.rows[i];
     __syncthreads(); /* the previous row's LDS reads done */
-    if (!topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, true)) {
+    /* (1024-thread workgroups: the full path alone; with round 1 beside it
+     * the loop would need scratch at four waves per SIMD) */
+    if (TBLOCK > 512 || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, true)) {
       __syncthreads();
       topp_full_row<EPT, BF16, TBLOCK, NBK>(a, row, keys, bstart, R);
     }
