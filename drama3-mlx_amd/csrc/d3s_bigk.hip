@@ -1,27 +1,36 @@
-/* k_bigk: the op graph's sampler for k beyond the generic kernel's LDS sort
- * (k > 16384, on rows longer than the nucleus kernel takes), gfx950 wave64.
+/* The sorting path: the op graph's sampler for k beyond the generic
+ * kernel's LDS sort (k > 16384, on rows longer than the nucleus kernel
+ * takes), gfx950 wave64.
  *
  * The reference's op graph (src/sampling.c:22-49) takes any k up to V: with
- * top-k disabled it argsorts the whole row (:33-35).  One 1024-thread
- * workgroup per row:
- *  1. x = L / T, classification and max (refused / all -inf rows as every
- *     kernel treats them);
- *  2. the exact row sum (2^-40 fixed point of d3s_expf(x - m)), and the row's
- *     composite keys (ordkey(x), ~index) written to the workspace in index
- *     order, with the first pass's digit counts;
- *  3. a stable LSD radix sort of the keys by ordkey(x) descending, four 8-bit
- *     passes between two workspace buffers, in tiles of 1024 keys in index
- *     order: a wave's peers of a digit by eight ballots, per-wave digit counts
- *     in LDS turned into places by one thread per digit, two barriers a tile
- *     (ordering LDS only; each tile's keys load during the tile before), and
- *     the next pass's digit counts taken on the way.  Stability keeps equal x
- *     in index order, so the result is the order (x desc, index asc) of every
- *     kernel;
- *  4. the op graph's tail over the first k ranks (bigk_tail: the generic
- *     kernel's definition with coalesced reads: exact prefix sums chunk by
- *     chunk to the cut, the kept sum, probabilities and the race).
+ * top-k disabled it argsorts the whole row (:33-35).  Each row is cut into
+ * up to 16 segments of whole 1024-key tiles, so a launch of few rows still
+ * spreads over the CUs; six launches, 1024 threads a workgroup:
+ *  k_bk_keys (a workgroup per segment): x = L / T, classification and the
+ *     segment's max; the composite keys (ordkey(x), ~index) written to the
+ *     workspace in index order, with the segment's digit counts for the first
+ *     radix pass;
+ *  k_bk_pass, four times (a workgroup per segment): one pass of a stable LSD
+ *     radix sort by ordkey(x) descending (8-bit digits, between two buffers).
+ *     The segment's first place for digit d is the row's keys of smaller
+ *     digits plus the earlier segments' keys of digit d (every segment's
+ *     counts, from the pass before); within the segment, tiles of 1024 keys
+ *     in order: a wave's peers of a digit by eight ballots, per-wave digit
+ *     counts in LDS turned into places by one thread per digit, two barriers
+ *     a tile (ordering LDS only; each tile's keys load during the tile
+ *     before).  Each key's place gives the segment it lands in for the next
+ *     pass: the next pass's counts per (segment, digit), gathered in LDS and
+ *     added to the workspace's table once per workgroup.  The first pass also
+ *     takes the segment's exact sum (2^-40 fixed point of d3s_expf(x - m), m
+ *     the row's max from every segment's).  Stability keeps equal x in index
+ *     order, so the result is the order (x desc, index asc) of every kernel;
+ *  the tail, over the first k ranks cut into the same segments (k_bk_sums,
+ *     k_bk_cut, k_bk_race, k_bk_pick below): refused and all -inf rows as
+ *     every kernel treats them; else the generic kernel's definition: the
+ *     exact prefix sums to the cut, the kept sum, probabilities and the race.
  * The same definition as the generic and nucleus kernels, bit for bit.  The
- * workspace holds two buffers of the row's keys (16 bytes per element). */
+ * workspace holds, per row, two buffers of the row's keys (16 bytes per
+ * element), the four passes' count tables and the segments' records. */
 #include "d3s_generic.h"
 
 #pragma clang fp contract(off)
@@ -60,6 +69,10 @@ __device__ __forceinline__ uint64_t wave_peers(uint32_t d, uint64_t live) {
   return peers;
 }
 
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return ((uint64_t)readlane_u((uint32_t)(v >> 32), l) << 32) | readlane_u((uint32_t)v, l);
+}
+
 constexpr int BK_CH = 4096; /* ranks of the cut's exact scan, staged in LDS */
 
 /* block sum of per-thread fixed-point values (below 2^56 in total); opens
@@ -78,83 +91,464 @@ __device__ __forceinline__ uint64_t bk_block_sum(uint64_t v, uint32_t *lo, uint3
   return t;
 }
 
+constexpr int BK_SMAX = 16; /* segments per row (at most) */
+constexpr int BK_B = 8;     /* loads a thread keeps in flight in the streaming loops */
+constexpr int BK_PF = 4;    /* tiles of keys a pass keeps in flight (even) */
+constexpr int BK_WGS = 512; /* workgroups a launch aims at: two per CU */
+
+/* a segment's record: its max and refusal flag (k_bk_keys), its exact sum
+ * (the first pass); then, for the segment's ranks [s L, s L + L) after the
+ * sort, the sums of their terms fix40(d3s_expf(x_r - lse)) and
+ * fix40(d3s_expf(x_r - x_0)) (k_bk_sums) and their race's first maximum
+ * (k_bk_race); segment 0's record also holds the row's cut and 1 / kept sum
+ * (k_bk_cut) */
+struct __align__(16) BkMeta {
+  float max;
+  uint32_t flags;
+  uint64_t sum;
+  uint64_t psum, ksum;
+  float best;
+  int bestr;
+  int cut;
+  float inv;
+};
+
+/* a launch's rows in the workspace: the rows' key buffers, then their count
+ * tables ([row][pass][segment][digit]), then their segments' records */
+struct BkLayout {
+  uint64_t *keys; /* [n][2][vstride] */
+  uint32_t *hist; /* [n][4][BK_SMAX][NB] */
+  BkMeta *meta;   /* [n][BK_SMAX] */
+  int64_t vstride;
+  int nseg, tps;  /* segments per row, tiles per segment */
+  float inv_sl;   /* 1 / (tps BK_T), rounded */
+};
+
+/* the segment holding position pos: pos / (tps BK_T), from a float
+ * estimate within one of it (pos < 2^26 and the segment length are exact
+ * in fp32; the product's relative error is below 2^-23) */
+__device__ __forceinline__ uint32_t bk_seg_of(uint32_t pos, const BkLayout &L) {
+  const uint32_t sl = (uint32_t)(L.tps * BK_T);
+  uint32_t q = (uint32_t)((float)pos * L.inv_sl);
+  q = q * sl > pos ? q - 1u : q;
+  q = (q + 1u) * sl <= pos ? q + 1u : q;
+  return q;
+}
+
+/* the row's max and refusal flag from its segments' records (every wave
+ * alike: lane s reads segment s, all in one round of loads); with S, also
+ * the row's exact sum (the first pass's) */
+__device__ __forceinline__ void bk_row_max(const BkLayout &L, int row, float &M, uint32_t &F, uint64_t *S = nullptr) {
+  const int lane = lane_id();
+  const BkMeta *mt = L.meta + (size_t)row * BK_SMAX;
+  float m = -__builtin_inff();
+  uint32_t f = 0u;
+  uint64_t sm = 0ull;
+  if (lane < L.nseg) {
+    m = mt[lane].max;
+    f = mt[lane].flags;
+    if (S) sm = mt[lane].sum;
+  }
+  M = wave_max_f(m);
+  F = __ballot(f & 1u) ? 1u : 0u;
+  if (S) {
+    uint64_t t = 0ull;
+    for (int s2 = 0; s2 < L.nseg; s2++) t += readlane_u64(sm, s2);
+    *S = t;
+  }
+}
+
+/* k_bk_keys: a segment's keys in index order, its max and flags, its digit
+ * counts for the first pass; the later passes' counts of the segment zeroed
+ * (they are added to by the pass before each) */
+template <bool BF16>
+__global__ __launch_bounds__(BK_T) void k_bk_keys(SampleArgs a, BkLayout L) {
+  __shared__ uint32_t hist[NB];
+  __shared__ float sh_max[BK_NW];
+  __shared__ uint32_t sh_flag[BK_NW];
+  const int seg = (int)blockIdx.x, row = (int)blockIdx.y;
+  const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int V = a.vocab;
+  const int lo = seg * L.tps * BK_T, hi = min(V, lo + L.tps * BK_T);
+  const RowP rp = row_params(a, row);
+  const float T = rp.T;
+  const bool t_finite = T < __builtin_inff();
+  const float y = 1.0f / T;
+  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
+  uint64_t *buf0 = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  if (tid < NB) hist[tid] = 0u;
+  __syncthreads();
+  float xm = -__builtin_inff();
+  uint32_t fl = 0u;
+#pragma unroll 1
+  for (int i0 = lo + tid; i0 < hi; i0 += BK_B * BK_T) { /* BK_B loads in flight, then their work */
+    float v[BK_B];
+#pragma unroll
+    for (int q = 0; q < BK_B; q++) {
+      const int i = i0 + q * BK_T;
+      v[q] = i < hi ? load_logit<BF16>(rowp, i, rp.banned) : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < BK_B; q++) {
+      const int i = i0 + q * BK_T;
+      if (i < hi) {
+        const float xi = scale_logit(v[q], T, y, t_finite);
+        const uint32_t c = classify(xi);
+        fl |= c;
+        if (!(c & 1u)) xm = fmaxf(xm, xi);
+        const uint64_t key = composite_key(xi, i);
+        buf0[i] = key;
+        atomicAdd(&hist[bk_digit(key, 0)], 1u);
+      }
+    }
+  }
+  xm = wave_max_f(xm);
+  const uint32_t wf = __ballot(fl & 1u) ? 1u : 0u;
+  if (lane == 0) {
+    sh_max[wid] = xm;
+    sh_flag[wid] = wf;
+  }
+  __syncthreads();
+  uint32_t *gh = L.hist + (size_t)row * 4 * BK_SMAX * NB;
+  if (tid < NB) {
+    gh[seg * NB + tid] = hist[tid];
+#pragma unroll
+    for (int p = 1; p < 4; p++) gh[(p * BK_SMAX + seg) * NB + tid] = 0u;
+  }
+  if (tid == 0) {
+    float M = sh_max[0];
+    uint32_t F = sh_flag[0];
+    for (int w = 1; w < BK_NW; w++) {
+      M = fmaxf(M, sh_max[w]);
+      F |= sh_flag[w];
+    }
+    BkMeta m;
+    m.max = M;
+    m.flags = F;
+    m.sum = 0ull;
+    L.meta[(size_t)row * BK_SMAX + seg] = m;
+  }
+}
+
+/* k_bk_pass: one radix pass of a segment (the layout above); refused and all
+ * -inf rows are left to the tail */
+__global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int pass) {
+  __shared__ uint32_t base[NB];            /* a digit's next place */
+  __shared__ uint32_t tot[NB];             /* the row's keys of each digit */
+  __shared__ uint32_t wcnt[2][BK_NW][NB];  /* a tile's count of each digit in each wave, then its place */
+  __shared__ uint32_t nxt[BK_SMAX * NB];   /* the next pass's counts by (segment, digit) */
+  __shared__ uint32_t sh_lo[BK_NW], sh_hi[BK_NW];
+  const int seg = (int)blockIdx.x, row = (int)blockIdx.y;
+  const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int V = a.vocab;
+  const int lo = seg * L.tps * BK_T, hi = min(V, lo + L.tps * BK_T);
+  float M;
+  uint32_t F;
+  bk_row_max(L, row, M, F);
+  if ((F & 1u) || M == -__builtin_inff()) return; /* (every workgroup of the row alike) */
+  uint64_t *buf = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  const uint64_t *src = buf + (pass & 1) * L.vstride;
+  uint64_t *dst = buf + ((pass & 1) ^ 1) * L.vstride;
+  uint32_t *gh = L.hist + (size_t)row * 4 * BK_SMAX * NB;
+  const uint32_t *cnt = gh + (size_t)pass * BK_SMAX * NB;
+
+  /* the segment's first place of each digit: the row's keys of smaller
+   * digits plus the earlier segments' of this digit */
+  if (tid < NB) {
+    uint32_t c[BK_SMAX];
+#pragma unroll
+    for (int s2 = 0; s2 < BK_SMAX; s2++) c[s2] = s2 < L.nseg ? cnt[s2 * NB + tid] : 0u; /* one round of loads */
+    uint32_t t = 0u, pre = 0u;
+#pragma unroll
+    for (int s2 = 0; s2 < BK_SMAX; s2++) {
+      pre += s2 < seg ? c[s2] : 0u;
+      t += c[s2];
+    }
+    tot[tid] = t;
+    base[tid] = pre;
+  }
+  for (int j = tid; j < 2 * BK_NW * NB; j += BK_T) (&wcnt[0][0][0])[j] = 0u;
+  if (pass < 3)
+    for (int j = tid; j < L.nseg * NB; j += BK_T) nxt[j] = 0u;
+  __syncthreads();
+  if (wid == 0) { /* the digits' starts, four per lane */
+    uint32_t h[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) h[q] = tot[4 * lane + q];
+    const uint32_t ls = h[0] + h[1] + h[2] + h[3];
+    uint32_t run = wave_scan_add_u32(ls) - ls;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      base[4 * lane + q] += run;
+      run += h[q];
+    }
+  }
+  __syncthreads();
+
+  /* the segment's tiles in order: two count buffers alternate between
+   * tiles, each cleared a tile after its last read; each thread's keys of
+   * the next BK_PF tiles in flight (a workgroup keeps BK_PF tiles of reads
+   * outstanding: the pass is bound by that latency, not by its work) */
+  const uint64_t lt = (1ull << lane) - 1ull;
+  uint64_t acc = 0ull; /* the first pass: the segment's exact sum */
+  uint64_t pf[BK_PF];
+#pragma unroll
+  for (int q = 0; q < BK_PF; q++) pf[q] = lo + q * BK_T + tid < hi ? src[lo + q * BK_T + tid] : 0ull;
+#pragma unroll 1
+  for (int g0 = lo; g0 < hi; g0 += BK_PF * BK_T) {
+#pragma unroll
+    for (int q = 0; q < BK_PF; q++) {
+      const int t0 = g0 + q * BK_T;
+      if (t0 >= hi) break; /* (uniform) */
+      const int par = q & 1; /* (BK_PF even: tiles alternate) */
+      const int i = t0 + tid;
+      const bool valid = i < hi;
+      const uint64_t key = pf[q];
+      const int ip = i + BK_PF * BK_T;
+      pf[q] = ip < hi ? src[ip] : 0ull;
+      const uint64_t live = __ballot(valid);
+      const uint32_t d = bk_digit(key, pass);
+      const uint64_t peers = wave_peers<8>(d, live);
+      const uint32_t below = (uint32_t)__popcll(peers & lt);
+      if (valid && below == 0u) wcnt[par][wid][d] = (uint32_t)__popcll(peers);
+      if (pass == 0 && valid) acc += d3s_fix40_exp(key_x(key) - M); /* (x <= m) */
+      lds_barrier();
+      if (tid < NB) {
+        uint32_t run = base[tid];
+#pragma unroll
+        for (int w = 0; w < BK_NW; w++) {
+          const uint32_t c = wcnt[par][w][tid];
+          wcnt[par][w][tid] = run;
+          wcnt[par ^ 1][w][tid] = 0u; /* last read a tile ago */
+          run += c;
+        }
+        base[tid] = run;
+      }
+      lds_barrier();
+      if (valid) {
+        const uint32_t pos = wcnt[par][wid][d] + below;
+        dst[pos] = key;
+        if (pass < 3) { /* the segment the key lands in, for the next pass */
+          const uint32_t ds = bk_seg_of(pos, L);
+          atomicAdd(&nxt[ds * NB + bk_digit(key, pass + 1)], 1u);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (pass < 3) {
+    uint32_t *gn = gh + (size_t)(pass + 1) * BK_SMAX * NB;
+    for (int j = tid; j < L.nseg * NB; j += BK_T) {
+      const uint32_t c = nxt[j];
+      if (c) atomicAdd(&gn[j], c);
+    }
+  }
+  if (pass == 0) {
+    const uint64_t S = bk_block_sum(acc, sh_lo, sh_hi);
+    if (tid == 0) L.meta[(size_t)row * BK_SMAX + seg].sum = S;
+  }
+}
+
+/* the row's lse (and the refusal or all -inf decision) from its segments'
+ * records; false for a row the tail leaves to k_bk_cut's special result */
+__device__ __forceinline__ bool bk_row_lse(const BkLayout &L, int row, float &lse) {
+  float M;
+  uint32_t F;
+  uint64_t S;
+  bk_row_max(L, row, M, F, &S);
+  if ((F & 1u) || M == -__builtin_inff()) return false;
+  lse = M + d3s_logf(d3s_fixsum_to_f32(S));
+  return true;
+}
+
 /* The op graph's tail (generic_tail_opgraph's definition, bit for bit) over
- * the k ranked keys in global memory, with coalesced reads: the exact prefix
- * sums of fix40(d3s_expf(x_r - lse)) are taken chunk by chunk (interleaved
- * per-thread sums: integers, so the order does not matter) until a chunk's
- * end passes top_p; that chunk is staged in LDS and scanned rank by rank for
- * the cut.  The kept sum, the probabilities and the race run over the ranks
- * interleaved across the threads (the race's first maximum: the largest
- * score, ties to the smaller rank). */
-__device__ __forceinline__ void bigk_tail(const SampleArgs &a, const int row, const float lse, const float top_p,
-                                          const uint64_t *glist, uint64_t *lch, uint32_t *sh_lo, uint32_t *sh_hi,
-                                          uint32_t *sh_u32, float *sh_best, int *sh_bestr) {
+ * the first k ranks, the ranks cut into the sort's segments:
+ *  k_bk_sums (a workgroup per segment): the segment's sums of the exact
+ *    prefix terms fix40(d3s_expf(x_r - lse)) and of the kept-sum terms
+ *    fix40(d3s_expf(x_r - x_0)) (integers: any order);
+ *  k_bk_cut (a workgroup per row): the cut, the first r > 0 whose exact
+ *    prefix passes top_p: the first segment whose end passes it, then that
+ *    segment chunk by chunk and the passing chunk rank by rank; the kept sum
+ *    (the earlier segments' sums plus the cut segment's ranks below the cut);
+ *  k_bk_race (a workgroup per segment): probabilities, candidates and each
+ *    segment's race (the first maximum: the largest score, ties to the
+ *    smaller rank);
+ *  k_bk_pick (a wave per row): the segments' maxima, the first one. */
+__global__ __launch_bounds__(BK_T) void k_bk_sums(SampleArgs a, BkLayout L) {
+  __shared__ uint32_t sh_lo[BK_NW], sh_hi[BK_NW];
+  const int seg = (int)blockIdx.x, row = (int)blockIdx.y, tid = (int)threadIdx.x;
+  float lse;
+  if (!bk_row_lse(L, row, lse)) return;
+  const uint64_t *glist = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  const float v0 = key_x(glist[0]);
+  const int lo = seg * L.tps * BK_T, hi = min(a.k, lo + L.tps * BK_T);
+  uint64_t ps = 0ull, ks = 0ull;
+#pragma unroll 1
+  for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
+    uint64_t kv[BK_B];
+#pragma unroll
+    for (int q = 0; q < BK_B; q++) kv[q] = r0 + q * BK_T < hi ? glist[r0 + q * BK_T] : 0ull;
+#pragma unroll
+    for (int q = 0; q < BK_B; q++)
+      if (r0 + q * BK_T < hi) {
+        const float x = key_x(kv[q]);
+        ps += d3s_fix40_exp(x - lse); /* (x <= x_0 <= lse) */
+        ks += d3s_fix40_exp(x - v0);
+      }
+  }
+  ps = bk_block_sum(ps, sh_lo, sh_hi);
+  ks = bk_block_sum(ks, sh_lo, sh_hi);
+  if (tid == 0) {
+    L.meta[(size_t)row * BK_SMAX + seg].psum = ps;
+    L.meta[(size_t)row * BK_SMAX + seg].ksum = ks;
+  }
+}
+
+__global__ __launch_bounds__(BK_T) void k_bk_cut(SampleArgs a, BkLayout L) {
+  __shared__ uint64_t lch[BK_CH]; /* the cut's chunk */
+  __shared__ uint32_t sh_lo[BK_NW], sh_hi[BK_NW], sh_u32[BK_NW];
+  const int row = (int)blockIdx.x, tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
+  const int k = a.k;
+  float lse;
+  if (!bk_row_lse(L, row, lse)) {
+    float M;
+    uint32_t F;
+    bk_row_max(L, row, M, F);
+    write_special(a, row, !(F & 1u));
+    return;
+  }
+  const RowP rp = row_params(a, row);
+  const float top_p = rp.top_p;
+  const uint64_t *glist = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  BkMeta *mt = L.meta + (size_t)row * BK_SMAX;
+  const float v0 = key_x(glist[0]);
+  const int SL = L.tps * BK_T;
+  const int nrs = (k + SL - 1) / SL; /* segments holding ranks below k */
+  /* the first segment whose end passes top_p (its prefix before: base);
+   * lane s holds segment s's sums */
+  uint64_t lp = 0ull, lk = 0ull;
+  if (lane < nrs) {
+    lp = mt[lane].psum;
+    lk = mt[lane].ksum;
+  }
+  uint64_t base = 0ull, kept = 0ull;
+  int c = nrs;
+  for (int s2 = 0; s2 < nrs; s2++) {
+    const uint64_t P = base + readlane_u64(lp, s2);
+    if (d3s_fixsum_to_f32(P) > top_p) {
+      c = s2;
+      break;
+    }
+    base = P;
+    kept += readlane_u64(lk, s2);
+  }
+  int cut = k;
+  if (c < nrs) {
+    /* the cut lies in segment c (a pass at rank 0 alone is no cut: the
+     * segment's later ranks pass too, and the first of them is) */
+    const int lo = c * SL, hi = min(k, lo + SL);
+#pragma unroll 1
+    for (int r_lo = lo; r_lo < hi; r_lo += BK_CH) {
+      const int r_hi = min(hi, r_lo + BK_CH);
+      uint64_t loc = 0;
+#pragma unroll 4
+      for (int r = r_lo + tid; r < r_hi; r += BK_T) loc += d3s_fix40_exp(key_x(glist[r]) - lse);
+      const uint64_t tot = bk_block_sum(loc, sh_lo, sh_hi);
+      if (!(r_hi > 1 && d3s_fixsum_to_f32(base + tot) > top_p)) {
+        base += tot;
+        continue;
+      }
+      /* this chunk: its keys to LDS, each thread a run of BK_CH / BK_T
+       * consecutive ranks */
+      for (int r = r_lo + tid; r < r_hi; r += BK_T) lch[r - r_lo] = glist[r];
+      __syncthreads();
+      constexpr int RUN = BK_CH / BK_T;
+      uint64_t f[RUN];
+      uint64_t part = 0;
+#pragma unroll
+      for (int q = 0; q < RUN; q++) {
+        const int r = r_lo + tid * RUN + q;
+        f[q] = r < r_hi ? d3s_fix40_exp(key_x(lch[tid * RUN + q]) - lse) : 0ull;
+        part += f[q];
+      }
+      uint64_t P = base + block_excl_scan_u64<BK_NW>(part, sh_lo, sh_hi);
+      int cl = k;
+#pragma unroll
+      for (int q = 0; q < RUN; q++) {
+        const int r = r_lo + tid * RUN + q;
+        P += f[q];
+        if (r < r_hi && r > 0 && cl == k && d3s_fixsum_to_f32(P) > top_p) cl = r;
+      }
+      const int cm = wave_min_i32(cl);
+      if (lane == 0) sh_u32[wid] = (uint32_t)cm;
+      __syncthreads();
+      for (int w = 0; w < BK_NW; w++) cut = min(cut, (int)sh_u32[w]);
+      break;
+    }
+    /* the kept sum: the segments before c and segment c's ranks below the cut */
+    uint64_t ks = 0ull;
+#pragma unroll 1
+    for (int r0 = lo + tid; r0 < cut; r0 += BK_B * BK_T) {
+      uint64_t kv[BK_B];
+#pragma unroll
+      for (int q = 0; q < BK_B; q++) kv[q] = r0 + q * BK_T < cut ? glist[r0 + q * BK_T] : 0ull;
+#pragma unroll
+      for (int q = 0; q < BK_B; q++)
+        if (r0 + q * BK_T < cut) ks += d3s_fix40_exp(key_x(kv[q]) - v0);
+    }
+    kept += bk_block_sum(ks, sh_lo, sh_hi);
+  }
+  if (tid == 0) {
+    mt[0].cut = cut;
+    mt[0].inv = 1.0f / d3s_fixsum_to_f32(kept);
+  }
+}
+
+__global__ __launch_bounds__(BK_T) void k_bk_race(SampleArgs a, BkLayout L) {
+  __shared__ float sh_best[BK_NW];
+  __shared__ int sh_bestr[BK_NW];
+  const int seg = (int)blockIdx.x, row = (int)blockIdx.y;
   const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
   const int k = a.k;
+  float lse;
+  if (!bk_row_lse(L, row, lse)) return;
+  const uint64_t *glist = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  BkMeta *mt = L.meta + (size_t)row * BK_SMAX;
+  const int lo = seg * L.tps * BK_T, hi = min(k, lo + L.tps * BK_T);
+  if (lo >= hi) return;
+  const int cut = mt[0].cut;
+  const float inv = mt[0].inv;
   const float v0 = key_x(glist[0]);
-  /* ---- the cut: the first r > 0 whose exact prefix passes top_p */
-  int cut = k;
-  uint64_t base = 0;
-#pragma unroll 1
-  for (int r_lo = 0; r_lo < k; r_lo += BK_CH) {
-    const int r_hi = min(k, r_lo + BK_CH);
-    uint64_t loc = 0;
-#pragma unroll 4
-    for (int r = r_lo + tid; r < r_hi; r += BK_T) loc += d3s_fix40(d3s_expf(key_x(glist[r]) - lse));
-    const uint64_t tot = bk_block_sum(loc, sh_lo, sh_hi);
-    if (!(r_hi > 1 && d3s_fixsum_to_f32(base + tot) > top_p)) {
-      base += tot;
-      continue;
-    }
-    /* the cut lies in this chunk: its keys to LDS, each thread a run of
-     * BK_CH / BK_T consecutive ranks */
-    for (int r = r_lo + tid; r < r_hi; r += BK_T) lch[r - r_lo] = glist[r];
-    __syncthreads();
-    constexpr int RUN = BK_CH / BK_T;
-    uint64_t f[RUN];
-    uint64_t part = 0;
-#pragma unroll
-    for (int q = 0; q < RUN; q++) {
-      const int r = r_lo + tid * RUN + q;
-      f[q] = r < r_hi ? d3s_fix40(d3s_expf(key_x(lch[tid * RUN + q]) - lse)) : 0ull;
-      part += f[q];
-    }
-    uint64_t P = base + block_excl_scan_u64<BK_NW>(part, sh_lo, sh_hi);
-    int cl = k;
-#pragma unroll
-    for (int q = 0; q < RUN; q++) {
-      const int r = r_lo + tid * RUN + q;
-      P += f[q];
-      if (r < r_hi && r > 0 && cl == k && d3s_fixsum_to_f32(P) > top_p) cl = r;
-    }
-    const int cm = wave_min_i32(cl);
-    if (lane == 0) sh_u32[wid] = (uint32_t)cm;
-    __syncthreads();
-    for (int w = 0; w < BK_NW; w++) cut = min(cut, (int)sh_u32[w]);
-    break;
-  }
-  /* ---- the kept sum of fix40(d3s_expf(x_r - x_0)) over r < cut */
-  uint64_t ks = 0;
-#pragma unroll 4
-  for (int r = tid; r < cut; r += BK_T) ks += d3s_fix40(d3s_expf(key_x(glist[r]) - v0));
-  const float inv = 1.0f / d3s_fixsum_to_f32(bk_block_sum(ks, sh_lo, sh_hi));
-  /* ---- probabilities, candidates and the race over every rank */
   float bs = -1.0f;
   int br = 0x7fffffff;
   const float *urow = a.u + (size_t)row * k;
-#pragma unroll 2
-  for (int r = tid; r < k; r += BK_T) {
-    const uint64_t key = glist[r];
-    const float p = r < cut ? d3s_expf(key_x(key) - v0) * inv : 0.0f;
-    const float noise = -d3s_logf(1.0f - urow[r]);
-    const float score = p / noise;
-    const float sc = score > -1.0f ? score : -1.0f;
-    if (sc > bs || br == 0x7fffffff) { /* this thread's ranks increase: its first maximum */
-      bs = sc;
-      br = r;
+#pragma unroll 1
+  for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
+    uint64_t kv[BK_B];
+    float uu[BK_B];
+#pragma unroll
+    for (int q = 0; q < BK_B; q++) {
+      const int r = r0 + q * BK_T;
+      kv[q] = r < hi ? glist[r] : 0ull;
+      uu[q] = r < hi ? urow[r] : 0.0f;
     }
-    if (a.probs) a.probs[(size_t)row * k + r] = p;
-    if (a.cand) a.cand[(size_t)row * k + r] = key_idx(key);
+#pragma unroll
+    for (int q = 0; q < BK_B; q++) {
+      const int r = r0 + q * BK_T;
+      if (r < hi) {
+        const uint64_t key = kv[q];
+        const float p = r < cut ? d3s_expf_nonpos(key_x(key) - v0) * inv : 0.0f;
+        const float noise = -d3s_logf(1.0f - uu[q]);
+        const float score = p / noise;
+        const float sc = score > -1.0f ? score : -1.0f;
+        if (sc > bs || br == 0x7fffffff) { /* this thread's ranks increase: its first maximum */
+          bs = sc;
+          br = r;
+        }
+        if (a.probs) a.probs[(size_t)row * k + r] = p;
+        if (a.cand) a.cand[(size_t)row * k + r] = key_idx(key);
+      }
+    }
   }
   wave_argmax(bs, br);
   if (lane == 0) {
@@ -170,157 +564,26 @@ __device__ __forceinline__ void bigk_tail(const SampleArgs &a, const int row, co
         b = sh_best[w];
         r = sh_bestr[w];
       }
-    a.ids[row] = key_idx(glist[r]);
+    mt[seg].best = b;
+    mt[seg].bestr = r;
   }
 }
 
-template <bool BF16>
-__global__ __launch_bounds__(BK_T) void k_bigk(SampleArgs a, uint64_t *ws, int64_t vstride) {
-  __shared__ uint32_t base[NB];            /* a digit's next place */
-  __shared__ uint32_t hist[NB];            /* the next pass's digit counts */
-  __shared__ uint32_t wcnt[2][BK_NW][NB];  /* a tile's count of each digit in each wave, then its place */
-  __shared__ float sh_max[BK_NW];
-  __shared__ uint32_t sh_flag[BK_NW], sh_lo[BK_NW], sh_hi[BK_NW];
-  const int row = (int)blockIdx.x, tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
-  const int V = a.vocab;
-  const RowP rp = row_params(a, row);
-  const float T = rp.T;
-  const bool t_finite = T < __builtin_inff();
-  const float y = 1.0f / T;
-  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
-  auto xat = [&](int i) { return scale_logit(load_logit<BF16>(rowp, i, rp.banned), T, y, t_finite); };
-
-  /* ---- 1. max and classification */
-  float xm = -__builtin_inff();
-  uint32_t fl = 0u;
-  for (int i = tid; i < V; i += BK_T) {
-    const float xi = xat(i);
-    const uint32_t c = classify(xi);
-    fl |= c;
-    if (!(c & 1u)) xm = fmaxf(xm, xi);
+__global__ __launch_bounds__(WAVE) void k_bk_pick(SampleArgs a, BkLayout L) {
+  const int row = (int)blockIdx.x, lane = lane_id();
+  float lse;
+  if (!bk_row_lse(L, row, lse)) return;
+  const BkMeta *mt = L.meta + (size_t)row * BK_SMAX;
+  const int SL = L.tps * BK_T;
+  const int nrs = (a.k + SL - 1) / SL;
+  float b = -2.0f;
+  int r = 0x7fffffff;
+  if (lane < nrs) {
+    b = mt[lane].best;
+    r = mt[lane].bestr;
   }
-  xm = wave_max_f(xm);
-  const uint32_t wf = __ballot(fl & 1u) ? 1u : 0u;
-  if (lane == 0) {
-    sh_max[wid] = xm;
-    sh_flag[wid] = wf;
-  }
-  if (tid < NB) hist[tid] = 0u;
-  __syncthreads();
-  float M = sh_max[0];
-  uint32_t F = sh_flag[0];
-  for (int w = 1; w < BK_NW; w++) {
-    M = fmaxf(M, sh_max[w]);
-    F |= sh_flag[w];
-  }
-  if (F & 1u) {
-    write_special(a, row, false);
-    return;
-  }
-  if (M == -__builtin_inff()) {
-    write_special(a, row, true);
-    return;
-  }
-
-  /* ---- 2. the exact row sum, the keys in index order and the first pass's
-   * digit counts */
-  uint64_t *buf[2] = {ws + (size_t)row * 2 * (size_t)vstride, ws + (size_t)row * 2 * (size_t)vstride + vstride};
-  uint64_t acc = 0;
-  for (int i = tid; i < V; i += BK_T) {
-    const float xi = xat(i);
-    acc += d3s_fix40(d3s_expf(xi - M));
-    const uint64_t key = composite_key(xi, i);
-    buf[0][i] = key;
-    atomicAdd(&hist[bk_digit(key, 0)], 1u);
-  }
-  {
-    const uint64_t w = wave_sum_u64(acc);
-    if (lane == 0) {
-      sh_lo[wid] = (uint32_t)w;
-      sh_hi[wid] = (uint32_t)(w >> 32);
-    }
-  }
-  __syncthreads();
-  uint64_t S = 0;
-  for (int w = 0; w < BK_NW; w++) S += ((uint64_t)sh_hi[w] << 32) | sh_lo[w];
-  const float lse = M + d3s_logf(d3s_fixsum_to_f32(S));
-
-  /* ---- 3. stable LSD radix sort by ordkey(x) descending.  Per tile of
-   * 1024 keys (index order within the pass): each wave counts its keys of
-   * each digit (the first lane of a digit's peers files the count); thread t
-   * < 256 turns digit t's counts into places (the running base plus the
-   * earlier waves'); each key goes to its wave's place plus its peers below
-   * it.  Two count buffers alternate between tiles, so each is cleared a tile
-   * after its last read.  The next pass's digit counts are taken on the way. */
-  const uint64_t lt = (1ull << lane) - 1ull; /* lanes below this one */
-#pragma unroll 1
-  for (int pass = 0; pass < 4; pass++) {
-    const uint64_t *src = buf[pass & 1];
-    uint64_t *dst = buf[(pass & 1) ^ 1];
-    /* both count buffers zero for the pass's first two tiles (the last
-     * tile of the pass before left its places in one of them) */
-    for (int j = tid; j < 2 * BK_NW * NB; j += BK_T) (&wcnt[0][0][0])[j] = 0u;
-    if (wid == 0) { /* the pass's digit counts -> starts, four per lane */
-      uint32_t h[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) h[q] = hist[4 * lane + q];
-      const uint32_t ls = h[0] + h[1] + h[2] + h[3];
-      uint32_t run = wave_scan_add_u32(ls) - ls;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        base[4 * lane + q] = run;
-        hist[4 * lane + q] = 0u;
-        run += h[q];
-      }
-    }
-    __syncthreads();
-    /* each tile's key is loaded one tile ahead, its latency behind the
-     * previous tile's barriers (which order LDS only) */
-    uint64_t next = tid < V ? src[tid] : 0ull;
-    int par = 0;
-#pragma unroll 1
-    for (int t0 = 0; t0 < V; t0 += BK_T, par ^= 1) {
-      const int i = t0 + tid;
-      const bool valid = i < V;
-      const uint64_t key = next;
-      next = i + BK_T < V ? src[i + BK_T] : 0ull;
-      const uint64_t live = __ballot(valid);
-      const uint32_t d = bk_digit(key, pass);
-      const uint64_t peers = wave_peers<8>(d, live);
-      const uint32_t below = (uint32_t)__popcll(peers & lt);
-      if (valid && below == 0u) wcnt[par][wid][d] = (uint32_t)__popcll(peers);
-      if (pass < 3) {
-        const uint32_t d2 = bk_digit(key, pass + 1);
-        const uint64_t p2 = wave_peers<8>(d2, live);
-        if (valid && (p2 & lt) == 0ull) atomicAdd(&hist[d2], (uint32_t)__popcll(p2));
-      }
-      lds_barrier();
-      if (tid < NB) {
-        uint32_t run = base[tid];
-#pragma unroll
-        for (int w = 0; w < BK_NW; w++) {
-          const uint32_t c = wcnt[par][w][tid];
-          wcnt[par][w][tid] = run;
-          wcnt[par ^ 1][w][tid] = 0u; /* last read a tile ago */
-          run += c;
-        }
-        base[tid] = run;
-      }
-      lds_barrier();
-      if (valid) dst[wcnt[par][wid][d] + below] = key;
-    }
-    __syncthreads(); /* the pass's keys and the next pass's counts, for every thread */
-  }
-
-  /* ---- 4. the op graph's tail over the first k ranks (four passes end in
-   * buf[0]) */
-  {
-    __shared__ uint32_t sh_u32[BK_NW];
-    __shared__ float sh_best[BK_NW];
-    __shared__ int sh_bestr[BK_NW];
-    static_assert(sizeof(wcnt) >= BK_CH * sizeof(uint64_t), "the chunk fits in the count buffers");
-    bigk_tail(a, row, lse, rp.top_p, buf[0], (uint64_t *)&wcnt[0][0][0], sh_lo, sh_hi, sh_u32, sh_best, sh_bestr);
-  }
+  wave_argmax(b, r);
+  if (lane == 0) a.ids[row] = key_idx(L.keys[(size_t)row * 2 * (size_t)L.vstride + r]);
 }
 
 }  // namespace
@@ -328,13 +591,19 @@ __global__ __launch_bounds__(BK_T) void k_bigk(SampleArgs a, uint64_t *ws, int64
 /* elements of a row's key buffer (whole 512-byte blocks) */
 static int64_t bigk_vstride(int vocab) { return ((int64_t)vocab + 63) & ~(int64_t)63; }
 
-size_t bigk_row_bytes(const SampleArgs &a) { return 2 * (size_t)bigk_vstride(a.vocab) * sizeof(uint64_t); }
+/* per row: two key buffers, four count tables, the segments' records */
+size_t bigk_row_bytes(const SampleArgs &a) {
+  return 2 * (size_t)bigk_vstride(a.vocab) * sizeof(uint64_t) + 4 * (size_t)BK_SMAX * NB * sizeof(uint32_t) +
+         (size_t)BK_SMAX * sizeof(BkMeta);
+}
 
 bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
   const size_t per_row = bigk_row_bytes(a);
-  if (!ws || ws_bytes < per_row) return false;
+  if (!ws || ws_bytes < per_row || a.vocab < 1) return false;
   const int64_t chunk = (int64_t)(ws_bytes / per_row);
   const int es = dt == DT_F32 ? 4 : 2;
+  const int64_t vstride = bigk_vstride(a.vocab);
+  const int tiles = (a.vocab + BK_T - 1) / BK_T;
   for (int64_t r0 = 0; r0 < a.n_rows; r0 += chunk) {
     SampleArgs c = a;
     const int64_t n = a.n_rows - r0 < chunk ? a.n_rows - r0 : chunk;
@@ -347,12 +616,27 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
     c.ids = a.ids + r0;
     if (a.probs) c.probs = a.probs + (size_t)r0 * a.k;
     if (a.cand) c.cand = a.cand + (size_t)r0 * a.k;
+    /* segments: enough workgroups for the CUs, whole tiles each */
+    int want = (int)((BK_WGS + n - 1) / n);
+    want = want < 1 ? 1 : (want > BK_SMAX ? BK_SMAX : want);
+    BkLayout L;
+    L.tps = (tiles + want - 1) / want;
+    L.nseg = (tiles + L.tps - 1) / L.tps;
+    L.inv_sl = 1.0f / (float)(L.tps * BK_T);
+    L.vstride = vstride;
+    L.keys = (uint64_t *)ws;
+    L.hist = (uint32_t *)((char *)ws + (size_t)n * 2 * (size_t)vstride * sizeof(uint64_t));
+    L.meta = (BkMeta *)((char *)L.hist + (size_t)n * 4 * BK_SMAX * NB * sizeof(uint32_t));
+    const dim3 grid((unsigned)L.nseg, (unsigned)n);
     if (dt == DT_F32)
-      hipLaunchKernelGGL(k_bigk<false>, dim3((unsigned)n), dim3(BK_T), 0, s, c, (uint64_t *)ws,
-                         bigk_vstride(a.vocab));
+      hipLaunchKernelGGL(k_bk_keys<false>, grid, dim3(BK_T), 0, s, c, L);
     else
-      hipLaunchKernelGGL(k_bigk<true>, dim3((unsigned)n), dim3(BK_T), 0, s, c, (uint64_t *)ws,
-                         bigk_vstride(a.vocab));
+      hipLaunchKernelGGL(k_bk_keys<true>, grid, dim3(BK_T), 0, s, c, L);
+    for (int pass = 0; pass < 4; pass++) hipLaunchKernelGGL(k_bk_pass, grid, dim3(BK_T), 0, s, c, L, pass);
+    hipLaunchKernelGGL(k_bk_sums, grid, dim3(BK_T), 0, s, c, L);
+    hipLaunchKernelGGL(k_bk_cut, dim3((unsigned)n), dim3(BK_T), 0, s, c, L);
+    hipLaunchKernelGGL(k_bk_race, grid, dim3(BK_T), 0, s, c, L);
+    hipLaunchKernelGGL(k_bk_pick, dim3((unsigned)n), dim3(WAVE), 0, s, c, L);
   }
   return true;
 }

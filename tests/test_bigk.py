@@ -1,6 +1,7 @@
 """k beyond the generic kernel's LDS sort on rows longer than the nucleus
 kernel takes: the reference's op graph with top-k disabled on a wide row
-(src/sampling.c:33-35, a full argsort), here the sorting kernel (k_bigk).
+(src/sampling.c:33-35, a full argsort), here the sorting kernels (k_bk_*: a
+radix sort over the row's segments, then the tail).
 
 Ids, candidates (the index of every rank) and probabilities must equal the
 oracle's bit for bit; the oracle is pinned by the closed form and brute force
