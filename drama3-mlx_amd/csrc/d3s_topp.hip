@@ -285,7 +285,7 @@ __device__ __forceinline__ CutBands topp_cut_bands(uint64_t Tq, uint64_t S, floa
  * uncertainty, when more elements than a wave holds would go to that wave, or
  * when no kept score is positive. */
 constexpr int TOPP_FULL = -2;
-constexpr int TOPP_RETRY = -3; /* the ids path's round 1 (internal) */
+constexpr int TOPP_RETRY = -3; /* the ids path's exact retry (internal) */
 constexpr int TOPP_REDO_WG = 64; /* k_topp_redo's workgroups (at most) */
 constexpr int TF_CAP = WAVE; /* the elements (and refined ranks) one wave takes */
 
@@ -437,11 +437,11 @@ __device__ __forceinline__ int topp_bucket_of_rank(const uint32_t *bstart, int r
 }
 
 /* 4'-5' once the bucket counts and group sums are in LDS.  Returns the id,
- * TOPP_FULL, or (round 0: the exact prefix puts the cut outside the group the
- * bands chose) TOPP_RETRY, after which the caller runs the row again as round
- * 1 (exact_grp): exact group sums of fix40(expf(x - lse)) then give the group
- * holding the cut and the exact prefix before it.  Every thread calls it and
- * every return follows a barrier. */
+ * TOPP_FULL, or (the first try: the exact prefix puts the cut outside the
+ * range the bands chose) TOPP_RETRY, after which the row is run again as the
+ * exact retry (exact_grp): exact group sums of fix40(expf(x - lse)) then give
+ * the group holding the cut and the exact prefix before it.  Every thread
+ * calls it and every return follows a barrier. */
 template <int EPT, int TBLOCK, int NBK>
 __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const float (&x)[EPT],
                                              float m, float xmin, float scale, float top_p,
@@ -456,9 +456,9 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   int *rr = (int *)(dyn + tf_rr(TBLOCK));
   float *ru = (float *)(dyn + tf_ru(TBLOCK));
   /* [0] elements, [1] flag, [2] id, [3] refined ranks, [4] the cut group,
-   * [5] (round 0) the group holding the certain keep band's end */
+   * [5] (the first try) the group holding the certain keep band's end */
   uint32_t *misc = (uint32_t *)(dyn + tf_misc(TBLOCK));
-  /* [0] the cut group's prefix Q; [1] round 0: group [5]'s Q, round 1: the
+  /* [0] the cut group's prefix Q; [1] the first try: group [5]'s Q, the retry: the
    * exact prefix before the cut group */
   uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32);
   uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
@@ -507,7 +507,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   const bool settled1 = Tq == 0ull;                     /* every prefix passes: cut 1 */
   const bool settledk = Tq > ((uint64_t)k << 41);      /* none reaches it: cut k */
   uint64_t tdrop = ~0ull, tkeep = 0ull;
-  uint64_t pg0 = 0ull; /* round 1: the exact prefix before the group */
+  uint64_t pg0 = 0ull; /* the retry: the exact prefix before the group */
   if (!exact_grp) {
     if (!settled1 && !settledk) {
       const CutBands cb = topp_cut_bands_lean(Tq, S, lse, lnS, xmin, k);
@@ -523,7 +523,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       }
     }
   } else {
-    /* round 1: exact group sums (the scan's barriers ordered the clearing
+    /* the retry: exact group sums (the scan's barriers ordered the clearing
      * before these), their prefixes, the first group reaching Tq */
 #pragma unroll
     for (int j = 0; j < EPT; j++) { /* (-inf and past the row: 0, into a slot past the groups') */
@@ -543,10 +543,10 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   }
   __syncthreads(); /* the starts, the map, the cut group */
   const int g = settled1 || (settledk && !exact_grp) ? -1 : (int)misc[4]; /* -1: no group (cleared to ~0) */
-  /* the cut lies in groups [gl, g]: round 0 widens the range back to the
+  /* the cut lies in groups [gl, g]: the first try widens the range back to the
    * group where the bands' keep end falls when the elements fit one wave
    * (the bands straddling a group boundary would otherwise leave a cut
-   * before the group to round 1) */
+   * before the group to the retry) */
   int gl = g;
   if (g >= 0) {
     if (exact_grp) {
@@ -712,7 +712,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
         const int src = (int)__builtin_ctzll(at | (1ull << 63));
         qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
       }
-      /* (round 1: the cut from the group's exact prefixes below) */
+      /* (the retry: the cut from the group's exact prefixes below) */
       certain = !exact_grp && (cut <= 1 || qlast < tkeep);
     } else {
       cut = klo;
@@ -757,7 +757,7 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
         const int src = (int)__builtin_ctzll(at | (1ull << 63));
         qlast = ((uint64_t)readlane_u((uint32_t)(qr >> 32), src) << 32) | readlane_u((uint32_t)qr, src);
       }
-      /* the cut outside the group: round 1 (after round 0), the full path */
+      /* the cut outside the group: the retry (after the first try), the full path */
       if (lane == 0 && (p0 >= Tq || re == 0x7fffffff)) misc[2] = (uint32_t)(exact_grp ? TOPP_FULL : TOPP_RETRY);
     }
     __syncthreads();
@@ -1184,7 +1184,7 @@ constexpr int topp_ids_waves(int ept, int tb) { return tb == 512 ? 8 : topp_wave
 
 /* The ids-only path for row `row` (ids only, k = V), by the whole workgroup;
  * dyn: its LDS arrays.  Returns true when the row's id is written, false when
- * the row needs another round (the full path after round 1, exact_grp). */
+ * the row needs another pass (the retry, exact_grp, or after it the full path). */
 template <int EPT, bool BF16, int TBLOCK, int NBK>
 __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row, char *dyn, uint32_t *bstart,
                                              TRed &R, const bool exact_grp) {
@@ -1269,7 +1269,7 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
   return false; /* TOPP_FULL, TOPP_RETRY, or scale 0 (a single finite x, or a row of equal ones) */
 }
 
-/* k_topp_ids: ids only, k = V; the ids-only path, the rows it leaves (round 1
+/* k_topp_ids: ids only, k = V; the ids-only path, the rows it leaves (the retry
  * or the full path) filed for k_topp_redo */
 template <int EPT, bool BF16, int TBLOCK>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids_waves(EPT, TBLOCK)))) void k_topp_ids(
@@ -1280,7 +1280,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids
     rd.rows[atomicAdd(rd.count, 1u)] = row;
 }
 
-/* k_topp_redo: each filed row again, the ids-only path's round 1 and, where
+/* k_topp_redo: each filed row again, the ids-only path's exact retry and, where
  * that leaves it, the full path (TOPP_REDO_WG workgroups take the rows in
  * turn; a few rows per launch, so registers are given room: the loop around
  * the row must not spill); the last workgroup to finish clears the counts.
@@ -1299,7 +1299,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) voi
   for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
     const int row = rd.rows[i];
     __syncthreads(); /* the previous row's LDS reads done */
-    /* (1024-thread workgroups: the full path alone; with round 1 beside it
+    /* (1024-thread workgroups: the full path alone; with the retry beside it
      * the loop would need scratch at four waves per SIMD) */
     if (TBLOCK > 512 || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, true)) {
       __syncthreads();
