@@ -106,6 +106,8 @@ struct __align__(16) BkMeta {
   float max;
   uint32_t flags;
   uint64_t sum;
+  uint32_t kor, kand; /* OR and AND of the segment's digit words (k_bk_keys) */
+  uint32_t klow;      /* OR of the low 16 bits of its x (k_bk_keys) */
   uint64_t psum, ksum;
   float best;
   int bestr;
@@ -113,11 +115,14 @@ struct __align__(16) BkMeta {
   float inv;
 };
 
-/* a launch's rows in the workspace: the rows' key buffers, then their count
- * tables ([row][pass][segment][digit]), then their segments' records */
+/* a launch's rows in the workspace: the rows' key buffers, their count
+ * tables ([row][pass][segment][digit]: filled by the pass before each), the
+ * segments' counts of digits 0 and 2 in index order ([row][2][segment][digit]:
+ * the first pass's, k_bk_keys'), then their segments' records */
 struct BkLayout {
   uint64_t *keys; /* [n][2][vstride] */
   uint32_t *hist; /* [n][4][BK_SMAX][NB] */
+  uint32_t *hidx; /* [n][2][BK_SMAX][NB] */
   BkMeta *meta;   /* [n][BK_SMAX] */
   int64_t vstride;
   int nseg, tps;  /* segments per row, tiles per segment */
@@ -137,17 +142,30 @@ __device__ __forceinline__ uint32_t bk_seg_of(uint32_t pos, const BkLayout &L) {
 
 /* the row's max and refusal flag from its segments' records (every wave
  * alike: lane s reads segment s, all in one round of loads); with S, also
- * the row's exact sum (the first pass's) */
-__device__ __forceinline__ void bk_row_max(const BkLayout &L, int row, float &M, uint32_t &F, uint64_t *S = nullptr) {
+ * the row's exact sum (the first pass's); with fp, the first radix pass the
+ * row runs: 4 when every key's x is the same (no pass reorders anything:
+ * the keys stay in index order), 2 when every x has its low 16 bits zero
+ * (bf16 logits at T = 1), else 0.  In the second case digits 0 and 1 are
+ * 0x0000 or 0xffff by x's sign, which digit 3 holds: keys equal in digits 2
+ * and 3 are equal in x, so passes 2 and 3 alone, from index order, give the
+ * same stable order as all four.  Skipping two keeps the result in the
+ * first buffer. */
+__device__ __forceinline__ void bk_row_max(const BkLayout &L, int row, float &M, uint32_t &F, uint64_t *S = nullptr,
+                                           int *fp = nullptr) {
   const int lane = lane_id();
   const BkMeta *mt = L.meta + (size_t)row * BK_SMAX;
   float m = -__builtin_inff();
-  uint32_t f = 0u;
+  uint32_t f = 0u, o = 0u, n = ~0u, lw = 0u;
   uint64_t sm = 0ull;
   if (lane < L.nseg) {
     m = mt[lane].max;
     f = mt[lane].flags;
     if (S) sm = mt[lane].sum;
+    if (fp) {
+      o = mt[lane].kor;
+      n = mt[lane].kand;
+      lw = mt[lane].klow;
+    }
   }
   M = wave_max_f(m);
   F = __ballot(f & 1u) ? 1u : 0u;
@@ -156,16 +174,25 @@ __device__ __forceinline__ void bk_row_max(const BkLayout &L, int row, float &M,
     for (int s2 = 0; s2 < L.nseg; s2++) t += readlane_u64(sm, s2);
     *S = t;
   }
+  if (fp) {
+    uint32_t ro = 0u, rn = ~0u;
+    for (int s2 = 0; s2 < L.nseg; s2++) {
+      ro |= readlane_u(o, s2);
+      rn &= readlane_u(n, s2);
+    }
+    *fp = ro == rn ? 4 : (__ballot(lw != 0u) == 0ull ? 2 : 0);
+  }
 }
 
-/* k_bk_keys: a segment's keys in index order, its max and flags, its digit
- * counts for the first pass; the later passes' counts of the segment zeroed
- * (they are added to by the pass before each) */
+/* k_bk_keys: a segment's keys in index order, its max and flags, its counts
+ * of digits 0 and 2 in index order (the first pass's, whichever it is) and
+ * the OR and AND of its digit words; the later passes' counts of the
+ * segment zeroed (they are added to by the pass before each) */
 template <bool BF16>
 __global__ __launch_bounds__(BK_T) void k_bk_keys(SampleArgs a, BkLayout L) {
-  __shared__ uint32_t hist[NB];
+  __shared__ uint32_t hist[2][NB];
   __shared__ float sh_max[BK_NW];
-  __shared__ uint32_t sh_flag[BK_NW];
+  __shared__ uint32_t sh_flag[BK_NW], sh_or[BK_NW], sh_and[BK_NW], sh_low[BK_NW];
   const int seg = (int)blockIdx.x, row = (int)blockIdx.y;
   const int tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
   const int V = a.vocab;
@@ -176,10 +203,10 @@ __global__ __launch_bounds__(BK_T) void k_bk_keys(SampleArgs a, BkLayout L) {
   const float y = 1.0f / T;
   const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
   uint64_t *buf0 = L.keys + (size_t)row * 2 * (size_t)L.vstride;
-  if (tid < NB) hist[tid] = 0u;
+  if (tid < 2 * NB) (&hist[0][0])[tid] = 0u;
   __syncthreads();
   float xm = -__builtin_inff();
-  uint32_t fl = 0u;
+  uint32_t fl = 0u, wo = 0u, wn = ~0u, wl = 0u;
 #pragma unroll 1
   for (int i0 = lo + tid; i0 < hi; i0 += BK_B * BK_T) { /* BK_B loads in flight, then their work */
     float v[BK_B];
@@ -198,34 +225,56 @@ __global__ __launch_bounds__(BK_T) void k_bk_keys(SampleArgs a, BkLayout L) {
         if (!(c & 1u)) xm = fmaxf(xm, xi);
         const uint64_t key = composite_key(xi, i);
         buf0[i] = key;
-        atomicAdd(&hist[bk_digit(key, 0)], 1u);
+        atomicAdd(&hist[0][bk_digit(key, 0)], 1u);
+        atomicAdd(&hist[1][bk_digit(key, 2)], 1u);
+        const uint32_t dw = (uint32_t)((~key) >> 32); /* the digit word */
+        wo |= dw;
+        wn &= dw;
+        wl |= d3s_f2u(xi) & 0xffffu;
       }
     }
   }
   xm = wave_max_f(xm);
   const uint32_t wf = __ballot(fl & 1u) ? 1u : 0u;
+#pragma unroll
+  for (int sh = 1; sh < WAVE; sh <<= 1) {
+    wo |= (uint32_t)__shfl_xor((int)wo, sh);
+    wn &= (uint32_t)__shfl_xor((int)wn, sh);
+    wl |= (uint32_t)__shfl_xor((int)wl, sh);
+  }
   if (lane == 0) {
     sh_max[wid] = xm;
     sh_flag[wid] = wf;
+    sh_or[wid] = wo;
+    sh_and[wid] = wn;
+    sh_low[wid] = wl;
   }
   __syncthreads();
   uint32_t *gh = L.hist + (size_t)row * 4 * BK_SMAX * NB;
+  uint32_t *hx = L.hidx + (size_t)row * 2 * BK_SMAX * NB;
   if (tid < NB) {
-    gh[seg * NB + tid] = hist[tid];
+    hx[seg * NB + tid] = hist[0][tid];
+    hx[(BK_SMAX + seg) * NB + tid] = hist[1][tid];
 #pragma unroll
     for (int p = 1; p < 4; p++) gh[(p * BK_SMAX + seg) * NB + tid] = 0u;
   }
   if (tid == 0) {
     float M = sh_max[0];
-    uint32_t F = sh_flag[0];
+    uint32_t F = sh_flag[0], O = sh_or[0], N = sh_and[0], W = sh_low[0];
     for (int w = 1; w < BK_NW; w++) {
       M = fmaxf(M, sh_max[w]);
       F |= sh_flag[w];
+      O |= sh_or[w];
+      N &= sh_and[w];
+      W |= sh_low[w];
     }
     BkMeta m;
     m.max = M;
     m.flags = F;
     m.sum = 0ull;
+    m.kor = O;
+    m.kand = N;
+    m.klow = W;
     L.meta[(size_t)row * BK_SMAX + seg] = m;
   }
 }
@@ -244,13 +293,35 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
   const int lo = seg * L.tps * BK_T, hi = min(V, lo + L.tps * BK_T);
   float M;
   uint32_t F;
-  bk_row_max(L, row, M, F);
+  int fp;
+  bk_row_max(L, row, M, F, nullptr, &fp);
   if ((F & 1u) || M == -__builtin_inff()) return; /* (every workgroup of the row alike) */
   uint64_t *buf = L.keys + (size_t)row * 2 * (size_t)L.vstride;
-  const uint64_t *src = buf + (pass & 1) * L.vstride;
-  uint64_t *dst = buf + ((pass & 1) ^ 1) * L.vstride;
+  if (pass < fp) { /* a pass the row skips (its digit is every key's); the first takes the sum */
+    if (pass == 0) {
+      uint64_t acc = 0ull;
+#pragma unroll 1
+      for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
+        uint64_t kv[BK_B];
+#pragma unroll
+        for (int q = 0; q < BK_B; q++) kv[q] = r0 + q * BK_T < hi ? buf[r0 + q * BK_T] : 0ull;
+#pragma unroll
+        for (int q = 0; q < BK_B; q++)
+          if (r0 + q * BK_T < hi) acc += d3s_fix40_exp(key_x(kv[q]) - M); /* (x <= m) */
+      }
+      const uint64_t S = bk_block_sum(acc, sh_lo, sh_hi);
+      if (tid == 0) L.meta[(size_t)row * BK_SMAX + seg].sum = S;
+    }
+    return;
+  }
+  const int e = pass - fp; /* the passes run before this one */
+  const uint64_t *src = buf + (e & 1) * L.vstride;
+  uint64_t *dst = buf + ((e & 1) ^ 1) * L.vstride;
   uint32_t *gh = L.hist + (size_t)row * 4 * BK_SMAX * NB;
-  const uint32_t *cnt = gh + (size_t)pass * BK_SMAX * NB;
+  /* the segments' counts: the index order's for the row's first pass, else
+   * the pass before's */
+  const uint32_t *cnt = pass == fp ? L.hidx + (size_t)row * 2 * BK_SMAX * NB + (fp == 2 ? BK_SMAX * NB : 0)
+                                   : gh + (size_t)pass * BK_SMAX * NB;
 
   /* the segment's first place of each digit: the row's keys of smaller
    * digits plus the earlier segments' of this digit */
@@ -591,9 +662,9 @@ __global__ __launch_bounds__(WAVE) void k_bk_pick(SampleArgs a, BkLayout L) {
 /* elements of a row's key buffer (whole 512-byte blocks) */
 static int64_t bigk_vstride(int vocab) { return ((int64_t)vocab + 63) & ~(int64_t)63; }
 
-/* per row: two key buffers, four count tables, the segments' records */
+/* per row: two key buffers, six count tables, the segments' records */
 size_t bigk_row_bytes(const SampleArgs &a) {
-  return 2 * (size_t)bigk_vstride(a.vocab) * sizeof(uint64_t) + 4 * (size_t)BK_SMAX * NB * sizeof(uint32_t) +
+  return 2 * (size_t)bigk_vstride(a.vocab) * sizeof(uint64_t) + 6 * (size_t)BK_SMAX * NB * sizeof(uint32_t) +
          (size_t)BK_SMAX * sizeof(BkMeta);
 }
 
@@ -626,7 +697,8 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
     L.vstride = vstride;
     L.keys = (uint64_t *)ws;
     L.hist = (uint32_t *)((char *)ws + (size_t)n * 2 * (size_t)vstride * sizeof(uint64_t));
-    L.meta = (BkMeta *)((char *)L.hist + (size_t)n * 4 * BK_SMAX * NB * sizeof(uint32_t));
+    L.hidx = L.hist + (size_t)n * 4 * BK_SMAX * NB;
+    L.meta = (BkMeta *)(L.hidx + (size_t)n * 2 * BK_SMAX * NB);
     const dim3 grid((unsigned)L.nseg, (unsigned)n);
     if (dt == DT_F32)
       hipLaunchKernelGGL(k_bk_keys<false>, grid, dim3(BK_T), 0, s, c, L);
