@@ -20,9 +20,11 @@
  *     a tile (ordering LDS only; each tile's keys load during the tile
  *     before).  Each key's place gives the segment it lands in for the next
  *     pass: the next pass's counts per (segment, digit), gathered in LDS and
- *     added to the workspace's table once per workgroup.  The first pass also
- *     takes the segment's exact sum (2^-40 fixed point of d3s_expf(x - m), m
- *     the row's max from every segment's).  Stability keeps equal x in index
+ *     added to the workspace's table once per workgroup.  A row whose x all
+ *     have zero low 16 bits (bf16 logits at T = 1) skips the first two passes
+ *     (bk_row_max says why that is exact).  The row's first pass also takes
+ *     the segment's exact sum (2^-40 fixed point of d3s_expf(x - m), m the
+ *     row's max from every segment's).  Stability keeps equal x in index
  *     order, so the result is the order (x desc, index asc) of every kernel;
  *  the tail, over the first k ranks cut into the same segments (k_bk_sums,
  *     k_bk_cut, k_bk_race, k_bk_pick below): refused and all -inf rows as
@@ -30,7 +32,7 @@
  *     exact prefix sums to the cut, the kept sum, probabilities and the race.
  * The same definition as the generic and nucleus kernels, bit for bit.  The
  * workspace holds, per row, two buffers of the row's keys (16 bytes per
- * element), the four passes' count tables and the segments' records. */
+ * element), the passes' count tables and the segments' records. */
 #include "d3s_generic.h"
 
 #pragma clang fp contract(off)
@@ -97,7 +99,7 @@ constexpr int BK_PF = 4;    /* tiles of keys a pass keeps in flight (even) */
 constexpr int BK_WGS = 512; /* workgroups a launch aims at: two per CU */
 
 /* a segment's record: its max and refusal flag (k_bk_keys), its exact sum
- * (the first pass); then, for the segment's ranks [s L, s L + L) after the
+ * (the row's first pass); then, for the segment's ranks [s L, s L + L) after the
  * sort, the sums of their terms fix40(d3s_expf(x_r - lse)) and
  * fix40(d3s_expf(x_r - x_0)) (k_bk_sums) and their race's first maximum
  * (k_bk_race); segment 0's record also holds the row's cut and 1 / kept sum
@@ -297,8 +299,8 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
   bk_row_max(L, row, M, F, nullptr, &fp);
   if ((F & 1u) || M == -__builtin_inff()) return; /* (every workgroup of the row alike) */
   uint64_t *buf = L.keys + (size_t)row * 2 * (size_t)L.vstride;
-  if (pass < fp) { /* a pass the row skips (its digit is every key's); the first takes the sum */
-    if (pass == 0) {
+  if (pass < fp) { /* a pass the row skips; with no pass to run, the first takes the sum */
+    if (fp == 4 && pass == 0) {
       uint64_t acc = 0ull;
 #pragma unroll 1
       for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
@@ -361,7 +363,7 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
    * the next BK_PF tiles in flight (a workgroup keeps BK_PF tiles of reads
    * outstanding: the pass is bound by that latency, not by its work) */
   const uint64_t lt = (1ull << lane) - 1ull;
-  uint64_t acc = 0ull; /* the first pass: the segment's exact sum */
+  uint64_t acc = 0ull; /* the row's first pass: the segment's exact sum */
   uint64_t pf[BK_PF];
 #pragma unroll
   for (int q = 0; q < BK_PF; q++) pf[q] = lo + q * BK_T + tid < hi ? src[lo + q * BK_T + tid] : 0ull;
@@ -382,7 +384,7 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
       const uint64_t peers = wave_peers<8>(d, live);
       const uint32_t below = (uint32_t)__popcll(peers & lt);
       if (valid && below == 0u) wcnt[par][wid][d] = (uint32_t)__popcll(peers);
-      if (pass == 0 && valid) acc += d3s_fix40_exp(key_x(key) - M); /* (x <= m) */
+      if (pass == fp && valid) acc += d3s_fix40_exp(key_x(key) - M); /* (the row's first pass; x <= m) */
       lds_barrier();
       if (tid < NB) {
         uint32_t run = base[tid];
@@ -414,7 +416,7 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
       if (c) atomicAdd(&gn[j], c);
     }
   }
-  if (pass == 0) {
+  if (pass == fp) {
     const uint64_t S = bk_block_sum(acc, sh_lo, sh_hi);
     if (tid == 0) L.meta[(size_t)row * BK_SMAX + seg].sum = S;
   }
