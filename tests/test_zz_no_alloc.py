@@ -87,6 +87,22 @@ def test_no_alloc_nucleus_ids_only(gpu, oracle):
         assert np.array_equal(b[0], oracle.sample(x, u, 1.0, 0.95, banned=b_, n_threads=8)["ids"])
 
 
+def test_no_alloc_sorting_scratch_limit(gpu, oracle):
+    """k > 16384 on a wide row sorts one row at a time in the scratch: a row
+    of 239 552 elements (its keys, count tables and records fill the scratch
+    after the counters exactly) is sampled; one element more is refused with
+    D3S_ERR_SCRATCH before anything is launched."""
+    rng = np.random.default_rng(74)
+    for V, rc in ((239552, 0), (239553, -6)):
+        x = (rng.standard_normal((1, V)) * 2.0).astype(np.float32)
+        u = oracle.uniform(74, V, 1, V)
+        got = gpu.sample(x, u, 1.0, 0.9, want_probs=False, noalloc=True)
+        print(f"[no-alloc] sorting V={V} rc={got['rc']}", flush=True)
+        assert got["rc"] == rc
+        if rc == 0:
+            assert got["ids"][0] == oracle.sample(x, u, 1.0, 0.9, n_threads=8)["ids"][0]
+
+
 def test_no_alloc_one_wave_rows(gpu, oracle):
     """rows that use no scratch at all: the same route and bits as d3s_sample"""
     L = gpu.lib()
