@@ -44,8 +44,8 @@ constexpr int BK_T = 1024;
 constexpr int BK_NW = BK_T / WAVE;
 
 /* a workgroup barrier that orders LDS only: global loads and stores stay in
- * flight across it (the sort's global writes are ordered by the full barrier
- * at the start of the next pass) */
+ * flight across it (a pass's global writes are ordered before the next pass
+ * by the launch boundary between them) */
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
