@@ -128,6 +128,9 @@ struct BkLayout {
   BkMeta *meta;   /* [n][BK_SMAX] */
   int64_t vstride;
   int nseg, tps;  /* segments per row, tiles per segment */
+  int pass0;      /* the first pass launched: 2 when every row's x is known to
+                     have zero low 16 bits (bf16 logits at a scalar T of 1),
+                     else 0 */
   float inv_sl;   /* 1 / (tps BK_T), rounded */
 };
 
@@ -299,8 +302,8 @@ __global__ __launch_bounds__(BK_T) void k_bk_pass(SampleArgs a, BkLayout L, int 
   bk_row_max(L, row, M, F, nullptr, &fp);
   if ((F & 1u) || M == -__builtin_inff()) return; /* (every workgroup of the row alike) */
   uint64_t *buf = L.keys + (size_t)row * 2 * (size_t)L.vstride;
-  if (pass < fp) { /* a pass the row skips; with no pass to run, the first takes the sum */
-    if (fp == 4 && pass == 0) {
+  if (pass < fp) { /* a pass the row skips; with no pass to run, the first launched takes the sum */
+    if (fp == 4 && pass == L.pass0) {
       uint64_t acc = 0ull;
 #pragma unroll 1
       for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
@@ -706,7 +709,10 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
       hipLaunchKernelGGL(k_bk_keys<false>, grid, dim3(BK_T), 0, s, c, L);
     else
       hipLaunchKernelGGL(k_bk_keys<true>, grid, dim3(BK_T), 0, s, c, L);
-    for (int pass = 0; pass < 4; pass++) hipLaunchKernelGGL(k_bk_pass, grid, dim3(BK_T), 0, s, c, L, pass);
+    /* bf16 logits at T = 1 (after the clamp to 1e-5 either way): x = L, whose
+     * low 16 bits are zero, so every row skips passes 0 and 1 (bk_row_max) */
+    L.pass0 = dt == DT_BF16 && !a.temperature && a.temperature_scalar == 1.0f ? 2 : 0;
+    for (int pass = L.pass0; pass < 4; pass++) hipLaunchKernelGGL(k_bk_pass, grid, dim3(BK_T), 0, s, c, L, pass);
     hipLaunchKernelGGL(k_bk_sums, grid, dim3(BK_T), 0, s, c, L);
     hipLaunchKernelGGL(k_bk_cut, dim3((unsigned)n), dim3(BK_T), 0, s, c, L);
     hipLaunchKernelGGL(k_bk_race, grid, dim3(BK_T), 0, s, c, L);

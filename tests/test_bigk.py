@@ -88,6 +88,25 @@ def test_large_k_edge_rows(gpu, oracle):
     assert got["ids"][0] == -1 and got["ids"][1] == 0
 
 
+def test_large_k_bf16_at_unit_temperature(gpu, oracle):
+    """bf16 logits at a scalar T of 1 (x = L: every x has zero low 16 bits), the
+    rows whose first two radix passes are skipped and not launched: ordinary
+    rows, a row of one value (no pass runs at all), a masked stretch, a banned
+    index, both signs, ties."""
+    V, k = 20000, 20000
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((5, V)) * 2.0).astype(np.float32)
+    x[1, :] = -0.75
+    x[2, 5000:15000] = -np.inf
+    x[3] = np.round(x[3] * 2) / 2  # a few values, many ties of each sign
+    logits = W.f32_to_bf16_bits(x)
+    u = oracle.uniform(6, 0, 5, k)
+    banned = np.array([-1, -1, 3, -1, 17], np.int32)
+    for T, P in ((1.0, 0.9), (1.0, 1.0)):
+        check(gpu, oracle, logits, u, T, P, banned=banned, label=f"bigk bf16 T={T} top_p={P}")
+    check(gpu, oracle, logits, u, 1.0, 0.9, banned=banned, label="bigk bf16 T=1 no-alloc", noalloc=True)
+
+
 def test_large_k_without_allocation(gpu, oracle):
     """d3s_sample_noalloc sorts one row at a time in its fixed scratch (after
     the segmented kernel's counters, which stay zero)."""
