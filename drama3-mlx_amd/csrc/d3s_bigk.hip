@@ -230,7 +230,9 @@ __global__ __launch_bounds__(BK_T) void k_bk_keys(SampleArgs a, BkLayout L) {
         if (!(c & 1u)) xm = fmaxf(xm, xi);
         const uint64_t key = composite_key(xi, i);
         buf0[i] = key;
-        atomicAdd(&hist[0][bk_digit(key, 0)], 1u);
+        /* (with pass 0 not launched its counts are not read; its digit is
+         * then one of two values by the sign: 1024 atomics on two words) */
+        if (L.pass0 == 0) atomicAdd(&hist[0][bk_digit(key, 0)], 1u);
         atomicAdd(&hist[1][bk_digit(key, 2)], 1u);
         const uint32_t dw = (uint32_t)((~key) >> 32); /* the digit word */
         wo |= dw;
@@ -695,10 +697,13 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
     /* segments: enough workgroups for the CUs, whole tiles each */
     int want = (int)((BK_WGS + n - 1) / n);
     want = want < 1 ? 1 : (want > BK_SMAX ? BK_SMAX : want);
-    BkLayout L;
+    BkLayout L{};
     L.tps = (tiles + want - 1) / want;
     L.nseg = (tiles + L.tps - 1) / L.tps;
     L.inv_sl = 1.0f / (float)(L.tps * BK_T);
+    /* bf16 logits at T = 1 (after the clamp to 1e-5 either way): x = L, whose
+     * low 16 bits are zero, so every row skips passes 0 and 1 (bk_row_max) */
+    L.pass0 = dt == DT_BF16 && !a.temperature && a.temperature_scalar == 1.0f ? 2 : 0;
     L.vstride = vstride;
     L.keys = (uint64_t *)ws;
     L.hist = (uint32_t *)((char *)ws + (size_t)n * 2 * (size_t)vstride * sizeof(uint64_t));
@@ -709,9 +714,6 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
       hipLaunchKernelGGL(k_bk_keys<false>, grid, dim3(BK_T), 0, s, c, L);
     else
       hipLaunchKernelGGL(k_bk_keys<true>, grid, dim3(BK_T), 0, s, c, L);
-    /* bf16 logits at T = 1 (after the clamp to 1e-5 either way): x = L, whose
-     * low 16 bits are zero, so every row skips passes 0 and 1 (bk_row_max) */
-    L.pass0 = dt == DT_BF16 && !a.temperature && a.temperature_scalar == 1.0f ? 2 : 0;
     for (int pass = L.pass0; pass < 4; pass++) hipLaunchKernelGGL(k_bk_pass, grid, dim3(BK_T), 0, s, c, L, pass);
     hipLaunchKernelGGL(k_bk_sums, grid, dim3(BK_T), 0, s, c, L);
     hipLaunchKernelGGL(k_bk_cut, dim3((unsigned)n), dim3(BK_T), 0, s, c, L);
