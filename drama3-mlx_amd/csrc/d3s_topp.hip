@@ -1276,8 +1276,10 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids
     SampleArgs a, ToppRedo rd) {
   D3S_TOPP_SHARED
   const int row = (int)blockIdx.x;
-  if (!topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, false) && tid == 0)
-    rd.rows[atomicAdd(rd.count, 1u)] = row;
+  /* (FLAG_EXACT_LSE: every row straight to the exact retry) */
+  const bool filed =
+      (a.flags & FLAG_EXACT_LSE) != 0u || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, false);
+  if (filed && tid == 0) rd.rows[atomicAdd(rd.count, 1u)] = row;
 }
 
 /* k_topp_redo: each filed row again, the ids-only path's exact retry and, where
@@ -1319,10 +1321,8 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) voi
 #undef D3S_TOPP_SHARED
 
 /* the ids-only path takes calls with k = V and neither probabilities nor
- * candidates */
-bool topp_ids_call(const SampleArgs &a) {
-  return !a.probs && !a.cand && a.k == a.vocab && (a.flags & FLAG_EXACT_LSE) == 0;
-}
+ * candidates (with FLAG_EXACT_LSE, every row by its exact retry) */
+bool topp_ids_call(const SampleArgs &a) { return !a.probs && !a.cand && a.k == a.vocab; }
 
 template <int EPT, bool BF16, int TBLOCK>
 bool try_topp(const SampleArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
@@ -1340,7 +1340,8 @@ bool try_topp(const SampleArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
       rd.done = (uint32_t *)((char *)ws + 128);
       rd.rows = (int32_t *)((char *)ws + split_counter_bytes());
       hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), arrays, s, a, rd);
-      const int grid = a.n_rows < TOPP_REDO_WG ? a.n_rows : TOPP_REDO_WG;
+      /* (every row filed under FLAG_EXACT_LSE: a workgroup each) */
+      const int grid = a.n_rows < TOPP_REDO_WG || (a.flags & FLAG_EXACT_LSE) ? a.n_rows : TOPP_REDO_WG;
       hipLaunchKernelGGL((k_topp_redo<EPT, BF16, TBLOCK>), dim3(grid), dim3(TBLOCK), ranked > arrays ? ranked : arrays,
                          s, a, rd);
       return true;

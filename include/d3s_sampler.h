@@ -40,7 +40,9 @@ extern "C" {
 #define D3S_FLAG_GENERIC 1u      /* always the streaming kernel (the same results) */
 #define D3S_FLAG_EXACT_LSE 2u    /* register kernels: always compute the exact row
                                     sum (by default only rows whose top-p cut it
-                                    could change) */
+                                    could change); the nucleus kernel's ids-only
+                                    form: every row by its exact retry (the same
+                                    results) */
 #define D3S_FLAG_EXACT_SELECT 4u /* register kernels: always the radix select */
 #define D3S_FLAG_OP_GRAPH 8u     /* every row in the op graph's order, as the
                                     reference computes it with D3_NO_FUSED_SAMPLER

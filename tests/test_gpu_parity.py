@@ -579,6 +579,30 @@ def test_ranked_nucleus_edge_rows(gpu, oracle):
         compare(oracle, gpu, x[3:], u[3:], T, 0.9, label=f"nucleus rows T={T}")
 
 
+def test_ranked_nucleus_exact_retry_on_every_row(gpu, oracle):
+    """k = V, ids only, D3S_FLAG_EXACT_LSE: every row of the nucleus kernel's
+    ids path goes straight to its exact retry (exact group sums of
+    fix40(expf(x - lse)) give the group holding the cut), which otherwise only
+    the rows whose first try cannot settle take; C5 rows, ties, masked
+    stretches, a banned index, per-row T and top_p, the 1024-thread form."""
+    w = W.make("C5", rows=512, seed=23, uniforms=False)
+    u = oracle.uniform(23, 0, 512, 4097)
+    compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], w["banned"], flags=gpu.FLAG_EXACT_LSE,
+            label="nucleus exact retry, C5 rows")
+    rng = np.random.default_rng(24)
+    for V in (4097, 5000):
+        N = 16
+        x = (rng.standard_normal((N, V)) * 0.3).astype(np.float32)
+        x[1] = np.round(x[1] * 4)        # a few values, many ties each
+        x[2, ::3] = -np.inf              # a third masked
+        x[3, 7] = 20.0                   # one logit holds the nucleus
+        T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+        top_p = rng.uniform(0.5, 1.0, N).astype(np.float32)
+        ban = np.where(np.arange(N) % 3 == 0, 5, -1).astype(np.int32)
+        u = oracle.uniform(24, V, N, V)
+        compare(oracle, gpu, x, u, T, top_p, ban, flags=gpu.FLAG_EXACT_LSE, label=f"nucleus exact retry V={V}")
+
+
 def test_ranked_nucleus_no_positive_kept_score(gpu, oracle):
     """k = V with uniforms that leave no kept rank a positive score (u = 0:
     noise -0, score -inf; u = 1: noise +inf, score 0; u NaN or above 1): the
