@@ -105,6 +105,9 @@ def test_large_k_bf16_at_unit_temperature(gpu, oracle):
     for T, P in ((1.0, 0.9), (1.0, 1.0)):
         check(gpu, oracle, logits, u, T, P, banned=banned, label=f"bigk bf16 T={T} top_p={P}")
     check(gpu, oracle, logits, u, 1.0, 0.9, banned=banned, label="bigk bf16 T=1 no-alloc", noalloc=True)
+    # the same values as fp32 logits: every pass launched, the rows find the
+    # first two to skip on the device
+    check(gpu, oracle, W.bf16_bits_to_f32(logits), u, 1.0, 0.9, banned=banned, label="bigk fp32 of bf16 values, T=1")
 
 
 def test_large_k_without_allocation(gpu, oracle):
