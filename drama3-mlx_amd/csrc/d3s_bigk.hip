@@ -77,10 +77,21 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
 
 constexpr int BK_CH = 4096; /* ranks of the cut's exact scan, staged in LDS */
 
-/* block sum of per-thread fixed-point values (below 2^56 in total); opens
- * with a barrier (the scratch may still be being read) */
+/* sum over the wave of per-lane 64-bit values, exact modulo 2^64 (three
+ * 24-bit parts, each summed in 32 bits): a thread's partial sum over a long
+ * segment of terms near 2^40 can pass the shared wave sum's 2^45 */
+__device__ __forceinline__ uint64_t bk_wave_sum(uint64_t v) {
+  const uint32_t p0 = wave_sum_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t p1 = wave_sum_u32((uint32_t)((v >> 24) & 0xffffffu));
+  const uint32_t p2 = wave_sum_u32((uint32_t)(v >> 48));
+  return (uint64_t)p0 + ((uint64_t)p1 << 24) + ((uint64_t)p2 << 48);
+}
+
+/* block sum of per-thread fixed-point values, exact modulo 2^64 (the
+ * oracle's integer sums); opens with a barrier (the scratch may still be
+ * being read) */
 __device__ __forceinline__ uint64_t bk_block_sum(uint64_t v, uint32_t *lo, uint32_t *hi) {
-  const uint64_t w = wave_sum_u64(v);
+  const uint64_t w = bk_wave_sum(v);
   __syncthreads();
   if (lane_id() == 0) {
     lo[threadIdx.x / WAVE] = (uint32_t)w;
