@@ -110,6 +110,25 @@ def test_large_k_bf16_at_unit_temperature(gpu, oracle):
     check(gpu, oracle, W.bf16_bits_to_f32(logits), u, 1.0, 0.9, banned=banned, label="bigk fp32 of bf16 values, T=1")
 
 
+def test_large_k_no_positive_kept_score(gpu, oracle):
+    """k = V with uniforms that leave no kept rank a positive score (u = 0:
+    score -inf; u = 1: score 0; u NaN or above 1: NaN): the dropped ranks race
+    too, across the race's segments."""
+    V = k = 20000
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((5, V)) * 3.0).astype(np.float32)
+    u = oracle.uniform(7, 0, 5, k)
+    u[0, :3000] = 0.0     # kept ranks -inf: the first dropped rank past 3000 with a finite noise wins
+    u[1, :3000] = 1.0     # kept scores 0: rank 0 wins the tie with the dropped ranks' 0
+    u[2, :] = np.nan      # every score -1: rank 0
+    u[3, :3000] = 1.5     # kept scores NaN: a dropped rank wins
+    u[4, 0] = 0.0         # rank 0 alone scores -inf: another kept rank wins
+    got, exp = check(gpu, oracle, x, u, 1.0, 0.3, label="bigk no positive kept score")
+    won = lambda r: int(np.nonzero(exp["cand"][r] == exp["ids"][r])[0][0])
+    assert exp["probs"][0, won(0)] == 0.0 and exp["probs"][3, won(3)] == 0.0  # a dropped rank won
+    assert won(1) == 0 and won(2) == 0
+
+
 def test_large_k_without_allocation(gpu, oracle):
     """d3s_sample_noalloc sorts one row at a time in its fixed scratch (after
     the segmented kernel's counters, which stay zero)."""
