@@ -75,8 +75,6 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
   return ((uint64_t)readlane_u((uint32_t)(v >> 32), l) << 32) | readlane_u((uint32_t)v, l);
 }
 
-constexpr int BK_CH = 4096; /* ranks of the cut's exact scan, staged in LDS */
-
 /* sum over the wave of per-lane 64-bit values, exact modulo 2^64 (three
  * 24-bit parts, each summed in 32 bits): a thread's partial sum over a long
  * segment of terms near 2^40 can pass the shared wave sum's 2^45 */
@@ -84,6 +82,15 @@ __device__ __forceinline__ uint64_t bk_wave_sum(uint64_t v) {
   const uint32_t p0 = wave_sum_u32((uint32_t)(v & 0xffffffu));
   const uint32_t p1 = wave_sum_u32((uint32_t)((v >> 24) & 0xffffffu));
   const uint32_t p2 = wave_sum_u32((uint32_t)(v >> 48));
+  return (uint64_t)p0 + ((uint64_t)p1 << 24) + ((uint64_t)p2 << 48);
+}
+
+/* inclusive prefix sum over the wave of per-lane 64-bit values, exact
+ * modulo 2^64 (three 24-bit parts) */
+__device__ __forceinline__ uint64_t bk_wave_scan(uint64_t v) {
+  const uint32_t p0 = wave_scan_add_u32((uint32_t)(v & 0xffffffu));
+  const uint32_t p1 = wave_scan_add_u32((uint32_t)((v >> 24) & 0xffffffu));
+  const uint32_t p2 = wave_scan_add_u32((uint32_t)(v >> 48));
   return (uint64_t)p0 + ((uint64_t)p1 << 24) + ((uint64_t)p2 << 48);
 }
 
@@ -128,7 +135,7 @@ struct __align__(16) BkMeta {
   float inv;
 };
 
-/* a launch's rows in the workspace: the rows' key buffers, their count
+/* a launch's rows in the workspace (the tile sums after the records): the rows' key buffers, their count
  * tables ([row][pass][segment][digit]: filled by the pass before each), the
  * segments' counts of digits 0 and 2 in index order ([row][2][segment][digit]:
  * the first pass's, k_bk_keys'), then their segments' records */
@@ -137,6 +144,8 @@ struct BkLayout {
   uint32_t *hist; /* [n][4][BK_SMAX][NB] */
   uint32_t *hidx; /* [n][2][BK_SMAX][NB] */
   BkMeta *meta;   /* [n][BK_SMAX] */
+  uint64_t *tsum; /* [n][ntiles][2]: each tile's exact prefix and kept-sum terms' sums (k_bk_sums) */
+  int ntiles;     /* tiles of BK_T ranks a row */
   int64_t vstride;
   int nseg, tps;  /* segments per row, tiles per segment */
   int pass0;      /* the first pass launched: 2 when every row's x is known to
@@ -466,36 +475,49 @@ __device__ __forceinline__ bool bk_row_lse(const BkLayout &L, int row, float &ls
 __global__ __launch_bounds__(BK_T) void k_bk_sums(SampleArgs a, BkLayout L) {
   __shared__ uint32_t sh_lo[BK_NW], sh_hi[BK_NW];
   const int seg = (int)blockIdx.x, row = (int)blockIdx.y, tid = (int)threadIdx.x;
+  const int lane = lane_id(), wid = tid / WAVE;
   float lse;
   if (!bk_row_lse(L, row, lse)) return;
   const uint64_t *glist = L.keys + (size_t)row * 2 * (size_t)L.vstride;
+  uint64_t *ts = L.tsum + (size_t)row * 2 * (size_t)L.ntiles;
   const float v0 = key_x(glist[0]);
   const int lo = seg * L.tps * BK_T, hi = min(a.k, lo + L.tps * BK_T);
-  uint64_t ps = 0ull, ks = 0ull;
-#pragma unroll 1
-  for (int r0 = lo + tid; r0 < hi; r0 += BK_B * BK_T) {
-    uint64_t kv[BK_B];
+  /* wave w: the segment's tiles w, w + 16, ...; lane l the tile's ranks
+   * l + 64 q; each tile's two sums filed, the wave's totals kept */
+  uint64_t wp = 0ull, wk = 0ull;
+  for (int t = lo / BK_T + wid; t * BK_T < hi; t += BK_NW) {
+    const int r0 = t * BK_T + lane;
+    uint64_t kv[BK_T / WAVE];
 #pragma unroll
-    for (int q = 0; q < BK_B; q++) kv[q] = r0 + q * BK_T < hi ? glist[r0 + q * BK_T] : 0ull;
+    for (int q = 0; q < BK_T / WAVE; q++) kv[q] = r0 + q * WAVE < hi ? glist[r0 + q * WAVE] : 0ull;
+    uint64_t ps = 0ull, ks = 0ull;
 #pragma unroll
-    for (int q = 0; q < BK_B; q++)
-      if (r0 + q * BK_T < hi) {
+    for (int q = 0; q < BK_T / WAVE; q++)
+      if (r0 + q * WAVE < hi) {
         const float x = key_x(kv[q]);
         ps += d3s_fix40_exp(x - lse); /* (x <= x_0 <= lse) */
         ks += d3s_fix40_exp(x - v0);
       }
+    ps = bk_wave_sum(ps);
+    ks = bk_wave_sum(ks);
+    if (lane == 0) {
+      ts[2 * t] = ps;
+      ts[2 * t + 1] = ks;
+    }
+    wp += ps;
+    wk += ks;
   }
-  ps = bk_block_sum(ps, sh_lo, sh_hi);
-  ks = bk_block_sum(ks, sh_lo, sh_hi);
+  const uint64_t sp = bk_block_sum(lane == 0 ? wp : 0ull, sh_lo, sh_hi);
+  const uint64_t sk = bk_block_sum(lane == 0 ? wk : 0ull, sh_lo, sh_hi);
   if (tid == 0) {
-    L.meta[(size_t)row * BK_SMAX + seg].psum = ps;
-    L.meta[(size_t)row * BK_SMAX + seg].ksum = ks;
+    L.meta[(size_t)row * BK_SMAX + seg].psum = sp;
+    L.meta[(size_t)row * BK_SMAX + seg].ksum = sk;
   }
 }
 
 __global__ __launch_bounds__(BK_T) void k_bk_cut(SampleArgs a, BkLayout L) {
-  __shared__ uint64_t lch[BK_CH]; /* the cut's chunk */
   __shared__ uint32_t sh_lo[BK_NW], sh_hi[BK_NW], sh_u32[BK_NW];
+  __shared__ uint64_t sh_pk[2];
   const int row = (int)blockIdx.x, tid = (int)threadIdx.x, lane = lane_id(), wid = tid / WAVE;
   const int k = a.k;
   float lse;
@@ -533,59 +555,54 @@ __global__ __launch_bounds__(BK_T) void k_bk_cut(SampleArgs a, BkLayout L) {
   }
   int cut = k;
   if (c < nrs) {
-    /* the cut lies in segment c (a pass at rank 0 alone is no cut: the
-     * segment's later ranks pass too, and the first of them is) */
+    /* the cut lies in segment c: wave 0 finds the first of its tiles whose
+     * end passes top_p (with the prefix and the kept sum before it) from
+     * the tile sums; then that tile rank by rank, one rank a thread (a pass
+     * at rank 0 alone is no cut: the tile's later ranks pass too, and the
+     * first of them is) */
     const int lo = c * SL, hi = min(k, lo + SL);
-#pragma unroll 1
-    for (int r_lo = lo; r_lo < hi; r_lo += BK_CH) {
-      const int r_hi = min(hi, r_lo + BK_CH);
-      uint64_t loc = 0;
-#pragma unroll 4
-      for (int r = r_lo + tid; r < r_hi; r += BK_T) loc += d3s_fix40_exp(key_x(glist[r]) - lse);
-      const uint64_t tot = bk_block_sum(loc, sh_lo, sh_hi);
-      if (!(r_hi > 1 && d3s_fixsum_to_f32(base + tot) > top_p)) {
-        base += tot;
-        continue;
+    const uint64_t *ts = L.tsum + (size_t)row * 2 * (size_t)L.ntiles;
+    if (wid == 0) {
+      const int t_hi = (hi + BK_T - 1) / BK_T;
+      int ct = t_hi - 1;
+      uint64_t b = base, kk = kept;
+      for (int t0 = lo / BK_T; t0 < t_hi; t0 += WAVE) {
+        const int t = t0 + lane;
+        const uint64_t pt = t < t_hi ? ts[2 * t] : 0ull, kt = t < t_hi ? ts[2 * t + 1] : 0ull;
+        const uint64_t pin = bk_wave_scan(pt), kin = bk_wave_scan(kt);
+        const uint64_t m = __ballot(t < t_hi && d3s_fixsum_to_f32(b + pin) > top_p);
+        if (m) {
+          const int j = (int)__builtin_ctzll(m);
+          ct = t0 + j;
+          b += readlane_u64(pin - pt, j);
+          kk += readlane_u64(kin - kt, j);
+          break;
+        }
+        b += readlane_u64(pin, WAVE - 1);
+        kk += readlane_u64(kin, WAVE - 1);
       }
-      /* this chunk: its keys to LDS, each thread a run of BK_CH / BK_T
-       * consecutive ranks */
-      for (int r = r_lo + tid; r < r_hi; r += BK_T) lch[r - r_lo] = glist[r];
-      __syncthreads();
-      constexpr int RUN = BK_CH / BK_T;
-      uint64_t f[RUN];
-      uint64_t part = 0;
-#pragma unroll
-      for (int q = 0; q < RUN; q++) {
-        const int r = r_lo + tid * RUN + q;
-        f[q] = r < r_hi ? d3s_fix40_exp(key_x(lch[tid * RUN + q]) - lse) : 0ull;
-        part += f[q];
+      if (lane == 0) {
+        sh_u32[0] = (uint32_t)ct;
+        sh_pk[0] = b;
+        sh_pk[1] = kk;
       }
-      uint64_t P = base + block_excl_scan_u64<BK_NW>(part, sh_lo, sh_hi);
-      int cl = k;
-#pragma unroll
-      for (int q = 0; q < RUN; q++) {
-        const int r = r_lo + tid * RUN + q;
-        P += f[q];
-        if (r < r_hi && r > 0 && cl == k && d3s_fixsum_to_f32(P) > top_p) cl = r;
-      }
-      const int cm = wave_min_i32(cl);
-      if (lane == 0) sh_u32[wid] = (uint32_t)cm;
-      __syncthreads();
-      for (int w = 0; w < BK_NW; w++) cut = min(cut, (int)sh_u32[w]);
-      break;
     }
-    /* the kept sum: the segments before c and segment c's ranks below the cut */
-    uint64_t ks = 0ull;
-#pragma unroll 1
-    for (int r0 = lo + tid; r0 < cut; r0 += BK_B * BK_T) {
-      uint64_t kv[BK_B];
-#pragma unroll
-      for (int q = 0; q < BK_B; q++) kv[q] = r0 + q * BK_T < cut ? glist[r0 + q * BK_T] : 0ull;
-#pragma unroll
-      for (int q = 0; q < BK_B; q++)
-        if (r0 + q * BK_T < cut) ks += d3s_fix40_exp(key_x(kv[q]) - v0);
-    }
-    kept += bk_block_sum(ks, sh_lo, sh_hi);
+    __syncthreads();
+    const int ct = (int)sh_u32[0];
+    base = sh_pk[0];
+    kept = sh_pk[1];
+    const int r = ct * BK_T + tid;
+    const bool in = r < hi;
+    const float x = in ? key_x(glist[r]) : 0.0f;
+    const uint64_t f = in ? d3s_fix40_exp(x - lse) : 0ull;
+    const uint64_t P = base + block_excl_scan_u64<BK_NW>(f, sh_lo, sh_hi) + f;
+    const int cm = wave_min_i32(in && r > 0 && d3s_fixsum_to_f32(P) > top_p ? r : k);
+    __syncthreads(); /* (sh_u32 read above) */
+    if (lane == 0) sh_u32[wid] = (uint32_t)cm;
+    __syncthreads();
+    for (int w = 0; w < BK_NW; w++) cut = min(cut, (int)sh_u32[w]);
+    /* the kept sum: what came before the tile and its ranks below the cut */
+    kept += bk_block_sum(in && r < cut ? d3s_fix40_exp(x - v0) : 0ull, sh_lo, sh_hi);
   }
   if (tid == 0) {
     mt[0].cut = cut;
@@ -680,10 +697,11 @@ __global__ __launch_bounds__(WAVE) void k_bk_pick(SampleArgs a, BkLayout L) {
 /* elements of a row's key buffer (whole 512-byte blocks) */
 static int64_t bigk_vstride(int vocab) { return ((int64_t)vocab + 63) & ~(int64_t)63; }
 
-/* per row: two key buffers, six count tables, the segments' records */
+/* per row: two key buffers, six count tables, the segments' records, the
+ * tile sums */
 size_t bigk_row_bytes(const SampleArgs &a) {
   return 2 * (size_t)bigk_vstride(a.vocab) * sizeof(uint64_t) + 6 * (size_t)BK_SMAX * NB * sizeof(uint32_t) +
-         (size_t)BK_SMAX * sizeof(BkMeta);
+         (size_t)BK_SMAX * sizeof(BkMeta) + 2 * (size_t)((a.vocab + BK_T - 1) / BK_T) * sizeof(uint64_t);
 }
 
 bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
@@ -720,6 +738,8 @@ bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipSt
     L.hist = (uint32_t *)((char *)ws + (size_t)n * 2 * (size_t)vstride * sizeof(uint64_t));
     L.hidx = L.hist + (size_t)n * 4 * BK_SMAX * NB;
     L.meta = (BkMeta *)(L.hidx + (size_t)n * 2 * BK_SMAX * NB);
+    L.ntiles = tiles;
+    L.tsum = (uint64_t *)(L.meta + (size_t)n * BK_SMAX);
     const dim3 grid((unsigned)L.nseg, (unsigned)n);
     if (dt == DT_F32)
       hipLaunchKernelGGL(k_bk_keys<false>, grid, dim3(BK_T), 0, s, c, L);

@@ -89,11 +89,11 @@ def test_no_alloc_nucleus_ids_only(gpu, oracle):
 
 def test_no_alloc_sorting_scratch_limit(gpu, oracle):
     """k > 16384 on a wide row sorts one row at a time in the scratch: a row
-    of 239 552 elements (its keys, count tables and records fill the scratch
-    after the counters exactly) is sampled; one element more is refused with
-    D3S_ERR_SCRATCH before anything is launched."""
+    of 239 296 elements (the longest whose keys, count tables, records and
+    tile sums fit after the counters) is sampled; one element more is refused
+    with D3S_ERR_SCRATCH before anything is launched."""
     rng = np.random.default_rng(74)
-    for V, rc in ((239552, 0), (239553, -6)):
+    for V, rc in ((239296, 0), (239297, -6)):
         x = (rng.standard_normal((1, V)) * 2.0).astype(np.float32)
         u = oracle.uniform(74, V, 1, V)
         got = gpu.sample(x, u, 1.0, 0.9, want_probs=False, noalloc=True)
