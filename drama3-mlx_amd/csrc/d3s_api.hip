@@ -84,13 +84,13 @@ bool env_no_fused() { return getenv("D3_NO_FUSED_SAMPLER") != nullptr; }
 
 int launched() { return hipGetLastError() == hipSuccess ? D3S_OK : D3S_ERR_LAUNCH; }
 
-/* the sorting kernel's keys per launch from the stream's workspace: every
+/* the sorting kernels' keys per launch from the stream's workspace: every
  * row, up to 256 MiB (then launches of fewer rows), at least one row */
 constexpr size_t BIGK_WS_CAP = (size_t)256 << 20;
 
 /* the workspace sample_routed takes from a stream for these rows: the
  * segmented kernel's (counters and records), or the counters' block and the
- * sorting kernel's keys after it; 0 when no kernel needs one */
+ * sorting kernels' keys after it; 0 when no kernel needs one */
 size_t routed_workspace_bytes(const d3s::SampleArgs &a, d3s::Dtype dt) {
   const bool generic = (a.flags & D3S_FLAG_GENERIC) != 0u;
   if (!generic && d3s::split_segments(a, dt) > 0) return d3s::split_workspace_bytes(a, dt);
@@ -134,7 +134,7 @@ int sample_routed(const d3s::SampleArgs &a, d3s::Dtype dt, hipStream_t s, void *
     }
     if (d3s::launch_topp(a, dt, ws, ws_bytes, s)) return launched();
   }
-  if (a.k > d3s::generic_max_k()) { /* the sorting kernel, its keys after the counters' block */
+  if (a.k > d3s::generic_max_k()) { /* the sorting kernels, their keys after the counters' block */
     const size_t off = d3s::split_counter_bytes();
     if (!ws && stream_ws) {
       const size_t need = routed_workspace_bytes(a, dt);
@@ -188,7 +188,7 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   if (!no_alloc) return sample_routed(a, dt, (hipStream_t)stream);
   void *ws = nullptr;
   const size_t need = routed_workspace_bytes(a, dt);
-  if (need > 0) { /* the segmented kernel, the sorting kernel one row at a time, or the nucleus
+  if (need > 0) { /* the segmented kernel, the sorting kernels one row at a time, or the nucleus
                      ids path's filed rows (more rows than the scratch lists: the full path) */
     if (d3s::split_segments(a, dt) > 0 && need > D3S_SCRATCH_BYTES) return D3S_ERR_SCRATCH;
     ws = device_scratch();
@@ -274,7 +274,7 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
    * draw's indices go to first_idx or else main_tok (the pick reads each row's
    * before it writes it); the retry's to retry_idx or else the workspace. */
   /* one workspace block: the segmented kernel's counters and records, or the
-   * sorting kernel's keys, first (both draws use them in turn), then the
+   * sorting kernels' keys, first (both draws use them in turn), then the
    * retry's indices, never on the counters (which must stay zero for later
    * launches on this stream) */
   size_t split_bytes = routed_workspace_bytes(r.first, dt);

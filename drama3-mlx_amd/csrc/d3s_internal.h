@@ -147,10 +147,11 @@ size_t topp_workspace_bytes(const SampleArgs &a);
 /* Launch the streaming generic kernel (any V, k <= generic_max_k()). */
 bool launch_generic(const SampleArgs &a, Dtype dt, hipStream_t s);
 int generic_max_k();
-/* Launch the sorting kernel for k beyond generic_max_k() (any V, any k <= V):
- * one workgroup per row sorts the row's keys in ws (bigk_row_bytes per row;
- * rows go in launches of as many as ws holds).  Returns false when ws does
- * not hold one row. */
+/* Launch the sorting kernels for k beyond generic_max_k() (any V, any
+ * k <= V): each row cut into up to 16 segments, its keys radix-sorted in ws
+ * and the tail taken over the segments (bigk_row_bytes per row: keys, count
+ * tables, records, tile sums; rows go in launches of as many as ws holds).
+ * Returns false when ws does not hold one row. */
 bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s);
 size_t bigk_row_bytes(const SampleArgs &a);
 /* u[i] = d3s_uniform(seed, stream_id, i), i < n */

@@ -8,7 +8,7 @@ closed_form_rows.npz reaches the one-wave kernel (V = 257, k <= 40);
 closed_form_nucleus.npz the nucleus and generic kernels (k > 64 up to k = V);
 closed_form_wide.npz the fused, wide and generic kernels (V 10000 to 151936,
 bf16 values read as bf16 and widened to fp32); closed_form_sorted.npz the
-sorting kernel (k beyond 16384 on rows of 16500 and 20000)."""
+sorting kernels (k beyond 16384 on rows of 16500 and 20000)."""
 import os
 
 import numpy as np
