@@ -94,9 +94,12 @@ void launch_ras_select(const RasArgs &r, const int32_t *first, const int32_t *re
 /* Device memory the library keeps for one stream of the current device, at
  * least `bytes`, zero when first allocated (kernels that count in it leave it
  * zero again).  The first call on a stream, or one that needs more, allocates
- * (hipMalloc; the old block is freed, which waits for the device); later
- * calls return the same block.  Null when the allocation fails. */
+ * (hipMalloc); later calls return the same block.  A block the stream
+ * outgrows is kept (a call on another thread may still be enqueueing on it)
+ * until release_stream_workspace.  Null when the allocation fails. */
 void *stream_workspace(hipStream_t s, size_t bytes);
+/* Waits for the stream, then frees its block and the blocks it outgrew. */
+int release_stream_workspace(hipStream_t s);
 /* Launch the head's gemv. */
 void launch_linear(const LinearArgs &la, hipStream_t s);
 /* Launch the fused head: the gemv's logits and their sample in one launch
@@ -154,6 +157,8 @@ int generic_max_k();
  * Returns false when ws does not hold one row. */
 bool launch_bigk(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s);
 size_t bigk_row_bytes(const SampleArgs &a);
+/* w[i] = 0 for i < n_words (w 16-byte aligned), by a kernel */
+void launch_zero_fill(uint32_t *w, size_t n_words, hipStream_t s);
 /* u[i] = d3s_uniform(seed, stream_id, i), i < n */
 void launch_uniform(float *u, int64_t n, uint64_t seed, uint64_t stream_id, hipStream_t s);
 /* elementwise d3s_expf / d3s_logf / x / divisor / d3s_fix40 for the math self-test */

@@ -343,6 +343,17 @@ __global__ void k_uniform(float *u, int64_t n, uint64_t seed, uint64_t stream_id
   if (i < n) u[i] = d3s_uniform(seed, stream_id, (uint64_t)i);
 }
 
+/* w[i] = 0 for i < n, 16 bytes per thread where whole vectors fit (the
+ * workspace clear: a kernel node, never a memset node, in a captured graph) */
+__global__ void k_zero_fill(uint32_t *w, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n) {
+    *(uint4 *)(w + i) = make_uint4(0u, 0u, 0u, 0u);
+  } else {
+    for (int64_t j = i; j < n; j++) w[j] = 0u;
+  }
+}
+
 __global__ void k_math(const float *in, float *oe, float *ol, float *od, uint64_t *of, int64_t n,
                        float divisor) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -409,6 +420,13 @@ void launch_uniform(float *u, int64_t n, uint64_t seed, uint64_t stream_id, hipS
   const int B = 256;
   hipLaunchKernelGGL(k_uniform, dim3((unsigned)((n + B - 1) / B)), dim3(B), 0, s, u, n, seed,
                      stream_id);
+}
+
+void launch_zero_fill(uint32_t *w, size_t n_words, hipStream_t s) {
+  if (n_words == 0) return;
+  const int B = 256;
+  const size_t threads = (n_words + 3) / 4;
+  hipLaunchKernelGGL(k_zero_fill, dim3((unsigned)((threads + B - 1) / B)), dim3(B), 0, s, w, (int64_t)n_words);
 }
 
 void launch_math_selftest(const float *in, float *out_exp, float *out_log, float *out_div,

@@ -5,7 +5,9 @@
  * src/mlxu.c:52-89 and the test export d3_sample of src/testapi.c:155-166.
  * Work goes to the null stream, the counterpart of the reference's default
  * GPU stream (src/mlxu.c:20-26).  This layer allocates device memory for the
- * arrays it returns; the raw core (d3s_sample) never allocates. */
+ * arrays it returns, as MLX does for the reference's; its sampling calls take
+ * the raw core's workspace from the block the library keeps for the null
+ * stream (allocated on the first call whose route needs one, then reused). */
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>

@@ -22,8 +22,12 @@ FLAG_ONE_LAUNCH = 16
 COUNTER_REFUSED, COUNTER_ALL_MASKED, COUNTER_EXACT_SELECT, COUNTER_EXACT_LSE = range(4)
 NUM_COUNTERS = 4
 OK = 0
+ERR_ARG = -1
+ERR_UNSUPPORTED = -2
 ERR_SCRATCH = -6
+ERR_WORKSPACE = -7
 SCRATCH_BYTES = 4 << 20
+MAX_VOCAB = (1 << 24) - 1
 
 _lib = None
 
@@ -60,6 +64,25 @@ def lib():
         L.d3s_sample_noalloc.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
                                          vp, u32, vp]
         L.d3s_sample_noalloc.restype = i32
+        L.d3s_sample_ws.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
+                                    vp, u32, vp, i64, vp]
+        L.d3s_sample_ws.restype = i32
+        L.d3s_sample_workspace_bytes.argtypes = [i32, i64, i64, i32, u32]
+        L.d3s_sample_workspace_bytes.restype = i64
+        L.d3s_workspace_init.argtypes = [vp, i64, vp]
+        L.d3s_workspace_init.restype = i32
+        L.d3s_stream_workspace_release.argtypes = [vp]
+        L.d3s_stream_workspace_release.restype = i32
+        L.d3s_sample_ras_ws.argtypes = [vp, i32, i64, i64, i64, vp, vp, vp, i32,
+                                        ctypes.POINTER(RasParams), vp, vp, vp, vp, vp, vp, i64, vp]
+        L.d3s_sample_ras_ws.restype = i32
+        L.d3s_sample_ras_workspace_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(RasParams), i32]
+        L.d3s_sample_ras_workspace_bytes.restype = i64
+        L.d3s_linear_sample_bf16_ws.argtypes = [vp, vp, i64, i64, i64, vp, vp, i32, vp, vp, f32, f32, vp, vp,
+                                                vp, vp, u32, vp, i64, vp]
+        L.d3s_linear_sample_bf16_ws.restype = i32
+        L.d3s_linear_sample_workspace_bytes.argtypes = [i64, i64, i64, i32, u32, i32]
+        L.d3s_linear_sample_workspace_bytes.restype = i64
         L.d3s_sample_ras.argtypes = [vp, i32, i64, i64, i64, vp, vp, vp, i32,
                                      ctypes.POINTER(RasParams), vp, vp, vp, vp, vp, vp]
         L.d3s_sample_ras.restype = i32
@@ -91,19 +114,47 @@ def lib():
 
 
 def sample_raw(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, banned, ids,
-               probs=None, cand=None, counters=None, flags=0, stream=None, noalloc=False):
-    """d3s_sample (or d3s_sample_noalloc) on device pointers (ints).
-    temperature / top_p: a float (scalar) or a device pointer wrapped as
-    ("ptr", address)."""
+               probs=None, cand=None, counters=None, flags=0, stream=None, noalloc=False, workspace=None):
+    """d3s_sample (or d3s_sample_noalloc, or d3s_sample_ws with workspace =
+    (address, bytes)) on device pointers (ints).  temperature / top_p: a
+    float (scalar) or a device pointer wrapped as ("ptr", address)."""
     t_ptr, t_s = (temperature[1], 0.0) if isinstance(temperature, tuple) else (None, float(temperature))
     p_ptr, p_s = (top_p[1], 0.0) if isinstance(top_p, tuple) else (None, float(top_p))
+    if workspace is not None:
+        return lib().d3s_sample_ws(logits, dtype, n_rows, vocab, row_stride, u, k, t_ptr, p_ptr, t_s, p_s,
+                                   banned, ids, probs, cand, counters, flags, workspace[0], workspace[1], stream)
     fn = lib().d3s_sample_noalloc if noalloc else lib().d3s_sample
     return fn(logits, dtype, n_rows, vocab, row_stride, u, k, t_ptr, p_ptr, t_s, p_s,
               banned, ids, probs, cand, counters, flags, stream)
 
 
+def workspace_bytes(dtype, n_rows, vocab, k, flags=0):
+    """d3s_sample_workspace_bytes: the workspace d3s_sample_ws needs (or a
+    negative status)."""
+    return lib().d3s_sample_workspace_bytes(dtype, n_rows, vocab, k, flags)
+
+
+class Workspace:
+    """A caller-owned workspace for the *_ws entry points: device memory of
+    `nbytes`, cleared once by d3s_workspace_init on `stream`."""
+
+    def __init__(self, nbytes, stream=None):
+        import hiprt
+        self.nbytes = max(int(nbytes), 256)
+        self.buf = hiprt.DeviceBuffer(self.nbytes)
+        rc = lib().d3s_workspace_init(self.buf.ptr, self.nbytes, stream.ptr if stream else None)
+        if rc != OK:
+            raise RuntimeError(f"d3s_workspace_init: {rc}")
+
+    def arg(self):
+        return (self.buf.ptr, self.nbytes)
+
+    def free(self):
+        self.buf.free()
+
+
 def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True, row_stride=None,
-           vocab=None, stream=None, noalloc=False):
+           vocab=None, stream=None, noalloc=False, workspace=None):
     """Host arrays in, host arrays out (copies through device memory).
     logits: float32 or uint16 (bf16 bits) [N, row_stride]; u: float32 [N, k];
     temperature / top_p: scalars or float32 [N].  Returns dict(ids, probs, cand,
@@ -138,7 +189,8 @@ def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True,
     rc = sample_raw(bufs["logits"].ptr, dtype, N, V, stride, bufs["u"].ptr, k, T, P, ban,
                     bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
                     bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
-                    stream.ptr if stream else None, noalloc=noalloc)
+                    stream.ptr if stream else None, noalloc=noalloc,
+                    workspace=workspace.arg() if isinstance(workspace, Workspace) else workspace)
     out = dict(rc=rc)
     if rc != OK:
         return out

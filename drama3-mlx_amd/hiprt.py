@@ -39,18 +39,24 @@ def hip():
         H.hipGraphLaunch.argtypes = [vp, vp]
         H.hipGraphExecDestroy.argtypes = [vp]
         H.hipGraphDestroy.argtypes = [vp]
+        H.hipGraphGetNodes.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(sz)]
+        H.hipGraphNodeGetType.argtypes = [vp, ctypes.POINTER(i32)]
         for f in ("hipMalloc", "hipFree", "hipMemcpy", "hipMemcpyAsync", "hipMemset",
                   "hipDeviceSynchronize", "hipGetDeviceCount", "hipStreamCreate",
                   "hipStreamDestroy", "hipStreamSynchronize", "hipStreamWaitEvent", "hipEventCreate", "hipEventDestroy",
                   "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
                   "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate",
-                  "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy"):
+                  "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy", "hipGraphGetNodes",
+                  "hipGraphNodeGetType"):
             getattr(H, f).restype = i32
         _hip = H
     return _hip
 
 
 H2D, D2H, D2D = 1, 2, 3
+# hipGraphNodeType values (hip_runtime_api.h)
+GRAPH_NODE_TYPES = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty",
+                    6: "wait_event", 7: "event_record", 10: "mem_alloc", 11: "mem_free"}
 
 
 def check(rc, what="hip"):
@@ -150,3 +156,19 @@ class Event:
         if self.ptr:
             hip().hipEventDestroy(self.ptr)
             self.ptr = None
+
+
+def graph_node_types(graph):
+    """The type name of every node of a captured hipGraph_t (by
+    hipGraphGetNodes / hipGraphNodeGetType), in the order HIP lists them."""
+    H = hip()
+    n = ctypes.c_size_t(0)
+    check(H.hipGraphGetNodes(graph, None, ctypes.byref(n)), "hipGraphGetNodes")
+    nodes = (ctypes.c_void_p * max(n.value, 1))()
+    check(H.hipGraphGetNodes(graph, nodes, ctypes.byref(n)), "hipGraphGetNodes")
+    out = []
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        check(H.hipGraphNodeGetType(nodes[i], ctypes.byref(t)), "hipGraphNodeGetType")
+        out.append(GRAPH_NODE_TYPES.get(t.value, f"type{t.value}"))
+    return out

@@ -8,9 +8,24 @@
  *     src/mlxu.c:771-774), as d3s_uniform_fill.
  * Plain pointers and sizes only; every pointer argument is device memory (or
  * memory the device can read); `stream` is a hipStream_t (NULL: the null stream).
- * Calls enqueue work and return.  d3s_sample allocates device memory only on a
- * stream's first call that needs its workspace (rows spread over several CUs)
- * and keeps it for that stream; d3s_sample_noalloc never allocates.
+ * Calls enqueue work and return.
+ *
+ * Workspace.  Some routes keep state in device memory between their launches
+ * (the arrival counters and records of rows spread over several CUs, the rows
+ * the nucleus kernel files for its second launch, the sorting kernels' keys).
+ * The *_ws entry points take that workspace from the caller and never
+ * allocate: size it with the matching *_workspace_bytes query, allocate it
+ * once, clear it once with d3s_workspace_init, and pass it to every call.
+ * One workspace serves any sequence of calls on one stream (calls that run
+ * at the same time, on several streams, need one workspace each).  Its first
+ * 256 KiB are counters that every launch leaves zero again; the rest is
+ * scratch.  The calls without _ws (d3s_sample, d3s_sample_ras,
+ * d3s_linear_sample_bf16) are a convenience that takes the workspace from a
+ * block the library keeps per (device, stream), allocated on the stream's
+ * first call that needs one (the NULL stream is one such stream for every
+ * thread); d3s_stream_workspace_release frees a stream's block.
+ * d3s_sample_noalloc never allocates either: its workspace is one fixed block
+ * of static device memory per GPU.
  */
 #ifndef D3S_SAMPLER_H
 #define D3S_SAMPLER_H
@@ -27,11 +42,17 @@ extern "C" {
 /* status codes */
 #define D3S_OK 0
 #define D3S_ERR_ARG -1         /* shape, pointer or parameter out of range */
-#define D3S_ERR_UNSUPPORTED -2 /* k beyond d3s_max_k() */
+#define D3S_ERR_UNSUPPORTED -2 /* vocab (and so k) beyond D3S_MAX_VOCAB */
 #define D3S_ERR_LAUNCH -3      /* the HIP launch failed */
 #define D3S_ERR_DTYPE -4       /* unknown logits dtype */
 #define D3S_ERR_NOMEM -5       /* the library's workspace could not be allocated */
 #define D3S_ERR_SCRATCH -6     /* d3s_sample_noalloc: the call needs more than D3S_SCRATCH_BYTES */
+#define D3S_ERR_WORKSPACE -7   /* *_ws: the caller's workspace is smaller than the call needs */
+
+/* The widest row the sampler takes: 2^24 - 1 elements.  The exact row sum
+ * adds terms of up to 2^40 (units of 2^-40) in 64 bits, so 2^24 - 1 terms
+ * never wrap; wider rows return D3S_ERR_UNSUPPORTED. */
+#define D3S_MAX_VOCAB 16777215
 
 /* the fixed device scratch of d3s_sample_noalloc, per GPU */
 #define D3S_SCRATCH_BYTES (4u << 20)
@@ -80,12 +101,47 @@ extern "C" {
  * A row with a NaN or +inf x is refused: ids = -1, cand = -1, probs = NaN.
  * A row whose x are all -inf gets ids = 0 (the reference kernel's answer).
  * The result is identical for every flag combination.
+ * The workspace comes from the block the library keeps for `stream` (see
+ * Workspace above); d3s_sample_ws takes the caller's.
  * Replaces: sample_with_noise (src/sampling.c:194-203, declared src/model.h:175-176). */
 int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
                const float *u, int k, const float *temperature, const float *top_p,
                float temperature_scalar, float top_p_scalar, const int32_t *banned,
                int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
                void *stream);
+
+/* Bytes of workspace d3s_sample_ws needs for a call with these arguments (0:
+ * the call's route keeps no state in device memory), or a negative status for
+ * arguments d3s_sample rejects.  The need depends on dtype, n_rows, vocab, k
+ * and flags (and on D3_NO_FUSED_SAMPLER only through the route, not the size).
+ * Replaces the one-time set-up of sample_kernel_call (src/sampling.c:142-157). */
+int64_t d3s_sample_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab, int k, unsigned flags);
+
+/* d3s_sample with the workspace given: never allocates, so it may be captured
+ * in a HIP graph.  workspace: device memory of workspace_bytes (256-byte
+ * aligned, cleared once by d3s_workspace_init; it may be NULL when
+ * d3s_sample_workspace_bytes is 0).  A workspace smaller than the call needs
+ * returns D3S_ERR_WORKSPACE before anything is launched.  Calls that share a
+ * workspace must run one after another (one stream).  Same results as
+ * d3s_sample. */
+int d3s_sample_ws(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                  const float *u, int k, const float *temperature, const float *top_p,
+                  float temperature_scalar, float top_p_scalar, const int32_t *banned,
+                  int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
+                  void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Clears a workspace on `stream` with the library's own fill kernel (no
+ * memset node, no allocation).  Call it once after allocating the workspace,
+ * before the first call that uses it (every launch leaves it ready for the
+ * next).  workspace 256-byte aligned, bytes a multiple of 4. */
+int d3s_workspace_init(void *workspace, int64_t bytes, void *stream);
+
+/* Frees the block the library keeps for `stream` on the current device
+ * (d3s_sample, d3s_sample_ras and d3s_linear_sample_bf16 without _ws), after
+ * waiting for the stream.  For a stream about to be destroyed, or to give the
+ * memory back; the next call on the stream that needs a block allocates a new
+ * one.  No call may use the stream meanwhile. */
+int d3s_stream_workspace_release(void *stream);
 
 /* d3s_sample without any allocation, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -137,14 +193,29 @@ typedef struct {
  * Rows within one wave's reach (k and k2 <= 64, vocab within d3s_sample's
  * one-wave rows) take one launch that reads each row once; any other k and
  * vocab d3s_sample takes run as two d3s_sample launches and a third that picks
- * (its retry indices go to retry_idx, or else to a workspace the library keeps
- * per stream, allocated on the first such call: D3S_ERR_NOMEM if it cannot).
+ * (the retry's indices go to retry_idx, else to code0, else to the
+ * workspace).  The workspace, when the draws' routes or the retry's indices
+ * need one, comes from the block the library keeps for `stream` (see
+ * Workspace above; D3S_ERR_NOMEM if it cannot be allocated).
  * Replaces: the two sample_with_noise calls, candidate_token and the repeat test of
  * tower_decode_step (src/tower.c:420-433). */
 int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
                    const float *u, const float *u_retry, const int32_t *history, int history_len,
                    const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
                    int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *stream);
+
+/* Bytes of workspace d3s_sample_ras_ws needs (0: none), or a negative status.
+ * has_retry_out: nonzero when the call will pass retry_idx or code0. */
+int64_t d3s_sample_ras_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab, const d3s_ras_params *params,
+                                       int has_retry_out);
+
+/* d3s_sample_ras with the workspace given (never allocates); the workspace
+ * contract of d3s_sample_ws. */
+int d3s_sample_ras_ws(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                      const float *u, const float *u_retry, const int32_t *history, int history_len,
+                      const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
+                      int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *workspace,
+                      int64_t workspace_bytes, void *stream);
 
 /* The backbone head's logits (src/backbone.c:1213-1215: m_linear of the last
  * hidden row with lm_head_audio): y[n, r] = bf16 of x[n, :] . w[r, :], in the
@@ -167,16 +238,16 @@ int d3s_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_
  * / flags / outputs and the same result bits, including the choice of the
  * reference kernel's or the op graph's order.  y [n_rows, V] receives the
  * logits, or may be NULL when the caller does not keep them (they then go to
- * the stream's workspace).  No banned index.
+ * the workspace).  No banned index.
  * By default the gemv and the sample are two launches on the stream, the
  * faster form.  With D3S_FLAG_ONE_LAUNCH, calls with k <= 64, V <= 8192 and
  * at most 62 rows take one launch instead: each workgroup computes 16 logits
  * and files its part of the sample (max, fast sum, the logits) in the
- * stream's workspace, and the last to arrive samples the row (one kernel node
- * instead of two, about 3.5 us slower on [1, 2048] x [4097, 2048]); other
- * calls take the two launches.  The workspace is the one d3s_sample keeps per
- * stream, allocated on the stream's first call that needs it (D3S_ERR_NOMEM
- * if it cannot).
+ * workspace, and the last to arrive samples the row (one kernel node
+ * instead of two, about 2 us slower on [1, 2048] x [4097, 2048]); other
+ * calls take the two launches.  A workspace, when the call needs one, comes
+ * from the block the library keeps for `stream` (see Workspace above;
+ * D3S_ERR_NOMEM if it cannot be allocated).
  * Replaces: m_linear through gemv_row (src/mlxu.c:454-496) followed by
  * sample_with_noise on its logits: the backbone head (src/backbone.c:1213-1215)
  * and the tower's codebook heads (src/tower.c:228-232,:264,:440-443). */
@@ -185,14 +256,28 @@ int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows,
                            float temperature_scalar, float top_p_scalar, int32_t *ids, float *probs,
                            int32_t *cand, uint32_t *counters, unsigned flags, void *stream);
 
+/* Bytes of workspace d3s_linear_sample_bf16_ws needs (0: none), or a negative
+ * status.  keeps_logits: nonzero when the call will pass y. */
+int64_t d3s_linear_sample_workspace_bytes(int64_t n_rows, int64_t K, int64_t V, int k, unsigned flags,
+                                          int keeps_logits);
+
+/* d3s_linear_sample_bf16 with the workspace given (never allocates); the
+ * workspace contract of d3s_sample_ws. */
+int d3s_linear_sample_bf16_ws(const uint16_t *x, const uint16_t *w, int64_t n_rows, int64_t K, int64_t V,
+                              uint16_t *y, const float *u, int k, const float *temperature, const float *top_p,
+                              float temperature_scalar, float top_p_scalar, int32_t *ids, float *probs,
+                              int32_t *cand, uint32_t *counters, unsigned flags, void *workspace,
+                              int64_t workspace_bytes, void *stream);
+
 /* u[i] = the i-th uniform of draw `draw` under `seed` (Philox4x32-10, counter
  * (i/4, draw), key seed, 24-bit values in [0, 1)), for i < n.
  * Replaces: m_uniform (src/mlxu.c:771-774) as used by sample_top_k_top_p
  * (src/sampling.c:208); the MLX generator itself is not reproduced. */
 int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream);
 
-/* The largest k d3s_sample accepts, and the largest vocab the fused kernel
- * takes for a dtype (wider rows use the streaming kernel). */
+/* The largest k d3s_sample accepts (D3S_MAX_VOCAB: any k up to the row's
+ * vocab), and the largest vocab the fused kernel takes for a dtype (wider
+ * rows use the other kernels). */
 int d3s_max_k(void);
 int d3s_fused_max_vocab(int dtype);
 

@@ -214,8 +214,9 @@ int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t voc
                       const float *top_p, float temperature_scalar, float top_p_scalar,
                       const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
                       float *lse, uint8_t *flags, double *gaps, int op_graph, int n_threads) {
-  if (n_rows < 0 || vocab < 1 || row_stride < vocab || k < 1 || k > vocab || !ids ||
-      (n_rows > 0 && (!logits || !u)) || (dtype != D3S_ORACLE_DTYPE_F32 && dtype != D3S_ORACLE_DTYPE_BF16))
+  if (n_rows < 0 || vocab < 1 || vocab > D3S_ORACLE_MAX_VOCAB || row_stride < vocab || k < 1 || k > vocab ||
+      !ids || (n_rows > 0 && (!logits || !u)) ||
+      (dtype != D3S_ORACLE_DTYPE_F32 && dtype != D3S_ORACLE_DTYPE_BF16))
     return -1;
   if (n_threads < 1) n_threads = 1;
   const int kernel = kernel_order(vocab, k, op_graph);

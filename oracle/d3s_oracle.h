@@ -44,6 +44,10 @@ extern "C" {
 #define D3S_ORACLE_DTYPE_F32 0
 #define D3S_ORACLE_DTYPE_BF16 1
 
+/* The widest row: the exact row sum adds up to vocab terms of at most 2^40
+ * (units of 2^-40) in 64 bits, which 2^24 - 1 terms never wrap. */
+#define D3S_ORACLE_MAX_VOCAB 16777215
+
 /* flags per row */
 #define D3S_ORACLE_BAD 1          /* non-finite x: refused, id -1 */
 #define D3S_ORACLE_TOPP_EDGE 2    /* some r in [1,k) has |c64_r - top_p| < 1e-6 */
@@ -58,7 +62,7 @@ extern "C" {
  * gaps [n_rows, 2] = (min_r |c64_r - top_p|, relative gap of the top two scores).
  * op_graph: nonzero takes the op graph's order for every call, as the
  * reference does when D3_NO_FUSED_SAMPLER is set (src/sampling.c:197).
- * Returns 0, or -1 for bad arguments. */
+ * Returns 0, or -1 for bad arguments (vocab above D3S_ORACLE_MAX_VOCAB included). */
 int d3s_oracle_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
                       int64_t row_stride, const float *u, int k, const float *temperature,
                       const float *top_p, float temperature_scalar, float top_p_scalar,

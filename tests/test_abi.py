@@ -54,7 +54,7 @@ def test_library_exports_every_declared_function(lib):
 
 def test_host_queries(lib):
     assert lib.d3s_version().startswith(b"d3sampler")
-    assert lib.d3s_max_k() == 1 << 26  # any k up to the vocab limit
+    assert lib.d3s_max_k() == (1 << 24) - 1  # any k up to the vocab limit, D3S_MAX_VOCAB
     assert lib.d3s_fused_max_vocab(0) >= 4097 and lib.d3s_fused_max_vocab(1) >= 4096
     assert lib.d3s_fused_max_vocab(7) == -4
 
@@ -74,8 +74,9 @@ def test_argument_validation_without_device(lib):
     assert d3s.sample_raw(**{**base, "flags": 64}) == -1
     assert d3s.sample_raw(**{**base, "flags": 16}) == -1  # 1, 2, 4, 8 are flags; 16 is not
     assert d3s.sample_raw(**{**base, "flags": 2 | 64}) == -1
-    huge = dict(base, vocab=(1 << 26) + 1, row_stride=(1 << 26) + 1)
-    assert d3s.sample_raw(**huge) == -1  # beyond the vocab limit (any k up to V is taken)
+    huge = dict(base, vocab=1 << 24, row_stride=1 << 24)
+    assert d3s.sample_raw(**huge) == -2  # beyond D3S_MAX_VOCAB (any k up to V is taken)
+    assert d3s.sample_raw(**dict(base, vocab=(1 << 26) + 1, row_stride=(1 << 26) + 1)) == -2
     assert d3s.sample_raw(**{**base, "n_rows": 0}) == 0  # nothing to do, nothing launched
 
 

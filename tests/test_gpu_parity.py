@@ -134,11 +134,12 @@ def test_uniform_fill_matches_host(gpu, oracle):
                                        ("C5", 4096)])
 def test_parity_on_configs(gpu, oracle, name, rows):
     """BASELINE.json's five configurations at their full shapes (C1: its
-    10 000 seeded rows in one launch)."""
+    10 000 seeded rows in one launch, which takes k_wave; the kernel that
+    serves C1's own calls is tested by test_c1_rows_on_the_latency_kernel)."""
     w = W.make(name, rows=rows, seed=42, uniforms=False)
     u = oracle.uniform(42, 0, rows, w["k"])
     compare(oracle, gpu, w["logits"], u, w["temperature"], w["top_p"], w["banned"],
-            label=f"config {name}")
+            label=f"config {name}" + (" (k_wave, one launch of 10 000 rows)" if name == "C1" else ""))
 
 
 def test_single_row_launches(gpu, oracle):
@@ -150,6 +151,54 @@ def test_single_row_launches(gpu, oracle):
         got = gpu.sample(w["logits"][r:r + 1], u[r:r + 1], 0.7, 0.7)
         assert got["ids"][0] == exp["ids"][r]
         assert np.array_equal(got["probs"][0], exp["probs"][r])
+
+
+def test_c1_rows_on_the_latency_kernel(gpu, oracle):
+    """BASELINE.json's 10 000 seeded C1 rows through the kernel that serves C1
+    (k_wave_row: launches of at most 1024 rows, one row per 4-wave workgroup):
+    the 10 000 rows as launches of 1024 rows and fewer, then 500 of them one
+    row per launch, as the CLI samples them (device-resident rows, one
+    d3s_sample call per row).  Ids, candidates and probabilities bit-equal to
+    the oracle; rows and boundary rows recorded for the parity summary."""
+    import hiprt
+    N, K = 10000, 30
+    w = W.make("C1", rows=N, seed=42, uniforms=False)
+    x = w["logits"]
+    u = oracle.uniform(42, 0, N, K)
+    exp = oracle.sample(x, u, 0.7, 0.7, n_threads=8)
+    edge = (exp["flags"] & (oracle.TOPP_EDGE | oracle.RACE_EDGE)) != 0
+    bad = 0
+    for r0 in range(0, N, 1024):
+        r1 = min(r0 + 1024, N)
+        banner(f"C1 k_wave_row launch rows {r0}..{r1 - 1}")
+        got = gpu.sample(x[r0:r1], u[r0:r1], 0.7, 0.7)
+        assert got["rc"] == 0, got["rc"]
+        bad += int(np.sum(got["ids"] != exp["ids"][r0:r1]))
+        assert np.array_equal(got["ids"], exp["ids"][r0:r1]), r0
+        assert np.array_equal(got["cand"], exp["cand"][r0:r1]), r0
+        assert np.array_equal(got["probs"], exp["probs"][r0:r1]), r0
+    parity_report.record("config C1 (k_wave_row, launches of <= 1024 rows)", N, bad, int(edge.sum()))
+
+    n1 = 500
+    rows = np.arange(0, N, N // n1)[:n1]
+    V = x.shape[1]
+    bl, bu = hiprt.to_device(x), hiprt.to_device(u)
+    ids, probs, cand = (hiprt.DeviceBuffer(4 * n1), hiprt.DeviceBuffer(4 * n1 * K),
+                        hiprt.DeviceBuffer(4 * n1 * K))
+    banner(f"C1 k_wave_row: {n1} one-row launches")
+    for i, r in enumerate(rows):
+        rc = gpu.sample_raw(bl.ptr + int(r) * V * 4, gpu.DTYPE_F32, 1, V, V, bu.ptr + int(r) * K * 4, K, 0.7, 0.7,
+                            None, ids.ptr + 4 * i, probs.ptr + 4 * K * i, cand.ptr + 4 * K * i)
+        assert rc == 0, (r, rc)
+    hiprt.synchronize()
+    got_ids = ids.download((n1,), np.int32)
+    bad1 = int(np.sum(got_ids != exp["ids"][rows]))
+    parity_report.record("config C1 (k_wave_row, one row per launch)", n1, bad1, int(edge[rows].sum()))
+    assert np.array_equal(got_ids, exp["ids"][rows])
+    assert np.array_equal(cand.download((n1, K), np.int32), exp["cand"][rows])
+    assert np.array_equal(probs.download((n1, K), np.float32), exp["probs"][rows])
+    for b in (bl, bu, ids, probs, cand):
+        b.free()
 
 
 @pytest.mark.parametrize("flags", [1, 2, 4, 6, 5])
