@@ -170,14 +170,64 @@ def traffic_probe(pool, g, n):
     log(f"traffic probe: 1 copy of {nbytes} B, {n} launches of {g} C3 batches")
 
 
-def counter_probe(name, pool, g_head):
-    """For rocprofv3 --pmc runs: launches of one workload only, each followed by
-    a synchronisation, so every dispatch in the profile is that workload's.
-    c1: 200 single C1 rows; c3one: 50 one-batch C3 launches; c3: 20 headline
-    launches (g_head batches each); c4 / c5: 20 launches of C4 / C5."""
+def calibration_copy():
+    """One 256 MiB device-to-device copy: the dispatch of known traffic (256 MiB
+    read, 256 MiB written) that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    import hiprt
+    nbytes = 256 << 20
+    src, dst = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
+    hiprt.synchronize()
+    hiprt.check(hiprt.hip().hipMemcpyAsync(dst.ptr, src.ptr, nbytes, hiprt.D2D, None), "copy")
+    hiprt.synchronize()
+    src.free()
+    dst.free()
+    return nbytes
+
+
+def head_probe(one_launch, n=20):
+    """The backbone head's gemv and its sample (bf16 [1, 2048] x [4097, 2048],
+    k 30): n calls of d3s_linear_sample_bf16, two launches (k_linear, then
+    k_wave_row) or one (k_head), each followed by a synchronisation, the
+    weights rotating over 8 copies."""
     import d3s
     import d3s_workloads as W
     import hiprt
+    K, Vh, copies = 2048, 4097, 8
+    rng = np.random.default_rng(11)
+    x = W.f32_to_bf16_bits(rng.standard_normal((1, K)).astype(np.float32))
+    w = W.f32_to_bf16_bits((rng.standard_normal((Vh, K)) * 0.06).astype(np.float32))
+    bx = hiprt.to_device(x)
+    bw = hiprt.DeviceBuffer(copies * w.nbytes)
+    for c in range(copies):
+        bw.upload(w, offset=c * w.nbytes)
+    y, u, ids = hiprt.DeviceBuffer(2 * Vh), hiprt.DeviceBuffer(4 * K_SAMPLE), hiprt.DeviceBuffer(16)
+    assert d3s.lib().d3s_uniform_fill(u.ptr, K_SAMPLE, 11, 0, None) == 0
+    hiprt.synchronize()
+    flags = d3s.FLAG_ONE_LAUNCH if one_launch else 0
+    for i in range(n):
+        assert d3s.lib().d3s_linear_sample_bf16(bx.ptr, bw.ptr + (i % copies) * w.nbytes, 1, K, Vh, y.ptr, u.ptr,
+                                                K_SAMPLE, None, None, 0.7, 0.7, ids.ptr, None, None, None, flags,
+                                                None) == 0
+        hiprt.synchronize()
+
+
+def counter_probe(name, pool, g_head):
+    """For rocprofv3 --pmc runs: the calibration copy, then launches of one
+    workload only, each followed by a synchronisation, so every other dispatch
+    in the profile is that workload's.  c1: 200 single C1 rows; c1rows /
+    c1long: 20 launches of 1024 C1 rows (one row per workgroup, k_wave_row) /
+    1025 (four rows per workgroup, k_wave); c2: 50 C2
+    launches (nine rows); c3one: 50 one-batch C3 launches; c3: 20 headline
+    launches (g_head batches each); c4 / c5: 20 launches of C4 / C5 (ids only);
+    head / head1: 20 backbone-head gemv + sample calls, two launches / one."""
+    import d3s
+    import d3s_workloads as W
+    import hiprt
+    calibration_copy()
+    if name in ("head", "head1"):
+        head_probe(name == "head1")
+        log(f"counter probe {name}: done")
+        return
     if name in ("c3", "c3one"):
         g = g_head if name == "c3" else 1
         ids = hiprt.DeviceBuffer(4 * ROWS * g)
@@ -186,8 +236,8 @@ def counter_probe(name, pool, g_head):
             hiprt.synchronize()
         log(f"counter probe {name}: done")
         return
-    cfg = {"c1": "C1", "c4": "C4", "c5": "C5"}[name]
-    w = W.make(cfg, rows=256 if name == "c1" else None, seed=5, uniforms=False)
+    cfg = {"c1": "C1", "c1rows": "C1", "c1long": "C1", "c2": "C2", "c4": "C4", "c5": "C5"}[name]
+    w = W.make(cfg, rows={"c1": 256, "c1rows": 1024, "c1long": 1025}.get(name), seed=5, uniforms=False)
     x = w["logits"]
     N, Vc = x.shape
     k = w["k"]
@@ -200,7 +250,7 @@ def counter_probe(name, pool, g_head):
     T, P = w["temperature"], w["top_p"]
     T = float(T) if np.ndim(T) == 0 else float(T[0])
     P = float(P) if np.ndim(P) == 0 else float(P[0])
-    for i in range(200 if name == "c1" else 20):
+    for i in range({"c1": 200, "c2": 50}.get(name, 20)):
         if name == "c1":
             r = i % N
             rc = d3s.sample_raw(lg.ptr + r * Vc * x.itemsize, dt, 1, Vc, Vc, u.ptr + r * k * 4, k, T, P,
@@ -718,7 +768,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the C2 / C4 / C5 figures")
-    ap.add_argument("--counter-probe", choices=["c1", "c3one", "c3", "c4", "c5"], default=None,
+    ap.add_argument("--counter-probe", choices=["c1", "c1rows", "c1long", "c2", "c3one", "c3", "c4", "c5", "head",
+                                                "head1"], default=None,
                     help="only run one workload's launches (for --pmc runs)")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="N",
                     help="only run the copy calibration and N headline launches (for --pmc runs)")
@@ -742,6 +793,9 @@ def main():
     if args.pool_batches % G:
         sys.exit("bench.py: --pool-batches must be a multiple of --batches-per-launch")
 
+    if args.counter_probe and args.counter_probe not in ("c3", "c3one"):
+        counter_probe(args.counter_probe, None, G)  # (needs no C3 pool)
+        return
     log("building the C3 batch pool")
     pool = Pool(args.pool_batches, 16)
     pool_mb = args.pool_batches * ROWS * BYTES_PER_ROW / 1e6

@@ -130,10 +130,46 @@ __device__ __forceinline__ uint64_t composite_key(float x, int idx) {
 __device__ __forceinline__ float key_x(uint64_t key) { return d3s_from_ordkey((uint32_t)(key >> 32)); }
 __device__ __forceinline__ int key_idx(uint64_t key) { return (int)(~(uint32_t)key); }
 
+/* The SampleArgs fields a row's first instructions need (its address and
+ * width, the banned index, the temperature, the uniforms, k and the flags),
+ * passed again as leading scalar kernel arguments ahead of the SampleArgs
+ * block.  gfx950
+ * preloads leading non-aggregate kernel arguments into SGPRs at wave launch
+ * (kernarg preloading, 14 SGPRs here: -amdgpu-kernarg-preload-count in the
+ * Makefile), so the row's loads issue at once instead of after the
+ * kernarg segment's round trip (~2.6k cycles measured at batch 1); the
+ * block's other fields arrive by s_load meanwhile.  56 bytes, no padding. */
+#define D3S_HOT_PARAMS                                                                                    \
+  const void *hot_logits, int64_t hot_stride, const int32_t *hot_banned, const float *hot_temperature,    \
+      const float *hot_u, float hot_T, int hot_vocab, int hot_k, unsigned hot_flags
+#define D3S_HOT_ARGS(a)                                                                                   \
+  (a).logits, (a).row_stride, (a).banned, (a).temperature, (a).u, (a).temperature_scalar, (a).vocab,     \
+      (a).k, (a).flags
+/* a's copies of the leading arguments replaced by them (the same values) */
+#define D3S_HOT_APPLY(a)                                                                                  \
+  do {                                                                                                    \
+    (a).logits = hot_logits;                                                                              \
+    (a).row_stride = hot_stride;                                                                          \
+    (a).banned = hot_banned;                                                                              \
+    (a).temperature = hot_temperature;                                                                    \
+    (a).u = hot_u;                                                                                        \
+    (a).temperature_scalar = hot_T;                                                                       \
+    (a).vocab = hot_vocab;                                                                                \
+    (a).k = hot_k;                                                                                        \
+    (a).flags = hot_flags;                                                                                \
+  } while (0)
+
 struct RowP {
   float T, top_p;
   int banned;
 };
+
+/* the row's top_p alone: kernels whose first steps must not wait on the
+ * kernarg segment read it after them (the other fields of row_params are
+ * leading kernel arguments) */
+__device__ __forceinline__ float row_top_p(const SampleArgs &a, int row) {
+  return a.top_p ? a.top_p[row] : a.top_p_scalar;
+}
 
 __device__ __forceinline__ RowP row_params(const SampleArgs &a, int row) {
   RowP p;

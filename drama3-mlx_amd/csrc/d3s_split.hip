@@ -119,9 +119,21 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+/* The leading scalar arguments (preloaded into SGPRs at wave launch): the
+ * fields a segment's loads and first steps need, and nseg, which places the
+ * segment; 48 bytes.  The SampleArgs block's copies are replaced by them. */
 template <int CPT, bool BF16>
-__global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *counters_ws, uint64_t *records,
-                                                   int nseg, int rec_words) {
+__global__ __launch_bounds__(SPLIT_T) void k_split(const void *hot_logits, int64_t hot_stride,
+                                                   const int32_t *hot_banned, const float *hot_temperature,
+                                                   float hot_T, int hot_vocab, int hot_k, int nseg, SampleArgs a,
+                                                   uint32_t *counters_ws, uint64_t *records, int rec_words) {
+  a.logits = hot_logits;
+  a.row_stride = hot_stride;
+  a.banned = hot_banned;
+  a.temperature = hot_temperature;
+  a.temperature_scalar = hot_T;
+  a.vocab = hot_vocab;
+  a.k = hot_k;
   using C = Chunks<CPT, BF16>;
   constexpr int ES = BF16 ? 2 : 4, EPC = C::EPC, NV = C::NV;
   constexpr int CAP = SPLIT_NW * CPT * WAVE; /* chunks per segment */
@@ -133,11 +145,6 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   const int V = a.vocab, k = a.k;
   int kpow = 2;
   while (kpow < k) kpow <<= 1;
-  const RowP rp = row_params(a, row);
-  const float T = rp.T, top_p = rp.top_p;
-  const int banned = rp.banned;
-  const bool t_finite = T < __builtin_inff(); /* false for +inf and NaN */
-  const float y = 1.0f / T;
   const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
   const int off = (int)(((uintptr_t)rowp & 15u) / ES);
   const uint4 *src = (const uint4 *)(rowp - off * ES);
@@ -153,6 +160,13 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(SampleArgs a, uint32_t *count
   const int vend = min(V, wend * EPC - off);                         /* past its last position */
   C c;
   c.load(src + cbase, min(max(wend - cbase, 0), CPT * WAVE), lane);
+  /* the row's parameters after its loads are issued (these may wait on the
+   * kernarg segment) */
+  const RowP rp = row_params(a, row);
+  const float T = rp.T, top_p = rp.top_p;
+  const int banned = rp.banned;
+  const bool t_finite = T < __builtin_inff(); /* false for +inf and NaN */
+  const float y = 1.0f / T;
   const int pos0 = (cbase + lane) * EPC - off;
   auto valid = [&](int i) { return (unsigned)C::pos(pos0, i) < (unsigned)vend; };
 #pragma unroll
@@ -492,8 +506,9 @@ bool try_split(const SampleArgs &a, int nseg, void *ws, size_t ws_bytes, hipStre
   const int rec_words = 2 + a.k; /* header, then the keys by rank */
   const size_t need = SPLIT_CNT_BYTES + (size_t)a.n_rows * nseg * rec_words * 8;
   if (!ws || need > ws_bytes) return false;
-  hipLaunchKernelGGL((k_split<CPT, BF16>), dim3((unsigned)(a.n_rows * nseg)), dim3(SPLIT_T), 0, s, a,
-                     (uint32_t *)ws, (uint64_t *)((char *)ws + SPLIT_CNT_BYTES), nseg, rec_words);
+  hipLaunchKernelGGL((k_split<CPT, BF16>), dim3((unsigned)(a.n_rows * nseg)), dim3(SPLIT_T), 0, s, a.logits,
+                     a.row_stride, a.banned, a.temperature, a.temperature_scalar, a.vocab, a.k, nseg, a,
+                     (uint32_t *)ws, (uint64_t *)((char *)ws + SPLIT_CNT_BYTES), rec_words);
   return true;
 }
 

@@ -234,15 +234,8 @@ struct WaveRow {
     return RowRef{a.counters, &S, src, nchunks, pos0, V, k, lane, banned, T, y, t_finite};
   }
 
-  /* the row's parameters and where its chunks lie */
+  /* where the row's chunks lie (from the row's address and width alone) */
   __device__ __forceinline__ void setup() {
-    const RowP rp = row_params(a, row);
-    T = rp.T;
-    top_p = rp.top_p;
-    banned = rp.banned;
-    t_finite = T < __builtin_inff(); /* false for +inf and NaN */
-    y = 1.0f / T;
-    uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
     /* a chunk never crosses a page, so the bytes outside the row it covers
      * are readable; they become -inf below */
     rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * ES;
@@ -252,13 +245,43 @@ struct WaveRow {
     pos0 = lane * EPC - off;
   }
 
+  /* one dword of a row-indexed array by a vector load (a VGPR, read into a
+   * scalar only where it is used): waiting for it counts vector loads only
+   * (issued in order), never the kernarg segment's scalar loads in flight */
+  __device__ __forceinline__ uint32_t row_word(const void *base) const {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (row + 1) * 4, BUFFER_FLAGS);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, 0, row * 4, 0);
+  }
+
+  /* the row's temperature, banned index and uniform (top_p, which only the
+   * tail needs, later), loaded before the row so that waiting for them does
+   * not wait for it; params_done() takes them once the row's loads are out */
+  uint32_t t_word, b_word;
+  __device__ __forceinline__ void params() {
+    t_word = a.temperature ? row_word(a.temperature) : d3s_f2u(a.temperature_scalar);
+    b_word = a.banned ? row_word(a.banned) : 0xffffffffu;
+    uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
+  }
+  __device__ __forceinline__ void params_done() {
+    const float t = d3s_u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)t_word));
+    T = t < 1e-5f ? 1e-5f : t; /* src/sampling.c:16,195 */
+    banned = __builtin_amdgcn_readfirstlane((int)b_word);
+    t_finite = T < __builtin_inff(); /* false for +inf and NaN */
+    y = 1.0f / T;
+  }
+
   __device__ __forceinline__ void load() {
+    /* every operand these loads need is a leading kernel argument (preloaded
+     * into SGPRs): nothing here waits on the kernarg segment */
     setup();
+    params();
     /* rows taken once (candidates from the registers) stream past the caches */
     if (reg_cands)
       c.template load<2>(src, nchunks, lane);
     else
       c.load(src, nchunks, lane);
+    params_done();
     /* the partial chunk at the row start and every chunk row from the one
      * holding the row end on */
     const int jlast = (nchunks - 1) / WAVE;
@@ -326,6 +349,7 @@ struct WaveRow {
   /* every quantity per element from x = L / T, as the oracle (T not finite,
    * or logits too large for the fast row sum) */
   __device__ __forceinline__ int slow_row() {
+    top_p = row_top_p(a, row);
     const RowRef R = ref();
     const float M = slow_max<CPT, BF16>(R);
     if (d3s_isnan(M) || M == -__builtin_inff()) return wave_write_special(a, row, !d3s_isnan(M));
@@ -359,6 +383,11 @@ struct WaveRow {
      * lower bound: at least k elements reach it), by ballot radix search */
     bool need_sel = (a.flags & FLAG_EXACT_SELECT) != 0;
     const uint32_t pre = wave_kth_prefix(d3s_ordkey(lm), (uint32_t)k);
+    /* top_p now (the kernarg segment has arrived by this step); the fence
+     * keeps its load from moving up to where a wait for it would stall the
+     * row's first steps */
+    asm volatile("" ::: "memory");
+    top_p = row_top_p(a, row);
     /* keys below -FLT_MAX's: the k-th lane max is -inf */
     if (pre < d3s_ordkey(-0x1.fffffep127f)) need_sel = true;
     const float tau = d3s_from_ordkey(pre);
@@ -904,7 +933,8 @@ void k_ras(RasArgs ra) {
  * tail again with it. */
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
-void k_wave_row(SampleArgs a) {
+void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
+  D3S_HOT_APPLY(a);
   __shared__ WaveLds lds;
   __shared__ uint32_t need;
   __shared__ float m_sh;
@@ -958,7 +988,8 @@ __global__ __launch_bounds__(WAVE *WR) void k_ras_select(RasArgs ra, const int32
 
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
-void k_wave(SampleArgs a) {
+void k_wave(D3S_HOT_PARAMS, SampleArgs a) {
+  D3S_HOT_APPLY(a);
   __shared__ WaveLds lds_all[WR];
   /* wave-uniform (the compiler cannot see it): row and all that follows stay scalar */
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
@@ -996,9 +1027,10 @@ bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
    * over more CUs, with three helper waves for the exact lse; larger ones
    * pack WR rows, which keeps the CUs fuller */
   if (a.n_rows <= WR_SPREAD_ROWS)
-    hipLaunchKernelGGL((k_wave_row<CPT, BF16>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s, a);
+    hipLaunchKernelGGL((k_wave_row<CPT, BF16>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s, D3S_HOT_ARGS(a), a);
   else
-    hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3((unsigned)((a.n_rows + WR - 1) / WR)), dim3(WAVE * WR), 0, s, a);
+    hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3((unsigned)((a.n_rows + WR - 1) / WR)), dim3(WAVE * WR), 0, s,
+                       D3S_HOT_ARGS(a), a);
   return true;
 }
 
