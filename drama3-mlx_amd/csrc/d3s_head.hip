@@ -165,7 +165,7 @@ __global__ __launch_bounds__(HEAD_T) void k_head(LinearArgs la, SampleArgs a, ui
       st_agent(rec, (uint64_t)d3s_f2u(Ls) | ((uint64_t)d3s_f2u(ssum) << 32));
       st_agent(rec + 1, (uint64_t)flags);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* the records retired before the count (see st_agent) */
     if (lane == 0) {
       uint32_t *cnt_row = counters_ws + (size_t)row * HEAD_CLINES * 32; /* 32 words = 128 bytes */
       const int g = seg / HEAD_GRP, ng = (nseg + HEAD_GRP - 1) / HEAD_GRP;

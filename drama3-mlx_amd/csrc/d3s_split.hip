@@ -349,7 +349,7 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(const void *hot_logits, int64
   }
 
   /* ---- publish the record: agent-coherent stores, completed before the
-   * arrival is counted */
+   * arrival is counted (the ordering argument is at st_agent) */
   uint64_t *rec = records + ((size_t)row * nseg + seg) * rec_words;
   if (threadIdx.x < nfiled) st_agent(rec + 2 + threadIdx.x, S.ranked[threadIdx.x]);
   if (threadIdx.x == 0) {

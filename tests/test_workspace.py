@@ -342,3 +342,50 @@ def test_stream_block_release(gpu, oracle):
         assert gpu.lib().d3s_stream_workspace_release(s.ptr) == 0
     assert gpu.lib().d3s_stream_workspace_release(s.ptr) == 0  # nothing left: still fine
     s.destroy()
+
+
+@pytest.mark.gpu
+def test_stream_block_shared_by_threads(gpu, oracle):
+    """Two host threads on one stream, one with calls the segmented kernel takes
+    (a 1 MiB block), the other with calls the sorting kernels take (k = V =
+    20 000, a block of several MiB): the stream's block grows while the other
+    thread may be enqueueing on the old one, which is kept, not freed. Every
+    call's ids equal the oracle's."""
+    import threading
+    import hiprt
+    rng = np.random.default_rng(96)
+    c4 = W.make("C4", rows=16, seed=96, uniforms=False)["logits"]
+    big = (rng.standard_normal((8, 20000)) * 2.0).astype(np.float32)
+    cases = [(c4, 30, 1, 1.0, 0.9), (big, 20000, 0, 1.0, 0.9)]
+    s = hiprt.Stream()
+    errors = []
+
+    def worker(x, k, dt, T, top_p, reps):
+        try:
+            N, V = x.shape
+            u = oracle.uniform(97, 0, N, k)
+            exp = oracle.sample(x, u, T, top_p, n_threads=4, detail=False)["ids"]
+            bx, bu, ids = hiprt.to_device(x), hiprt.to_device(u), hiprt.DeviceBuffer(4 * N)
+            for rep in range(reps):
+                rc = gpu.sample_raw(bx.ptr, dt, N, V, V, bu.ptr, k, T, top_p, None, ids.ptr, stream=s.ptr)
+                if rc != 0:
+                    errors.append(("rc", V, rep, rc))
+                    return
+                s.synchronize()
+                got = ids.download((N,), np.int32)
+                if not np.array_equal(got, exp):
+                    errors.append(("ids", V, rep))
+            for b in (bx, bu, ids):
+                b.free()
+        except Exception as e:  # reported below
+            errors.append(("exception", repr(e)))
+
+    threads = [threading.Thread(target=worker, args=c + (10,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert gpu.lib().d3s_stream_workspace_release(s.ptr) == 0
+    s.destroy()
+    banner(f"two threads on one stream: errors {errors}")
+    assert not errors, errors
