@@ -223,6 +223,12 @@ struct WaveRow {
   /* the candidates from the registers (staged in LDS) instead of read again
    * from L2: long launches, whose rows leave L2 before a second read */
   bool reg_cands = false;
+  /* k_wave_row: the fast lse' and its bound come from the workgroup's helper
+   * wave (lse_in: the two floats it files), read after a workgroup barrier
+   * that wave 0 passes on the way to the tail; `synced` says whether it did
+   * (the rows that end earlier pass it in the kernel) */
+  const float *lse_in = nullptr;
+  bool synced = false;
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -357,6 +363,60 @@ struct WaveRow {
     return finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, -d3s_logf(1.0f - uval), true);
   }
 
+  /* The fast row sum S' = sum 2^(L c + b) over the row (b = -RN(Lmax c)),
+   * lse' = M + ln 2 (log2 S' - delta) (delta = Lmax c + b exactly) and eps_s,
+   * the bound on |lse' - lse| less the final roundings: the relative error of
+   * 2^-delta S' against the exact row sum (the rounding of x, m, x - m and
+   * log2(e)/T, the fast exponent's error, d3s_expf's, the terms below e^-40,
+   * the fixed-point truncation, the accumulation's CPT + 3 + 6 roundings and
+   * the final one), then the log: twice its bound, times ln 2, with the
+   * product's rounding. */
+  __device__ __forceinline__ void fast_lse(float M, float cf, float b, float delta, float &lse, float &eps_s) {
+    if (BF16) c.launder();
+    float acc[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(c.val(i), cf, b));
+#pragma unroll
+    for (int w = EPC / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
+    const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
+    /* the hardware log2, within 2^-23 |log2 sp| + 2^-24 (checked by the tests) */
+    const float l2 = __builtin_amdgcn_logf(sp);
+    lse = M + (l2 * LN2_F - delta * LN2_F);
+    eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f + (float)(CPT + 11) * 0x1p-24f +
+            (float)V * 0x1p-40f + 0x1p-22f * fabsf(l2) + 0x1p-23f;
+  }
+
+  /* k_wave_row's helper wave: the row's max as compute() takes it, then
+   * fast_lse, filed at out[0..1] for wave 0.  Rows that compute() ends
+   * before its tail (refused, all -inf, T not finite, logits too large for
+   * the fast sum: the same tests on the same values) file nothing. */
+  __device__ __forceinline__ void helper_lse(float *out) {
+    if (!t_finite) return;
+    const float ninf = -__builtin_inff();
+    const float cf = LOG2E_F / T;
+    float lm = ninf;
+#pragma unroll
+    for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
+    const float Lmax = wave_maximum_f(lm);
+    if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) return;
+    const float M = scale_logit(Lmax, T, y, true);
+    if (M == __builtin_inff() || M == ninf) return;
+    const float h = Lmax * cf;
+    if (!(fabsf(h) < 0x1p24f)) return;
+    const float b = -h;
+    const float delta = __builtin_fmaf(Lmax, cf, b);
+    float lse, eps_s;
+    fast_lse(M, cf, b, delta, lse, eps_s);
+    if (lane == 0) {
+      out[0] = lse;
+      out[1] = eps_s;
+    }
+  }
+
   /* the row, once loaded (and masked), to its id */
   __device__ __forceinline__ int compute() {
     const float ninf = -__builtin_inff();
@@ -457,29 +517,9 @@ struct WaveRow {
       }
     }
 
-    /* ---- the fast row sum */
-    if (BF16) c.launder();
-    float acc[EPC];
-#pragma unroll
-    for (int e = 0; e < EPC; e++) acc[e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NV; i++) acc[i % EPC] += __builtin_amdgcn_exp2f(__builtin_fmaf(c.val(i), cf, b));
-#pragma unroll
-    for (int w = EPC / 2; w >= 1; w /= 2)
-#pragma unroll
-      for (int e = 0; e < w; e++) acc[e] = acc[e] + acc[e + w];
-    const float sp = wave_sum_f(acc[0]); /* >= 2^delta, about 1 */
-    /* the hardware log2, within 2^-23 |log2 sp| + 2^-24 (checked by the tests) */
-    const float l2 = __builtin_amdgcn_logf(sp);
-    const float lse = M + (l2 * LN2_F - delta * LN2_F);
-    /* bound on |lse' - lse|, less the final roundings: the relative error of
-     * 2^-delta S' against the exact row sum (the rounding of x, m, x - m and
-     * log2(e)/T, the fast exponent's error, d3s_expf's, the terms below e^-40,
-     * the fixed-point truncation, the accumulation's CPT + 3 + 6 roundings and
-     * the final one), then the log: twice its bound, times ln 2, with the
-     * product's rounding */
-    const float eps_s = 0x1p-24f * (2.0f * fabsf(M) + 160.0f) + EPS_EXP2 + 0x1p-23f +
-                        (float)(CPT + 11) * 0x1p-24f + (float)V * 0x1p-40f + 0x1p-22f * fabsf(l2) + 0x1p-23f;
+    /* ---- the fast row sum (here, or on the helper wave) */
+    float lse = 0.0f, eps_s = 0.0f;
+    if (!lse_in) fast_lse(M, cf, b, delta, lse, eps_s);
 
     int n;
     if (need_sel) {
@@ -542,6 +582,12 @@ struct WaveRow {
         if (q < cnt) S.keys[excl + q] = composite_key(scale_logit(read_logit(p), T, y, true), p);
       }
       n = (int)tot;
+    }
+    if (lse_in) {
+      __syncthreads(); /* the helper wave files lse' before it arrives */
+      synced = true;
+      lse = lse_in[0];
+      eps_s = lse_in[1];
     }
     return finish(n, M, lse, false, eps_s, noise, need_sel);
   }
@@ -927,10 +973,15 @@ void k_ras(RasArgs ra) {
 }
 
 /* k_wave for small launches: one row per 4-wave workgroup.  Wave 0 samples
- * the row as k_wave's waves do; the other three wait, and join only when the
- * cut needs the exact lse: the row's 2^-40 fixed-point sum of d3s_expf(x - M)
- * by all four (an integer sum, the same in any order), then wave 0 runs the
- * tail again with it. */
+ * the row as k_wave's waves do, except for the fast row sum: wave 1 loads the
+ * row too (its loads meet wave 0's in L2) and takes the max and the fast sum
+ * while wave 0 runs the threshold, the candidates and their filing; wave 0
+ * reads lse' after a barrier just before its tail.  Waves 2 and 3 wait, and
+ * all four join when the cut needs the exact lse: the row's 2^-40 fixed-point
+ * sum of d3s_expf(x - M) (an integer sum, the same in any order), then wave 0
+ * runs the tail again with it.  Every wave passes two barriers before the
+ * exact sum: wave 0 the first in compute() (or here, on rows that end
+ * earlier), the others here. */
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
 void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
@@ -939,21 +990,30 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   __shared__ uint32_t need;
   __shared__ float m_sh;
   __shared__ uint32_t s_lo[WR], s_hi[WR];
+  __shared__ float lse_sh[2];
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id();
   const int row = (int)blockIdx.x;
   WaveRow<CPT, BF16> r(a, lds, row);
+  r.V = a.vocab;
+  r.k = a.k;
+  r.lane = lane;
   if (wid == 0) {
-    r.V = a.vocab;
-    r.k = a.k;
-    r.lane = lane;
     r.defer_exact = true;
+    r.lse_in = lse_sh;
     r.load();
     const int id = r.compute();
     if (lane == 0) {
       need = id == NEED_EXACT ? 1u : 0u;
       m_sh = r.fin_M;
     }
+    if (!r.synced) __syncthreads();
+  } else {
+    if (wid == 1) {
+      r.load();
+      r.helper_lse(lse_sh);
+    }
+    __syncthreads();
   }
   __syncthreads();
   if (!need) return;
