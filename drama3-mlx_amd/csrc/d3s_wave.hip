@@ -947,28 +947,39 @@ __device__ __forceinline__ void ras_pick(const RasArgs &ra, int row, int id1, in
  * waves of a workgroup take one row: the first samples it with the caller's
  * parameters, the second with the retry's, side by side (the second's loads
  * of the row meet the first's in L2, so HBM reads it once).  Then the first
- * wave picks the main token (ras_pick). */
+ * wave picks the main token (ras_pick).  helpers (launches of one row per
+ * workgroup): waves 2 and 3 take the fast row sums of waves 0 and 1 (the
+ * draws' temperatures differ), as k_wave_row's wave 1 does; every wave then
+ * passes one barrier before the draws' tails.  Otherwise a workgroup of four
+ * waves takes two rows. */
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
-void k_ras(RasArgs ra) {
+void k_ras(RasArgs ra, int helpers) {
   __shared__ WaveLds lds_all[WR];
   __shared__ int drawn[WR];
+  __shared__ float lse_sh[2][2];
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
-  const int row = (int)(blockIdx.x * (blockDim.x / WAVE / 2)) + wid / 2;
+  const int row = helpers ? (int)blockIdx.x : (int)(blockIdx.x * (blockDim.x / WAVE / 2)) + wid / 2;
   const bool retry = (wid & 1) != 0;
   const int lane = lane_id();
-  if (row < ra.first.n_rows) {
-    const SampleArgs &a = retry ? ra.retry : ra.first;
-    WaveRow<CPT, BF16> r(a, lds_all[wid], row);
-    r.V = a.vocab;
-    r.k = a.k;
-    r.lane = lane;
+  const SampleArgs &a = retry ? ra.retry : ra.first;
+  WaveRow<CPT, BF16> r(a, lds_all[wid], row);
+  r.V = a.vocab;
+  r.k = a.k;
+  r.lane = lane;
+  if (helpers && wid >= 2) {
+    r.load();
+    r.helper_lse(lse_sh[wid & 1]);
+    __syncthreads();
+  } else if (row < ra.first.n_rows) {
+    if (helpers) r.lse_in = lse_sh[wid & 1];
     r.load();
     const int id = r.compute();
     if (lane == 0) drawn[wid] = id;
+    if (helpers && !r.synced) __syncthreads();
   }
   __syncthreads();
-  if (retry || row >= ra.first.n_rows) return;
+  if (retry || (helpers && wid >= 2) || row >= ra.first.n_rows) return;
   ras_pick(ra, row, drawn[wid], drawn[wid + 1]);
 }
 
@@ -1124,10 +1135,12 @@ void launch_exp2_selftest(const float *in, float *out, int64_t n, hipStream_t s)
 template <int CPT, bool BF16>
 bool try_ras(const RasArgs &r, int max_off, hipStream_t s) {
   if (r.first.vocab > wave_vmax<CPT, BF16>(max_off)) return false;
-  /* two waves per row: one row per workgroup for small launches, two otherwise */
+  /* two waves per row: for small launches one row per workgroup with two
+   * helper waves, otherwise two rows per workgroup */
   const int n = r.first.n_rows;
   const int rpw = n <= WR_SPREAD_ROWS ? 1 : WR / 2;
-  hipLaunchKernelGGL((k_ras<CPT, BF16>), dim3((unsigned)((n + rpw - 1) / rpw)), dim3(WAVE * 2 * rpw), 0, s, r);
+  hipLaunchKernelGGL((k_ras<CPT, BF16>), dim3((unsigned)((n + rpw - 1) / rpw)), dim3(WAVE * WR), 0, s, r,
+                     rpw == 1 ? 1 : 0);
   return true;
 }
 
