@@ -123,6 +123,14 @@ __device__ __forceinline__ void wave_argmax(float &s, int &r) {
   r = (int)readlane_u((uint32_t)r, 63);
 }
 
+/* The lane of the first maximum of the wave's scores (never NaN): the
+ * greatest score by a DPP maximum, then the lowest lane holding it.  The
+ * same lane as wave_argmax(s, lane) gives, with half its steps. */
+__device__ __forceinline__ int wave_first_max_lane(float s) {
+  const float m = wave_max_f(s);
+  return (int)__builtin_ctzll(__ballot(s == m));
+}
+
 __device__ __forceinline__ uint64_t composite_key(float x, int idx) {
   /* larger key = earlier rank: larger x, then the smaller index */
   return ((uint64_t)d3s_ordkey(x) << 32) | (uint64_t)(uint32_t)(~(uint32_t)idx);
@@ -293,8 +301,7 @@ __device__ __forceinline__ void wave_tail_finish(const SampleArgs &a, int row, f
     const float score = p / noise;
     sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
   }
-  int best = lane;
-  wave_argmax(sc, best);
+  const int best = wave_first_max_lane(sc);
   const int id = (int)readlane_u((uint32_t)idx, best);
   if (lane == 0) a.ids[row] = id;
   if (act) {
@@ -369,8 +376,7 @@ __device__ __forceinline__ void wave_race(const SampleArgs &a, int row, int idx,
     const float score = p / noise;
     sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
   }
-  int best = lane;
-  wave_argmax(sc, best);
+  const int best = wave_first_max_lane(sc);
   const int id = (int)readlane_u((uint32_t)idx, best);
   if (lane == 0) a.ids[row] = id;
   if (act) {

@@ -71,7 +71,11 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
  * readlane (a scalar broadcast), so the chain is one add per term. */
 __device__ __forceinline__ float wave_seq_sum_rl(float e, int n) {
   float s = 0.0f;
-  for (int r = 0; r < n; r++) s = s + readlane_f(e, r);
+#pragma unroll
+  for (int r = 0; r < WAVE; r++) {
+    if (r >= n) break;
+    s = s + readlane_f(e, r);
+  }
   return s;
 }
 
@@ -87,8 +91,7 @@ __device__ __forceinline__ int wave_race_p(const SampleArgs &a, int row, int idx
     const float score = p / noise;
     sc = score > -1.0f ? score : -1.0f; /* NaN, -inf and <= -1 never beat best = -1 */
   }
-  int best = lane;
-  wave_argmax(sc, best);
+  const int best = wave_first_max_lane(sc);
   const int id = (int)readlane_u((uint32_t)idx, best);
   if (lane == 0 && a.ids) a.ids[row] = id;
   if (act) {
