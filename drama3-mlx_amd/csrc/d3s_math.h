@@ -245,18 +245,17 @@ D3S_HD uint64_t d3s_fix40_unit(float e) {
 
 /* d3s_fix40(d3s_expf(z)) for z <= 0 (or -0, or -inf), without forming the
  * fp32 result: exp's polynomial value p lies in [2^-1/2, 2^1/2], so p * 2^24
- * is an integer below 2^25 and floor(p * 2^n * 2^40) is that integer shifted
- * by n + 16 (results below 2^-126 give 0 either way).  Same bits as the
- * two-step form; fewer instructions for the per-element row sum. */
+ * is an integer P below 2^25 and floor(p * 2^n * 2^40) = floor(P * 2^(n + 16))
+ * = (P * 2^16) >> -n (n <= 0; a shift past 40 leaves 0, as do results below
+ * 2^-126 either way): one 64-bit shift.  Same bits as the two-step form;
+ * fewer instructions for the per-element row sum. */
 D3S_HD uint64_t d3s_fix40_exp(float z) {
   const float zc = fmaxf(z, -0x1.a0p+6f); /* [-104, 0]; -inf -> -104 */
   float n;
   const float p = d3s_exp_core(zc, &n);
-  const uint64_t P = (uint64_t)(uint32_t)(p * 0x1.0p+24f);
-  const int sh = (int)n + 16; /* <= 16 */
-  const uint64_t left = P << (sh > 0 ? sh : 0);
-  const uint64_t right = P >> (sh < 0 ? (-sh > 63 ? 63 : -sh) : 0);
-  return sh >= 0 ? left : right;
+  const uint64_t P16 = (uint64_t)(uint32_t)(p * 0x1.0p+24f) << 16; /* below 2^41 */
+  const int sh = -(int)n;                                            /* 0 <= sh <= 151 */
+  return P16 >> (sh < 63 ? sh : 63);
 }
 
 /* uint64 -> fp32, round to nearest, ties to even (integer steps only). */
