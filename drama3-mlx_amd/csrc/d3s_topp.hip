@@ -590,25 +590,40 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     const int r = q * TBLOCK + tid;
     uv[q] = a.u[(size_t)row * k + (r < k ? r : k - 1)]; /* (r >= k: unused) */
   }
-  float hb0[EPT];
-  float lbm = -1.0f;
+  /* LB1, the largest first lower bound over the certainly kept ranks: lb
+   * decreases in u where it is defined (2^-24 <= u < 1; -1 elsewhere), so a
+   * thread's is the lb of its least such u (one evaluation, not one a rank) */
+  float umin = 1.0f;
 #pragma unroll
   for (int q = 0; q < EPT; q++) {
     const int r = q * TBLOCK + tid;
-    hb0[q] = -__builtin_inff();
-    if (r < khi) {
-      float lb, h;
-      topp_sbounds(emin, 1.0f, uv[q], lb, h);
-      hb0[q] = h;
-      if (r < klo) lbm = fmaxf(lbm, lb);
-    }
+    if (r < klo && uv[q] >= 0x1p-24f) umin = fminf(umin, uv[q]);
+  }
+  float lbm = -1.0f;
+  if (umin < 1.0f) {
+    float h_unused;
+    topp_sbounds(emin, 1.0f, umin, lbm, h_unused);
   }
   const float LB1 = block_max_f(lbm, R);
-  /* the ranks whose first upper bound reaches LB1, to one wave */
+  /* the ranks whose first upper bound (h = +inf for u <= 2^-24, rcp(u - 2^-24)
+   * (1 + 2^-18)(1 + 2^-20) below 1, 0 from 1 on) reaches LB1, to one wave.
+   * For LB1 > 0 that is u <= 2^-24 + C / LB1 with C within 1.0000004 (the
+   * rcp's ulp included): the test u <= uthr with 1.01 in C's place takes a
+   * superset, which the refinement below settles.  For LB1 <= 0 every rank
+   * that may be kept. */
   {
     uint32_t pm = 0u;
+    if (LB1 > 0.0f) {
+      const float uthr = 0x1p-24f + (1.0f / LB1) * 1.01f;
 #pragma unroll
-    for (int q = 0; q < EPT; q++) pm |= (hb0[q] >= LB1 ? 1u : 0u) << q;
+      for (int q = 0; q < EPT; q++) {
+        const int r = q * TBLOCK + tid;
+        pm |= (r < khi && uv[q] < 1.0f && uv[q] <= uthr ? 1u : 0u) << q;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < EPT; q++) pm |= (q * TBLOCK + tid < khi ? 1u : 0u) << q;
+    }
     int slot = wave_append_mask(pm, (int *)&misc[3]);
 #pragma unroll
     for (int q = 0; q < EPT; q++)
@@ -1247,16 +1262,19 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
   const float dmax = m - xmin;
   const float scale = (dmax > 0.0f && dmax < __builtin_inff()) ? (float)(NBK - 1) / dmax : 0.0f;
 
-  /* ---- 2'. each element's bucket count and its group's sum of fix40(e)
-   * (elements past the row count in the spare slot NBK + 1 and add 0 to a
-   * sum past the groups') */
+  /* ---- 2'. each element's bucket count and its group's sum of fix40(e).
+   * Elements past the row hold x = -inf: they count in the -inf bucket NBK,
+   * whose count nothing reads (its start is the finite total and it runs to
+   * the row's end), and add 0 to a sum past the groups'.  The bucket comes
+   * from d = x - m, as (m - x) scale = d (-scale) exactly. */
   if (scale > 0.0f) {
+    const float nscale = -scale;
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
-      const uint64_t f = d3s_fix40_exp(x[j] - m); /* fix40(expf(x - m)), 0 for -inf */
-      const int b = topp_bucket_of<NBK>(x[j], m, scale);
-      atomicAdd(&bstart[i < V ? b : NBK + 1], 1u);
+      const float d = x[j] - m;
+      const uint64_t f = d3s_fix40_exp(d); /* fix40(expf(x - m)), 0 for -inf */
+      const int b = (int)fminf(d * nscale, (float)NBK);
+      atomicAdd(&bstart[b], 1u);
       atomicAdd((unsigned long long *)&((uint64_t *)dyn)[(uint32_t)b / PER], (unsigned long long)f);
     }
     __syncthreads(); /* the counts and sums in (the row sum S is their total) */
