@@ -467,6 +467,16 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   /* thread t takes the uniforms of ranks q TBLOCK + t (q < EPT): read
    * coalesced */
 
+  /* this thread's ranks' uniforms, issued before the scan (not with the row:
+   * fewer registers live through the counting); the scan and the bands
+   * cover their wait */
+  float uv[EPT];
+#pragma unroll
+  for (int q = 0; q < EPT; q++) {
+    const int r = q * TBLOCK + tid;
+    uv[q] = a.u[(size_t)row * k + (r < k ? r : k - 1)]; /* (r >= k: unused) */
+  }
+
   /* ---- bucket starts, group prefixes and the row sum S, one scan */
   uint64_t gst, gs, S;
   {
@@ -581,14 +591,6 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       topp_ebounds<NBK>(gl * PER - 1, rs, dmax, emin, eh); /* the ranks before the range */
     else
       topp_ebounds<NBK>(bstart[NBK] < (uint32_t)V ? NBK : NBK - 1, rs, dmax, emin, eh); /* every rank */
-  }
-  /* this thread's ranks' uniforms, read here (not with the row: fewer
-   * registers live through the counting; other workgroups hide the wait) */
-  float uv[EPT];
-#pragma unroll
-  for (int q = 0; q < EPT; q++) {
-    const int r = q * TBLOCK + tid;
-    uv[q] = a.u[(size_t)row * k + (r < k ? r : k - 1)]; /* (r >= k: unused) */
   }
   /* LB1, the largest first lower bound over the certainly kept ranks: lb
    * decreases in u where it is defined (2^-24 <= u < 1; -1 elsewhere), so a
