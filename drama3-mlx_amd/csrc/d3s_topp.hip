@@ -59,6 +59,8 @@ struct TRed {
   float f[TNW], g[TNW], h[TNW];
   uint64_t s[TNW];
   uint64_t kept; /* the kept ranks' fixed-point sum */
+  uint64_t row_q[3]; /* the ids path's Tq and cut bands (wave 0's) */
+  float row_lse;
   uint32_t a[TNW];
   int r[TNW];
 };
@@ -508,21 +510,39 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       if (tot < (uint32_t)V) rmap[tot] = (uint16_t)(NBK + 1);
     }
   }
-  const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
-  const float lse = m + lnS;
-
-  /* ---- 4'. the cut's range [klo, khi]: the group whose prefix crosses the
-   * certain drop band (one thread's: the prefixes only grow) */
-  const uint64_t Tq = d3s_fixsum_gt_threshold(top_p);
+  /* ---- 4'. the row's lse, the least prefix above top_p (Tq) and the
+   * certain drop and keep bands: the same in every thread, so wave 0 alone
+   * computes them and files them in LDS while the other waves pass to the
+   * barrier; then the cut's range [klo, khi]: the group whose prefix crosses
+   * the certain drop band (one thread's: the prefixes only grow) */
+  if (tid < WAVE) {
+    const float lnS = d3s_logf(d3s_fixsum_to_f32(S));
+    const float lse0 = m + lnS;
+    const uint64_t Tq0 = d3s_fixsum_gt_threshold(top_p);
+    uint64_t td = ~0ull, tk = 0ull;
+    if (!exact_grp && Tq0 != 0ull && !(Tq0 > ((uint64_t)k << 41))) {
+      const CutBands cb = topp_cut_bands_lean(Tq0, S, lse0, lnS, xmin, k);
+      td = cb.tdrop;
+      tk = cb.tkeep;
+    }
+    if (tid == 0) {
+      R.row_q[0] = Tq0;
+      R.row_q[1] = td;
+      R.row_q[2] = tk;
+      R.row_lse = lse0;
+    }
+  }
+  __syncthreads();
+  const float lse = R.row_lse;
+  const uint64_t Tq = R.row_q[0];
   const bool settled1 = Tq == 0ull;                     /* every prefix passes: cut 1 */
   const bool settledk = Tq > ((uint64_t)k << 41);      /* none reaches it: cut k */
   uint64_t tdrop = ~0ull, tkeep = 0ull;
   uint64_t pg0 = 0ull; /* the retry: the exact prefix before the group */
   if (!exact_grp) {
     if (!settled1 && !settledk) {
-      const CutBands cb = topp_cut_bands_lean(Tq, S, lse, lnS, xmin, k);
-      tdrop = cb.tdrop;
-      tkeep = cb.tkeep;
+      tdrop = R.row_q[1];
+      tkeep = R.row_q[2];
       if (gst < tdrop && tdrop <= gst + gs) {
         misc[4] = (uint32_t)tid;
         misc64[0] = gst;
