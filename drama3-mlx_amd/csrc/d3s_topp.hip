@@ -646,16 +646,19 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
 #pragma unroll
       for (int q = 0; q < EPT; q++) pm |= (q * TBLOCK + tid < khi ? 1u : 0u) << q;
     }
-    int slot = wave_append_mask(pm, (int *)&misc[3]);
+    /* (most waves file none: the append is skipped wave by wave) */
+    if (__ballot(pm != 0u)) {
+      int slot = wave_append_mask(pm, (int *)&misc[3]);
 #pragma unroll
-    for (int q = 0; q < EPT; q++)
-      if ((pm >> q) & 1u) {
-        if (slot < TF_CAP) {
-          rr[slot] = q * TBLOCK + tid;
-          ru[slot] = uv[q];
+      for (int q = 0; q < EPT; q++)
+        if ((pm >> q) & 1u) {
+          if (slot < TF_CAP) {
+            rr[slot] = q * TBLOCK + tid;
+            ru[slot] = uv[q];
+          }
+          slot++;
         }
-        slot++;
-      }
+    }
   }
   __syncthreads();
   const uint32_t nref = misc[3];
@@ -700,16 +703,18 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
       const bool in = i < V && ((gb >= gl && gb <= g) || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
       gm |= (in ? 1u : 0u) << j;
     }
-    int slot = wave_append_mask(gm, (int *)&misc[0]);
+    if (__ballot(gm != 0u)) {
+      int slot = wave_append_mask(gm, (int *)&misc[0]);
 #pragma unroll
-    for (int j = 0; j < EPT; j++)
-      if ((gm >> j) & 1u) {
-        if (slot < TF_CAP) {
-          lkey[slot] = composite_key(x[j], j * TBLOCK + tid);
-          lval[slot] = (uint64_t)(uint32_t)topp_bucket_of<NBK>(x[j], m, scale);
+      for (int j = 0; j < EPT; j++)
+        if ((gm >> j) & 1u) {
+          if (slot < TF_CAP) {
+            lkey[slot] = composite_key(x[j], j * TBLOCK + tid);
+            lval[slot] = (uint64_t)(uint32_t)topp_bucket_of<NBK>(x[j], m, scale);
+          }
+          slot++;
         }
-        slot++;
-      }
+    }
   }
   __syncthreads();
   const uint32_t n2 = misc[0];
