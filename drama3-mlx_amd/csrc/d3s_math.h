@@ -101,7 +101,11 @@ D3S_HD float d3s_exp_core(float ac, float *n_out) {
 #pragma clang fp contract(off)
 #endif
   const float t = ac * 0x1.715476p+0f;                        /* a * log2(e) */
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float n = __builtin_rintf(t); /* the same: |t| < 2^22, ties to even (v_rndne_f32) */
+#else
   const float n = (t + 0x1.8p+23f) - 0x1.8p+23f;
+#endif
   float r = D3S_FMAF(n, -0x1.62e400p-1f, ac); /* a - n*ln2_hi (exact) */
   r = D3S_FMAF(n, -0x1.7f7d1cp-20f, r);       /* - n*ln2_lo */
   float p = 0x1.a01a02p-13f;                  /* 1/7! */
@@ -246,16 +250,16 @@ D3S_HD uint64_t d3s_fix40_unit(float e) {
 /* d3s_fix40(d3s_expf(z)) for z <= 0 (or -0, or -inf), without forming the
  * fp32 result: exp's polynomial value p lies in [2^-1/2, 2^1/2], so p * 2^24
  * is an integer P below 2^25 and floor(p * 2^n * 2^40) = floor(P * 2^(n + 16))
- * = (P * 2^16) >> -n (n <= 0; a shift past 40 leaves 0, as do results below
- * 2^-126 either way): one 64-bit shift.  Same bits as the two-step form;
- * fewer instructions for the per-element row sum. */
+ * = (P * 2^16) >> -n (n <= 0): one 64-bit shift.  Arguments below -43 give 0
+ * (e^-43 2^40 < 2^-22), as the clamp to -43 does (n >= -62, so the shift
+ * stays below 64, and P 2^16 < 2^41 shifted by 62 is 0).  Same bits as the
+ * two-step form; fewer instructions for the per-element row sum. */
 D3S_HD uint64_t d3s_fix40_exp(float z) {
-  const float zc = fmaxf(z, -0x1.a0p+6f); /* [-104, 0]; -inf -> -104 */
+  const float zc = fmaxf(z, -43.0f); /* [-43, 0]; -inf -> -43 */
   float n;
   const float p = d3s_exp_core(zc, &n);
   const uint64_t P16 = (uint64_t)(uint32_t)(p * 0x1.0p+24f) << 16; /* below 2^41 */
-  const int sh = -(int)n;                                            /* 0 <= sh <= 151 */
-  return P16 >> (sh < 63 ? sh : 63);
+  return P16 >> (int)(-n);                                          /* 0 <= -n <= 62 */
 }
 
 /* uint64 -> fp32, round to nearest, ties to even (integer steps only). */

@@ -615,12 +615,13 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   /* LB1, the largest first lower bound over the certainly kept ranks: lb
    * decreases in u where it is defined (2^-24 <= u < 1; -1 elsewhere), so a
    * thread's is the lb of its least such u (one evaluation, not one a rank) */
+  /* this thread's ranks q TBLOCK + tid below klo (khi) are those of q < qlo (qhi) */
+  const int qlo = klo > tid ? min((klo - tid + TBLOCK - 1) / TBLOCK, EPT) : 0;
+  const int qhi = khi > tid ? min((khi - tid + TBLOCK - 1) / TBLOCK, EPT) : 0;
   float umin = 1.0f;
 #pragma unroll
-  for (int q = 0; q < EPT; q++) {
-    const int r = q * TBLOCK + tid;
-    if (r < klo && uv[q] >= 0x1p-24f) umin = fminf(umin, uv[q]);
-  }
+  for (int q = 0; q < EPT; q++)
+    if (q < qlo && uv[q] >= 0x1p-24f) umin = fminf(umin, uv[q]);
   float lbm = -1.0f;
   if (umin < 1.0f) {
     float h_unused;
@@ -635,16 +636,15 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
    * that may be kept. */
   {
     uint32_t pm = 0u;
+    const uint32_t qmask = (1u << qhi) - 1u;
     if (LB1 > 0.0f) {
-      const float uthr = 0x1p-24f + (1.0f / LB1) * 1.01f;
+      /* (u < 1 folded in: the threshold is capped below 1) */
+      const float uthr = fminf(0x1p-24f + (1.0f / LB1) * 1.01f, 0x1.fffffep-1f);
 #pragma unroll
-      for (int q = 0; q < EPT; q++) {
-        const int r = q * TBLOCK + tid;
-        pm |= (r < khi && uv[q] < 1.0f && uv[q] <= uthr ? 1u : 0u) << q;
-      }
+      for (int q = 0; q < EPT; q++) pm |= (uv[q] <= uthr ? 1u : 0u) << q;
+      pm &= qmask;
     } else {
-#pragma unroll
-      for (int q = 0; q < EPT; q++) pm |= (q * TBLOCK + tid < khi ? 1u : 0u) << q;
+      pm = qmask;
     }
     /* (most waves file none: the append is skipped wave by wave) */
     if (__ballot(pm != 0u)) {
