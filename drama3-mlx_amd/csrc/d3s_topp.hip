@@ -1257,19 +1257,32 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
   /* ---- 1. x (with T = 1, x = L: RN(L / 1) = L), max and least finite x */
   float x[EPT];
   float xm = -__builtin_inff(), xl = __builtin_inff();
+  /* element j of this thread lies in the row for j < nj; reads through a
+   * buffer resource spanning the row (past its end they return 0, masked
+   * below), and the banned element is masked by the one thread holding it */
+  const int nj = V > tid ? min((V - tid + TBLOCK - 1) / TBLOCK, EPT) : 0;
   {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)rowp, (short)0, V * (BF16 ? 2 : 4), 0x00020000);
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
       const int i = j * TBLOCK + tid;
-      const int ii = i < V ? i : V - 1;
-      x[j] = BF16 ? d3s_bf16_to_f32(((const uint16_t *)rowp)[ii]) : ((const float *)rowp)[ii];
+      if (BF16)
+        x[j] = d3s_u2f((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, i * 2, 0, 0) << 16);
+      else
+        x[j] = d3s_u2f(__builtin_amdgcn_raw_buffer_load_b32(rs, i * 4, 0, 0));
+    }
+    if ((unsigned)rp.banned < (unsigned)V && tid == rp.banned % TBLOCK) {
+      const int jb = rp.banned / TBLOCK;
+#pragma unroll
+      for (int j = 0; j < EPT; j++)
+        if (j == jb) x[j] = -__builtin_inff();
     }
   }
   if (T == 1.0f) {
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
-      const float xi = i < V && i != rp.banned ? x[j] : -__builtin_inff();
+      const float xi = j < nj ? x[j] : -__builtin_inff();
       x[j] = xi;
       xm = __builtin_elementwise_maximum(xm, xi);
       xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
@@ -1277,8 +1290,7 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
   } else {
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
-      const float xi = i < V && i != rp.banned ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
+      const float xi = j < nj ? scale_logit(x[j], T, y, t_finite) : -__builtin_inff();
       x[j] = xi;
       xm = __builtin_elementwise_maximum(xm, xi);
       xl = fminf(xl, xi > -__builtin_inff() ? xi : __builtin_inff());
