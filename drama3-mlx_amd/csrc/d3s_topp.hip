@@ -293,7 +293,7 @@ constexpr int TF_CAP = WAVE; /* the elements (and refined ranks) one wave takes 
 
 /* byte offsets in the dynamic LDS region: group sums (one per thread); the
  * gathered elements' keys and buckets; the refined ranks and their uniforms;
- * counters; candidate bucket and rank bitmaps; the rank map */
+ * counters; candidate bucket and rank bitmaps */
 __host__ __device__ constexpr size_t tf_lkey(int tb) { return 8 * (size_t)tb; }
 __host__ __device__ constexpr size_t tf_lval(int tb) { return tf_lkey(tb) + 8 * TF_CAP; }
 __host__ __device__ constexpr size_t tf_rr(int tb) { return tf_lval(tb) + 8 * TF_CAP; }
@@ -301,11 +301,8 @@ __host__ __device__ constexpr size_t tf_ru(int tb) { return tf_rr(tb) + 4 * TF_C
 __host__ __device__ constexpr size_t tf_misc(int tb) { return tf_ru(tb) + 4 * TF_CAP; }
 __host__ __device__ constexpr size_t tf_cbits(int tb) { return tf_misc(tb) + 64; }
 __host__ __device__ constexpr size_t tf_rbits(int tb, int nbk) { return tf_cbits(tb) + 4 * (size_t)(nbk / 32 + 4); }
-__host__ __device__ constexpr size_t tf_map(int tb, int nbk, int V) {
-  return tf_rbits(tb, nbk) + 16 * (size_t)((V + 127) / 128);
-}
 __host__ __device__ constexpr size_t tf_bytes(int tb, int nbk, int V) {
-  return tf_map(tb, nbk, V) + 2 * (size_t)((V + 7) & ~7);
+  return tf_rbits(tb, nbk) + 16 * (size_t)((V + 127) / 128);
 }
 
 /* uint64 -> fp32 within a relative 2^-22 (two conversions and a sum) */
@@ -465,7 +462,6 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   uint64_t *misc64 = (uint64_t *)(dyn + tf_misc(TBLOCK) + 32);
   uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
   uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
-  uint16_t *rmap = (uint16_t *)(dyn + tf_map(TBLOCK, NBK, V)); /* bucket + 1 at each bucket's first rank */
   /* thread t takes the uniforms of ranks q TBLOCK + t (q < EPT): read
    * coalesced */
 
@@ -500,15 +496,11 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         st[e] = run;
-        if (cc[e] != 0u) rmap[run] = (uint16_t)(tid * PER + 4 * q + e + 1);
         run += cc[e];
       }
       *(uint4 *)&bstart[tid * PER + 4 * q] = make_uint4(st[0], st[1], st[2], st[3]);
     }
-    if (tid == 0) {
-      bstart[NBK] = tot;
-      if (tot < (uint32_t)V) rmap[tot] = (uint16_t)(NBK + 1);
-    }
+    if (tid == 0) bstart[NBK] = tot;
   }
   /* ---- 4'. the row's lse, the least prefix above top_p (Tq) and the
    * certain drop and keep bands: the same in every thread, so wave 0 alone
@@ -672,12 +664,9 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
     my_rr = mine ? rr[lane] : 0x7fffffff;
     my_ru = mine ? ru[lane] : 0.0f;
     int b = 0;
-    if (mine) {
-      /* the bucket holding rank r: the nearest first rank at or below it */
-      int p = my_rr, v = (int)rmap[p];
-      while (v == 0) v = (int)rmap[--p]; /* (rmap[0] = 1: bucket 0 holds rank 0) */
-      b = v - 1;
-    }
+    /* the bucket holding rank r: the last whose start is at or below r
+     * (a binary search over the starts, for these few ranks) */
+    if (mine) b = topp_bucket_of_rank<NBK>(bstart, my_rr);
     float lb = -1.0f, h = -__builtin_inff();
     if (mine) {
       float elo, ehi, l2;
@@ -1250,8 +1239,6 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
     uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
     for (int w = tid; w < NBK / 32 + 4; w += TBLOCK) cbits[w] = 0u;
     for (int w = tid; w < 4 * ((V + 127) / 128); w += TBLOCK) rbits[w] = 0u;
-    uint32_t *rmap = (uint32_t *)(dyn + tf_map(TBLOCK, NBK, V));
-    for (int w = tid; w < ((V + 7) & ~7) / 2; w += TBLOCK) rmap[w] = 0u;
   }
 
   /* ---- 1. x (with T = 1, x = L: RN(L / 1) = L), max and least finite x */
