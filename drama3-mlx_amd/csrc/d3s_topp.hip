@@ -124,22 +124,20 @@ __device__ __forceinline__ float block_max_f(float v, TRed &R) {
   return uni_f(row16_max_f(R.f[lane_id() & 15]));
 }
 
-/* the maxima of three values in one round */
-__device__ __forceinline__ void block_max3_f(float &u, float &v, float &w, TRed &R) {
+/* the maxima of two values in one round (IEEE maximum at every step: a NaN
+ * in any lane gives NaN, +inf is kept) */
+__device__ __forceinline__ void block_max2_f(float &u, float &v, TRed &R) {
   u = wave_max_f(u);
   v = wave_max_f(v);
-  w = wave_max_f(w);
   const int wid = threadIdx.x / WAVE, l16 = lane_id() & 15;
   __syncthreads();
   if (lane_id() == 0) {
     R.f[wid] = u;
     R.g[wid] = v;
-    R.h[wid] = w;
   }
   __syncthreads();
   u = uni_f(row16_max_f(R.f[l16]));
   v = uni_f(row16_max_f(R.g[l16]));
-  w = uni_f(row16_max_f(R.h[l16]));
 }
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, TRed &R) {
@@ -684,12 +682,13 @@ __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const
   /* ---- one gather: the cut group's elements and the candidates' buckets' */
   {
     uint32_t gm = 0u;
+    /* the range's buckets [b_lo, b_hi); element j of this thread lies in the row for j < nj */
+    const int b_lo = gl * PER, b_hi = g * PER + PER;
+    const int nj = V > tid ? min((V - tid + TBLOCK - 1) / TBLOCK, EPT) : 0;
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
-      const int i = j * TBLOCK + tid;
       const int bb = topp_bucket_of<NBK>(x[j], m, scale);
-      const int gb = bb / PER;
-      const bool in = i < V && ((gb >= gl && gb <= g) || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
+      const bool in = j < nj && ((bb >= b_lo && bb < b_hi) || ((cbits[bb >> 5] >> (bb & 31)) & 1u) != 0u);
       gm |= (in ? 1u : 0u) << j;
     }
     if (__ballot(gm != 0u)) {
@@ -1120,11 +1119,12 @@ __device__ __forceinline__ void topp_full(const SampleArgs &a, int row, const Ro
 template <int EPT>
 __device__ __forceinline__ bool topp_max_min(const SampleArgs &a, int row, float xm, float xl, float &m, float &xmin,
                                              TRed &R) {
-  const bool refused = !(xm < __builtin_inff()); /* NaN or +inf */
-  float nxl = -xl, bad = refused ? 1.0f : 0.0f;
-  m = refused ? 0.0f : xm;
-  block_max3_f(m, nxl, bad, R);
-  if (bad > 0.0f) {
+  /* xm: the thread's maximum with NaN propagated and +inf kept, so the
+   * row's is NaN or +inf exactly when some x is (refused) */
+  float M = xm, nxl = -xl;
+  block_max2_f(M, nxl, R);
+  m = M;
+  if (!(M < __builtin_inff())) {
     write_special(a, row, false);
     return false;
   }
