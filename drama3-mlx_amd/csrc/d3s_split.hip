@@ -27,6 +27,7 @@ namespace {
 constexpr int SPLIT_NW = 4;              /* waves per segment */
 constexpr int SPLIT_CPT = 8;             /* 16-byte chunks per lane */
 constexpr int SPLIT_CPT_WIDE = 10;       /* the wider form, when it fills the CUs more evenly */
+constexpr int SPLIT_CPT_LONG = 19;       /* the longest: one workgroup per CU (bf16: its registers) */
 constexpr int SPLIT_T = SPLIT_NW * WAVE; /* threads per segment */
 constexpr int SCAP = SPLIT_T;            /* candidates a segment ranks (one per thread) */
 constexpr int SPLIT_MAX_SEG = 16;        /* segments per row */
@@ -534,29 +535,35 @@ struct SplitShape {
   int cpt, nseg; /* nseg 0: the segmented kernel does not take the rows */
 };
 
-/* The segments' form for these rows: SPLIT_CPT chunks per lane, or
- * SPLIT_CPT_WIDE when its launch (fewer, longer segments) fills whole rounds
- * of the CUs more evenly and fits in one round (the bf16 form runs three
- * workgroups per CU).  A row's merge waits for its slowest segment, and a CU
- * holding one workgroup more than the others makes that segment slow. */
+/* The segments' form for these rows: SPLIT_CPT chunks per lane, or a longer
+ * form (SPLIT_CPT_WIDE, SPLIT_CPT_LONG: fewer, longer segments) when its
+ * launch fits in one round and fills whole rounds of the CUs at least as
+ * evenly; of equal fills the fewest segments (each segment's steps take
+ * about as long at twice the chunks with half the waves per SIMD, and the
+ * merge has fewer records).  Workgroups per CU by registers: the bf16 forms
+ * of 10 and 19 chunks run three and one.  A row's merge waits for its
+ * slowest segment, and a CU holding one workgroup more than the others makes
+ * that segment slow. */
 SplitShape split_shape(const SampleArgs &a, Dtype dt) {
   const int EPC = dt == DT_F32 ? 4 : 8;
   const int nchunks = (EPC - 1 + a.vocab + EPC - 1) / EPC; /* any start offset */
   const int cus = device_cus();
   SplitShape best{SPLIT_CPT, 0};
   double best_fill = -1.0;
-  for (const int cpt : {SPLIT_CPT, SPLIT_CPT_WIDE}) {
+  int64_t best_blocks = 0;
+  for (const int cpt : {SPLIT_CPT, SPLIT_CPT_WIDE, SPLIT_CPT_LONG}) {
     const int cap = SPLIT_NW * cpt * WAVE;
     const int nseg = (nchunks + cap - 1) / cap;
     const int64_t blocks = (int64_t)a.n_rows * nseg;
     if (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG || blocks > SPLIT_MAX_BLOCKS) continue;
-    const int per_cu = cpt == SPLIT_CPT_WIDE && dt == DT_BF16 ? 3 : 4; /* registers */
-    if (cpt == SPLIT_CPT_WIDE && blocks > (int64_t)cus * per_cu) continue;
+    const int per_cu = dt == DT_BF16 && cpt == SPLIT_CPT_LONG ? 1 : dt == DT_BF16 && cpt == SPLIT_CPT_WIDE ? 3 : 4;
+    if (cpt != SPLIT_CPT && blocks > (int64_t)cus * per_cu) continue;
     const int64_t rounds = (blocks + cus - 1) / cus;
     const double fill = (double)blocks / (double)(rounds * cus);
-    if (fill > best_fill + 1e-9) {
+    if (fill > best_fill + 1e-9 || (fill > best_fill - 1e-9 && blocks < best_blocks)) {
       best = SplitShape{cpt, nseg};
       best_fill = fill;
+      best_blocks = blocks;
     }
   }
   return best;
@@ -575,6 +582,9 @@ size_t split_workspace_bytes(const SampleArgs &a, Dtype dt) {
 bool launch_split(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
   const SplitShape sh = split_shape(a, dt);
   if (!sh.nseg) return false;
+  if (sh.cpt == SPLIT_CPT_LONG)
+    return dt == DT_F32 ? try_split<SPLIT_CPT_LONG, false>(a, sh.nseg, ws, ws_bytes, s)
+                        : try_split<SPLIT_CPT_LONG, true>(a, sh.nseg, ws, ws_bytes, s);
   if (sh.cpt == SPLIT_CPT_WIDE)
     return dt == DT_F32 ? try_split<SPLIT_CPT_WIDE, false>(a, sh.nseg, ws, ws_bytes, s)
                         : try_split<SPLIT_CPT_WIDE, true>(a, sh.nseg, ws, ws_bytes, s);
