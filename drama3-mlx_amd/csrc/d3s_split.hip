@@ -3,8 +3,9 @@
  *
  * A segment is SPLIT_NW waves x 64 lanes x CPT 16-byte chunks of the row, one
  * workgroup.  It runs the one-wave kernel's passes on its part (registers,
- * NaN-propagating max, a threshold from an 8-bit histogram of its 256 lane
- * maxima, candidate bits, the fast sum 2^(L c - h_s) relative to its own max)
+ * NaN-propagating max, a threshold that at least k of its lane maxima reach:
+ * the least of its waves' ceil(k / SPLIT_NW)-th largest, candidate chunks,
+ * the fast sum 2^(L c - h_s) relative to its own max)
  * and ranks its candidates: its top min(k, candidates) keys hold every key of
  * the row's top k that lies in the segment.  It publishes a record (max, fast
  * sum, flags, keys by rank) with agent-coherent stores, waits for them to
@@ -24,10 +25,10 @@
 namespace d3s {
 namespace {
 
-constexpr int SPLIT_NW = 4;              /* waves per segment */
+constexpr int SPLIT_NW = 8;              /* waves per segment (two per SIMD) */
 constexpr int SPLIT_CPT = 8;             /* 16-byte chunks per lane */
 constexpr int SPLIT_CPT_WIDE = 10;       /* the wider form, when it fills the CUs more evenly */
-constexpr int SPLIT_CPT_LONG = 19;       /* the longest: one workgroup per CU (bf16: its registers) */
+constexpr int SPLIT_CPT_LONG = 19;       /* the longest form */
 constexpr int SPLIT_T = SPLIT_NW * WAVE; /* threads per segment */
 constexpr int SCAP = SPLIT_T;            /* candidates a segment ranks (one per thread) */
 constexpr int SPLIT_MAX_SEG = 16;        /* segments per row */
@@ -538,12 +539,12 @@ struct SplitShape {
 /* The segments' form for these rows: SPLIT_CPT chunks per lane, or a longer
  * form (SPLIT_CPT_WIDE, SPLIT_CPT_LONG: fewer, longer segments) when its
  * launch fits in one round and fills whole rounds of the CUs at least as
- * evenly; of equal fills the fewest segments (each segment's steps take
- * about as long at twice the chunks with half the waves per SIMD, and the
- * merge has fewer records).  Workgroups per CU by registers: the bf16 forms
- * of 10 and 19 chunks run three and one.  A row's merge waits for its
- * slowest segment, and a CU holding one workgroup more than the others makes
- * that segment slow. */
+ * evenly; of equal fills the fewest segments (the merge has fewer records).
+ * Workgroups per CU by registers (eight-wave workgroups): bf16 two and one
+ * for 8 and 10 chunks (19 bf16 chunks, 152 elements a lane, measured slower
+ * than more segments: not taken); fp32 three, three and two.  A row's merge
+ * waits for its slowest segment, and a CU holding one workgroup more than
+ * the others makes that segment slow. */
 SplitShape split_shape(const SampleArgs &a, Dtype dt) {
   const int EPC = dt == DT_F32 ? 4 : 8;
   const int nchunks = (EPC - 1 + a.vocab + EPC - 1) / EPC; /* any start offset */
@@ -556,7 +557,8 @@ SplitShape split_shape(const SampleArgs &a, Dtype dt) {
     const int nseg = (nchunks + cap - 1) / cap;
     const int64_t blocks = (int64_t)a.n_rows * nseg;
     if (a.k > KF || nseg < 2 || nseg > SPLIT_MAX_SEG || blocks > SPLIT_MAX_BLOCKS) continue;
-    const int per_cu = dt == DT_BF16 && cpt == SPLIT_CPT_LONG ? 1 : dt == DT_BF16 && cpt == SPLIT_CPT_WIDE ? 3 : 4;
+    const int per_cu = dt == DT_BF16 ? (cpt == SPLIT_CPT ? 2 : cpt == SPLIT_CPT_WIDE ? 1 : 0)
+                                     : (cpt == SPLIT_CPT_LONG ? 2 : 3);
     if (cpt != SPLIT_CPT && blocks > (int64_t)cus * per_cu) continue;
     const int64_t rounds = (blocks + cus - 1) / cus;
     const double fill = (double)blocks / (double)(rounds * cus);
@@ -582,9 +584,8 @@ size_t split_workspace_bytes(const SampleArgs &a, Dtype dt) {
 bool launch_split(const SampleArgs &a, Dtype dt, void *ws, size_t ws_bytes, hipStream_t s) {
   const SplitShape sh = split_shape(a, dt);
   if (!sh.nseg) return false;
-  if (sh.cpt == SPLIT_CPT_LONG)
-    return dt == DT_F32 ? try_split<SPLIT_CPT_LONG, false>(a, sh.nseg, ws, ws_bytes, s)
-                        : try_split<SPLIT_CPT_LONG, true>(a, sh.nseg, ws, ws_bytes, s);
+  if (sh.cpt == SPLIT_CPT_LONG) /* (fp32 only) */
+    return dt == DT_F32 && try_split<SPLIT_CPT_LONG, false>(a, sh.nseg, ws, ws_bytes, s);
   if (sh.cpt == SPLIT_CPT_WIDE)
     return dt == DT_F32 ? try_split<SPLIT_CPT_WIDE, false>(a, sh.nseg, ws, ws_bytes, s)
                         : try_split<SPLIT_CPT_WIDE, true>(a, sh.nseg, ws, ws_bytes, s);
