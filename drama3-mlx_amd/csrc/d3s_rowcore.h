@@ -203,11 +203,13 @@ __device__ __forceinline__ uint64_t ld_agent(const uint64_t *p) {
 }
 
 /* rank the n keys of list (n + 2 entries of room): every key counts the keys
- * above its own; those below k land in ranked by rank.  Keys are distinct.
+ * above its own; those below k land in ranked by rank (PUBLISH: in global
+ * memory, by agent-coherent stores and with no closing barrier: the caller
+ * retires the stores before publishing).  Keys are distinct.
  * G adjacent lanes share a key (G = 4 when n <= NT / 4, 2 when n <=
  * NT / 2), each counting a share of the list; quad DPP adds the shares.
  * Called by every thread of an NT-thread workgroup. */
-template <int NT>
+template <int NT, bool PUBLISH = false>
 __device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k, uint64_t *ranked) {
   if (threadIdx.x == 0) {
     list[n] = 0ull; /* pads below every key */
@@ -231,9 +233,14 @@ __device__ __forceinline__ void rank_by_count(uint64_t *list, uint32_t n, int k,
     }
     if (lg >= 1) rank += dpp_u<0xb1, 0xf>(0u, rank); /* quad_perm [1,0,3,2] */
     if (lg >= 2) rank += dpp_u<0x4e, 0xf>(0u, rank); /* quad_perm [2,3,0,1] */
-    if (part == 0 && t < n && rank < (uint32_t)k) ranked[rank] = my;
+    if (part == 0 && t < n && rank < (uint32_t)k) {
+      if (PUBLISH)
+        st_agent(ranked + rank, my);
+      else
+        ranked[rank] = my;
+    }
   }
-  __syncthreads();
+  if (!PUBLISH) __syncthreads();
 }
 
 /* A row in registers: CPT 16-byte chunks per lane (chunk j * 64 + lane, from

@@ -345,7 +345,8 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(const void *hot_logits, int64
         const uint64_t lp = S.raw[w * WAVE + t];
         S.keys[threadIdx.x] = composite_key(scale_logit(d3s_u2f((uint32_t)(lp >> 32)), T, y, true), (int)(uint32_t)lp);
       }
-      rank_by_count<SPLIT_T>(S.keys, tot, k, S.ranked);
+      /* ranked straight into the record's key slots */
+      rank_by_count<SPLIT_T, true>(S.keys, tot, k, records + ((size_t)row * nseg + seg) * rec_words + 2);
       nfiled = min(tot, (uint32_t)k);
     }
   }
@@ -353,7 +354,6 @@ __global__ __launch_bounds__(SPLIT_T) void k_split(const void *hot_logits, int64
   /* ---- publish the record: agent-coherent stores, completed before the
    * arrival is counted (the ordering argument is at st_agent) */
   uint64_t *rec = records + ((size_t)row * nseg + seg) * rec_words;
-  if (threadIdx.x < nfiled) st_agent(rec + 2 + threadIdx.x, S.ranked[threadIdx.x]);
   if (threadIdx.x == 0) {
     st_agent(rec, (uint64_t)d3s_f2u(Ls) | ((uint64_t)d3s_f2u(ssum) << 32));
     st_agent(rec + 1, (uint64_t)flags | ((uint64_t)nfiled << 32));
