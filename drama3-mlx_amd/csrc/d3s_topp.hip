@@ -289,10 +289,12 @@ constexpr int TOPP_RETRY = -3; /* the ids path's exact retry (internal) */
 constexpr int TOPP_REDO_WG = 64; /* k_topp_redo's workgroups (at most) */
 constexpr int TF_CAP = WAVE; /* the elements (and refined ranks) one wave takes */
 
-/* byte offsets in the dynamic LDS region: group sums (one per thread); the
- * gathered elements' keys and buckets; the refined ranks and their uniforms;
- * counters; candidate bucket and rank bitmaps */
-__host__ __device__ constexpr size_t tf_lkey(int tb) { return 8 * (size_t)tb; }
+/* byte offsets in the dynamic LDS region: the gathered elements' keys and
+ * buckets; the refined ranks and their uniforms; counters; candidate bucket
+ * and rank bitmaps (the group sums, one per thread and one past them for
+ * the -inf bucket, are a static array of the kernels: their address folds
+ * into the atomics' offsets) */
+__host__ __device__ constexpr size_t tf_lkey(int) { return 0; }
 __host__ __device__ constexpr size_t tf_lval(int tb) { return tf_lkey(tb) + 8 * TF_CAP; }
 __host__ __device__ constexpr size_t tf_rr(int tb) { return tf_lval(tb) + 8 * TF_CAP; }
 __host__ __device__ constexpr size_t tf_ru(int tb) { return tf_rr(tb) + 4 * TF_CAP; }
@@ -442,12 +444,12 @@ __device__ __forceinline__ int topp_bucket_of_rank(const uint32_t *bstart, int r
 template <int EPT, int TBLOCK, int NBK>
 __device__ __forceinline__ int topp_ids_fast(const SampleArgs &a, int row, const float (&x)[EPT],
                                              float m, float xmin, float scale, float top_p,
-                                             uint32_t *bstart, char *dyn, TRed &R, const bool exact_grp) {
+                                             uint32_t *bstart, uint64_t *gsum, char *dyn, TRed &R,
+                                             const bool exact_grp) {
   constexpr int PER = NBK / TBLOCK;
   static_assert(PER % 4 == 0, "whole 16-byte groups of buckets per thread");
   const int V = a.vocab, k = a.k;
   const int tid = (int)threadIdx.x, lane = lane_id();
-  uint64_t *gsum = (uint64_t *)dyn;
   uint64_t *lkey = (uint64_t *)(dyn + tf_lkey(TBLOCK));
   uint64_t *lval = (uint64_t *)(dyn + tf_lval(TBLOCK)); /* bucket */
   int *rr = (int *)(dyn + tf_rr(TBLOCK));
@@ -1218,7 +1220,7 @@ constexpr int topp_ids_waves(int ept, int tb) { return tb == 512 ? 8 : topp_wave
  * the row needs another pass (the retry, exact_grp, or after it the full path). */
 template <int EPT, bool BF16, int TBLOCK, int NBK>
 __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row, char *dyn, uint32_t *bstart,
-                                             TRed &R, const bool exact_grp) {
+                                             uint64_t *gsum, TRed &R, const bool exact_grp) {
   constexpr int PER = NBK / TBLOCK;
   const int tid = (int)threadIdx.x;
   const int V = a.vocab;
@@ -1234,7 +1236,7 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
     for (int b = 4 * tid; b < NBK; b += 4 * TBLOCK) *(uint4 *)&bstart[b] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < 4) bstart[NBK + tid] = 0u;
     if (tid < 16) ((uint32_t *)(dyn + tf_misc(TBLOCK)))[tid] = tid == 4 || tid == 5 ? ~0u : 0u;
-    ((uint64_t *)dyn)[tid] = 0ull;
+    gsum[tid] = 0ull;
     uint32_t *cbits = (uint32_t *)(dyn + tf_cbits(TBLOCK));
     uint32_t *rbits = (uint32_t *)(dyn + tf_rbits(TBLOCK, NBK));
     for (int w = tid; w < NBK / 32 + 4; w += TBLOCK) cbits[w] = 0u;
@@ -1301,10 +1303,10 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
       const uint64_t f = d3s_fix40_exp(d); /* fix40(expf(x - m)), 0 for -inf */
       const int b = (int)fminf(d * nscale, (float)NBK);
       atomicAdd(&bstart[b], 1u);
-      atomicAdd((unsigned long long *)&((uint64_t *)dyn)[(uint32_t)b / PER], (unsigned long long)f);
+      atomicAdd((unsigned long long *)&gsum[(uint32_t)b / PER], (unsigned long long)f);
     }
     __syncthreads(); /* the counts and sums in (the row sum S is their total) */
-    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, m, xmin, scale, rp.top_p, bstart, dyn, R, exact_grp);
+    const int id = topp_ids_fast<EPT, TBLOCK, NBK>(a, row, x, m, xmin, scale, rp.top_p, bstart, gsum, dyn, R, exact_grp);
     if (id >= 0) {
       if (tid == 0) a.ids[row] = id;
       return true;
@@ -1319,10 +1321,12 @@ template <int EPT, bool BF16, int TBLOCK>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids_waves(EPT, TBLOCK)))) void k_topp_ids(
     SampleArgs a, ToppRedo rd) {
   D3S_TOPP_SHARED
+  __shared__ uint64_t gsum_s[TBLOCK + 2]; /* the group sums (entry TBLOCK: the -inf bucket's group) */
   const int row = (int)blockIdx.x;
   /* (FLAG_EXACT_LSE: every row straight to the exact retry) */
   const bool filed =
-      (a.flags & FLAG_EXACT_LSE) != 0u || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, false);
+      (a.flags & FLAG_EXACT_LSE) != 0u ||
+      !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, gsum_s, R, false);
   if (filed && tid == 0) rd.rows[atomicAdd(rd.count, 1u)] = row;
 }
 
@@ -1336,6 +1340,7 @@ template <int EPT, bool BF16, int TBLOCK>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) void k_topp_redo(
     SampleArgs a, ToppRedo rd) {
   D3S_TOPP_SHARED
+  __shared__ uint64_t gsum_s[TBLOCK + 2]; /* the group sums (entry TBLOCK: the -inf bucket's group) */
   const uint32_t n = __hip_atomic_load(rd.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   /* every workgroup reads the same count (nothing changes it before the
    * last arrival below); none filed: the counts are zero already, and no
@@ -1347,7 +1352,7 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) voi
     __syncthreads(); /* the previous row's LDS reads done */
     /* (1024-thread workgroups: the full path alone; with the retry beside it
      * the loop would need scratch at four waves per SIMD) */
-    if (TBLOCK > 512 || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, R, true)) {
+    if (TBLOCK > 512 || !topp_ids_row<EPT, BF16, TBLOCK, NBK>(a, row, (char *)keys, bstart, gsum_s, R, true)) {
       __syncthreads();
       topp_full_row<EPT, BF16, TBLOCK, NBK>(a, row, keys, bstart, R);
     }
