@@ -229,6 +229,10 @@ struct WaveRow {
    * (the rows that end earlier pass it in the kernel) */
   const float *lse_in = nullptr;
   bool synced = false;
+  /* k_wave_row: the exact row sum's two halves (2^-40 fixed point), filed by
+   * helper waves before that same barrier; a cut within the fast lse's margin
+   * takes the exact lse from them */
+  const uint64_t *ex_in = nullptr;
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -342,6 +346,7 @@ struct WaveRow {
     fin_M = M;
     fin_noise = noise;
     return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf, [&]() {
+      if (ex_in) return M + d3s_logf(d3s_fixsum_to_f32(ex_in[0] + ex_in[1]));
       return defer_exact ? __builtin_nanf("") : exact_lse<CPT, BF16>(ref(), M);
     });
   }
@@ -415,6 +420,83 @@ struct WaveRow {
       out[0] = lse;
       out[1] = eps_s;
     }
+  }
+
+  /* k_wave_row's exact-sum helper waves: the row's max as compute() takes it
+   * (the same M), then half the row's terms fix40(d3s_expf(x - M)) (part 0:
+   * each lane's first CPT / 2 chunks, part 1 the rest; masked elements
+   * hold -inf, whose term is 0), summed over the wave and filed at out[0].
+   * An integer sum, the same in any order: the two halves add to the oracle's
+   * row sum.  Rows that compute() ends at the max (refused, all -inf, T not
+   * finite: the same tests on the same values) file nothing; every other row
+   * files, whichever path wave 0 then takes. */
+  __device__ __forceinline__ void helper_exact(uint64_t *out, int part) {
+    if (!t_finite) return;
+    const float ninf = -__builtin_inff();
+    float lm = ninf;
+#pragma unroll
+    for (int i = 0; i < NV; i++) lm = fmaximum(lm, c.val(i));
+    const float Lmax = wave_maximum_f(lm);
+    if (d3s_isnan(Lmax) || Lmax == __builtin_inff()) return;
+    const float M = scale_logit(Lmax, T, y, true);
+    if (M == __builtin_inff() || M == ninf) return;
+    if (BF16) c.launder();
+    /* x = L / T.  d3s_div_rn is q = L y and two fmas wherever T lies in
+     * [2^-20, 2^21) and |L| in [2^-60, 2^100].  Smaller |L| give |x| < 2^-43,
+     * below half an ulp of M when |M| >= 2^-15, so x - M rounds to -M from
+     * either quotient; -inf (masked) and L < -2^100 give the term 0 from
+     * either (-inf, a huge x or NaN all clamp to -43); L > 2^100 sends wave 0
+     * to the slow path, which does not read this sum.  Otherwise (rare) the
+     * half is read again, a chunk at a time, and every term takes
+     * d3s_div_rn. */
+    const uint32_t eb = (d3s_f2u(T) >> 23) & 0xffu;
+    const bool quick = eb >= 127u - 20u && eb <= 127u + 20u && fabsf(M) >= 0x1p-15f;
+    constexpr int H = CPT / 2 * EPC; /* part 0: elements below H */
+    uint64_t acc = 0;
+    if (quick) {
+      auto term = [&](float L) {
+        const float q = L * y;
+        return d3s_fix40_exp(__builtin_fmaf(__builtin_fmaf(-q, T, L), y, q) - M);
+      };
+      /* two terms at a time (few live registers; wave 0 needs the sum only
+       * after its filing and ranking) */
+      if (part == 0) {
+#pragma unroll
+        for (int i = 0; i < H; i++) {
+          acc += term(c.val(i));
+          if (i & 1) __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int i = H; i < NV; i++) {
+          acc += term(c.val(i));
+          if (i & 1) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+      /* one chunk at a time, read again (L2) */
+      using C1 = Chunks<1, BF16>;
+      const uint4 *s1 = src;
+      asm volatile("" : "+s"(s1)); /* a second read: not to be matched with the first */
+      const int jlo = part == 0 ? 0 : CPT / 2, jhi = part == 0 ? CPT / 2 : CPT;
+#pragma unroll 1
+      for (int j = jlo; j < jhi; j++) {
+        const uint4 q = s1[min(j * WAVE + lane, nchunks - 1)];
+        C1 one;
+        one.w[0] = q.x;
+        one.w[1] = q.y;
+        one.w[2] = q.z;
+        one.w[3] = q.w;
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          const int pe = C::pos(pos0, j * EPC + e);
+          const float L = pe == banned ? -__builtin_inff() : one.val(e);
+          acc += (unsigned)pe < (unsigned)V ? d3s_fix40_exp(scale_logit(L, T, y, true) - M) : 0ull;
+        }
+      }
+    }
+    const uint64_t w = wave_sum_u64(acc);
+    if (lane == 0) out[0] = w;
   }
 
   /* the row, once loaded (and masked), to its id */
@@ -603,6 +685,13 @@ struct WaveRow {
 template <int CPT, bool BF16>
 constexpr int wave_occupancy() {
   return BF16 ? (CPT <= 8 ? 5 : 4) : (CPT <= 17 ? 5 : 3);
+}
+/* k_wave_row: at most WR_SPREAD_ROWS one-row workgroups over the CUs, so
+ * four waves per SIMD at most; the exact-sum helpers' terms get the room
+ * (bf16 rows past 5120 elements: three, the room their 64 words need) */
+template <int CPT, bool BF16>
+constexpr int row_occupancy() {
+  return (BF16 && CPT > 10) ? 3 : wave_occupancy<CPT, BF16>() < 4 ? wave_occupancy<CPT, BF16>() : 4;
 }
 
 /* k_linear: the backbone head's logits (src/backbone.c:1213-1215).  Each
@@ -984,24 +1073,22 @@ void k_ras(RasArgs ra, int helpers) {
 }
 
 /* k_wave for small launches: one row per 4-wave workgroup.  Wave 0 samples
- * the row as k_wave's waves do, except for the fast row sum: wave 1 loads the
- * row too (its loads meet wave 0's in L2) and takes the max and the fast sum
- * while wave 0 runs the threshold, the candidates and their filing; wave 0
- * reads lse' after a barrier just before its tail.  Waves 2 and 3 wait, and
- * all four join when the cut needs the exact lse: the row's 2^-40 fixed-point
- * sum of d3s_expf(x - M) (an integer sum, the same in any order), then wave 0
- * runs the tail again with it.  Every wave passes two barriers before the
- * exact sum: wave 0 the first in compute() (or here, on rows that end
- * earlier), the others here. */
+ * the row as k_wave's waves do, except for the row sums: wave 1 loads the row
+ * too (its loads meet wave 0's in L2) and takes the max and the fast sum, and
+ * waves 2 and 3 take the exact row sum's two halves (the 2^-40 fixed-point
+ * sum of d3s_expf(x - M)), while wave 0 runs the threshold, the candidates
+ * and their filing.  Wave 0 reads lse' after the workgroup's one barrier,
+ * just before its tail (or passes it here, on rows that end earlier); a cut
+ * within the fast lse's margin takes the exact lse from the helpers' halves
+ * and the tail goes on in the exact order, with no second pass over the
+ * row. */
 template <int CPT, bool BF16>
-__global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
+__global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(row_occupancy<CPT, BF16>())))
 void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   D3S_HOT_APPLY(a);
   __shared__ WaveLds lds;
-  __shared__ uint32_t need;
-  __shared__ float m_sh;
-  __shared__ uint32_t s_lo[WR], s_hi[WR];
   __shared__ float lse_sh[2];
+  __shared__ uint64_t ex_sh[2];
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id();
   const int row = (int)blockIdx.x;
@@ -1009,42 +1096,25 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   r.V = a.vocab;
   r.k = a.k;
   r.lane = lane;
+  /* the exact-sum helpers' loads wait ~512 cycles: issued with wave 0's,
+   * they share the CU's load path with them (C1 0.2 us slower); a little
+   * later they read L2 after wave 0's row is in, and still finish before
+   * wave 0 reaches its tail (2048 cycles: too late) */
+  if (wid >= 2) __builtin_amdgcn_s_sleep(8);
+  r.load();
   if (wid == 0) {
-    r.defer_exact = true;
     r.lse_in = lse_sh;
-    r.load();
-    const int id = r.compute();
-    if (lane == 0) {
-      need = id == NEED_EXACT ? 1u : 0u;
-      m_sh = r.fin_M;
-    }
+    r.ex_in = ex_sh;
+    r.defer_exact = true; /* (never asked: the helpers' halves are there) */
+    (void)r.compute();
     if (!r.synced) __syncthreads();
   } else {
-    if (wid == 1) {
-      r.load();
+    if (wid == 1)
       r.helper_lse(lse_sh);
-    }
+    else
+      r.helper_exact(&ex_sh[wid - 2], wid - 2);
     __syncthreads();
   }
-  __syncthreads();
-  if (!need) return;
-  const RowP rp = row_params(a, row);
-  const float y = 1.0f / rp.T, M = m_sh;
-  const char *rowp = (const char *)a.logits + (size_t)row * (size_t)a.row_stride * (BF16 ? 2 : 4);
-  uint64_t acc = 0;
-  for (int i = (int)threadIdx.x; i < a.vocab; i += WAVE * WR)
-    acc += d3s_fix40_exp(scale_logit(load_logit<BF16>(rowp, i, rp.banned), rp.T, y, true) - M);
-  const uint64_t w = wave_sum_u64(acc);
-  if (lane == 0) {
-    s_lo[wid] = (uint32_t)w;
-    s_hi[wid] = (uint32_t)(w >> 32);
-  }
-  __syncthreads();
-  if (wid != 0) return;
-  uint64_t tot = 0;
-#pragma unroll
-  for (int q = 0; q < WR; q++) tot += ((uint64_t)s_hi[q] << 32) | s_lo[q];
-  (void)r.exact_tail(M + d3s_logf(d3s_fixsum_to_f32(tot)));
 }
 
 /* The pick alone, one wave per row, after the two draws ran as separate

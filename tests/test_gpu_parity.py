@@ -303,6 +303,38 @@ def test_finite_logit_overflowing_after_temperature(gpu, oracle):
         assert np.all(got["ids"][:3] == -1) and np.all(got["ids"][3:5] == 11)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("op_graph", [False, True])
+def test_exact_row_sum_edges(gpu, oracle, bf16, op_graph):
+    """Every row takes the exact row sum (D3S_FLAG_EXACT_LSE) with tiny, zero
+    and subnormal logits beside ordinary ones, logits below -2^100, rows whose
+    max x lies below 2^-15 (all tiny, or tiny after a large T), and
+    temperatures past 2^21 and at the 1e-5 floor: the one-row kernel's
+    exact-sum helper waves take x = L / T by the product and two fmas only
+    where that cannot change a term."""
+    rng = np.random.default_rng(17)
+    N, V = 10, 4097
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    tiny = np.array([1e-30, -1e-30, 1e-40, -1e-44, 0.0, -0.0, 3e-19, -2e-25, 7e-21], np.float32)
+    x[0, :900] = np.resize(tiny, 900)
+    x[1, ::3] = -1e35
+    x[2, 100:140] = -3e38
+    x[3] = np.resize(tiny, V)
+    x[3, 7] = 1e-6
+    x[4] = (rng.standard_normal(V) * 4e-5).astype(np.float32)
+    x[5, :500] = np.resize(tiny, 500)
+    x[6, :500] = np.resize(tiny, 500)
+    x[7, ::5] = -2e32
+    x[8] = np.resize(tiny, V) * np.float32(1e20)
+    T = np.array([0.7, 1.0, 0.9, 1.0, 1.0, 4194304.0, 1e-5, 3e6, 0.7, 1.3], np.float32)
+    u = oracle.uniform(17, 0, N, 30)
+    if bf16:
+        x = W.f32_to_bf16_bits(x)
+    got, _ = compare(oracle, gpu, x, u, T, 0.9, flags=gpu.FLAG_EXACT_LSE, op_graph=op_graph,
+                     label=f"exact row sum edges bf16={bf16} op_graph={op_graph}")
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] == N
+
+
 @pytest.mark.parametrize("T,top_p", [(0.0, 0.7), (np.inf, 0.9), (np.nan, 0.9), (1e-5, 0.5),
                                      (1e4, 0.8), (0.7, np.nan), (0.7, -1.0), (0.7, 1.0)])
 def test_parameter_edges(gpu, oracle, T, top_p):
