@@ -318,9 +318,9 @@ def single_row_latency(n):
 def other_configs(reps):
     """Launch times of C2, C4 and C5 at their own shapes (BASELINE.json's
     configs; C3 and C1 are the headline).  Events on one stream around
-    back-to-back launches.  C4 and C5 rotate over copies of the inputs
-    totalling over 600 MB (more than twice the 256 MB Infinity Cache), so the
-    reads come from HBM.  C2 (75 KB a launch) is a latency figure: the nine
+    back-to-back launches after SETTLE_S of the same launches.  C4 and C5
+    rotate over copies of the inputs totalling over 600 MB (more than twice
+    the 256 MB Infinity Cache), so the reads come from HBM.  C2 (75 KB a launch) is a latency figure: the nine
     codebook rows as nine one-row launches (as the tower samples them) and as
     one nine-row launch, p50 over `reps` repetitions."""
     import d3s
@@ -376,9 +376,19 @@ def other_configs(reps):
             log(f"C2: one 9-row launch p50 {out[name]['one_launch_p50_us']:.2f} us, "
                 f"9 one-row launches p50 {out[name]['nine_launches_p50_us']:.2f} us")
             continue
+        # a first estimate of the launch time, then SETTLE_S of the same
+        # launches back to back (as before every headline phase), then the
+        # timed launches
+        a.record(s)
         for c in range(copies):
             assert launch(c) == 0
-        n = max(2 * copies, 20)
+        b.record(s)
+        b.synchronize()
+        t_est = a.elapsed_ms(b) * 1e-3 / copies
+        for i in range(settle_launches(t_est)):
+            assert launch(i % copies) == 0
+        hiprt.synchronize()
+        n = max(2 * copies, 100)
         a.record(s)
         for i in range(n):
             assert launch(i % copies) == 0
@@ -401,10 +411,17 @@ def other_configs(reps):
     lg, u, ids = hiprt.to_device(x), hiprt.DeviceBuffer(N * Vc * 4), hiprt.DeviceBuffer(4 * N)
     assert d3s.lib().d3s_uniform_fill(u.ptr, N * Vc, 42, 0, None) == 0
     hiprt.synchronize()
+    a.record(s)
     for _ in range(2):
         assert d3s.sample_raw(lg.ptr, d3s.DTYPE_BF16, N, Vc, Vc, u.ptr, Vc, 1.0, 0.9, None, ids.ptr,
                               stream=s.ptr) == 0
-    n = 10
+    b.record(s)
+    b.synchronize()
+    for _ in range(settle_launches(a.elapsed_ms(b) * 1e-3 / 2)):
+        assert d3s.sample_raw(lg.ptr, d3s.DTYPE_BF16, N, Vc, Vc, u.ptr, Vc, 1.0, 0.9, None, ids.ptr,
+                              stream=s.ptr) == 0
+    hiprt.synchronize()
+    n = 40
     a.record(s)
     for _ in range(n):
         assert d3s.sample_raw(lg.ptr, d3s.DTYPE_BF16, N, Vc, Vc, u.ptr, Vc, 1.0, 0.9, None, ids.ptr,
