@@ -229,9 +229,9 @@ struct WaveRow {
    * (the rows that end earlier pass it in the kernel) */
   const float *lse_in = nullptr;
   bool synced = false;
-  /* k_wave_row: the exact row sum's two halves (2^-40 fixed point), filed by
-   * helper waves before that same barrier; a cut within the fast lse's margin
-   * takes the exact lse from them */
+  /* k_wave_row: the exact row sum's three shares (2^-40 fixed point), filed
+   * by the helper waves before that same barrier; a cut within the fast lse's
+   * margin takes the exact lse from them */
   const uint64_t *ex_in = nullptr;
   C c; /* -inf outside the row and at the banned index */
 
@@ -346,7 +346,7 @@ struct WaveRow {
     fin_M = M;
     fin_noise = noise;
     return wave_tail(a, row, key, M, lse, exact, eps_s, noise, top_p, S.buf, [&]() {
-      if (ex_in) return M + d3s_logf(d3s_fixsum_to_f32(ex_in[0] + ex_in[1]));
+      if (ex_in) return M + d3s_logf(d3s_fixsum_to_f32(ex_in[0] + ex_in[1] + ex_in[2]));
       return defer_exact ? __builtin_nanf("") : exact_lse<CPT, BF16>(ref(), M);
     });
   }
@@ -399,7 +399,7 @@ struct WaveRow {
    * fast_lse, filed at out[0..1] for wave 0.  Rows that compute() ends
    * before its tail (refused, all -inf, T not finite, logits too large for
    * the fast sum: the same tests on the same values) file nothing. */
-  __device__ __forceinline__ void helper_lse(float *out) {
+  __device__ __forceinline__ void helper_lse(float *out, uint64_t *ex_out = nullptr) {
     if (!t_finite) return;
     const float ninf = -__builtin_inff();
     const float cf = LOG2E_F / T;
@@ -420,16 +420,75 @@ struct WaveRow {
       out[0] = lse;
       out[1] = eps_s;
     }
+    if (ex_out) { /* k_wave_row: the first share of the exact row sum */
+      if (BF16) c.launder();
+      const uint64_t w = exact_part<0, EX1>(M);
+      if (lane == 0) ex_out[0] = w;
+    }
   }
 
-  /* k_wave_row's exact-sum helper waves: the row's max as compute() takes it
-   * (the same M), then half the row's terms fix40(d3s_expf(x - M)) (part 0:
-   * each lane's first CPT / 2 chunks, part 1 the rest; masked elements
-   * hold -inf, whose term is 0), summed over the wave and filed at out[0].
-   * An integer sum, the same in any order: the two halves add to the oracle's
-   * row sum.  Rows that compute() ends at the max (refused, all -inf, T not
-   * finite: the same tests on the same values) file nothing; every other row
-   * files, whichever path wave 0 then takes. */
+  /* k_wave_row's three shares of the exact row sum, by element of each lane:
+   * wave 1 (after its fast sum) [0, EX1), waves 2 and 3 [EX1, EX2) and
+   * [EX2, NV) (about a fifth and two halves of the rest: each files before
+   * wave 0 reaches its tail) */
+  static constexpr int EX1 = (NV / 5) & ~1;
+  static constexpr int EX2 = EX1 + (NV - EX1) / 2;
+
+  /* the terms fix40(d3s_expf(x - M)) of elements [LO, HI) of every lane,
+   * summed over the wave (masked elements hold -inf, whose term is 0).  An
+   * integer sum, the same in any order: the shares add to the oracle's row
+   * sum.
+   * x = L / T: d3s_div_rn is q = L y and two fmas wherever T lies in
+   * [2^-20, 2^21) and |L| in [2^-60, 2^100].  Smaller |L| give |x| < 2^-43,
+   * below half an ulp of M when |M| >= 2^-15, so x - M rounds to -M from
+   * either quotient; -inf (masked) and L < -2^100 give the term 0 from either
+   * (-inf, a huge x or NaN all clamp to -43); L > 2^100 sends wave 0 to the
+   * slow path, which does not read this sum.  Otherwise (rare) the chunks are
+   * read again, one at a time, and every term takes d3s_div_rn. */
+  template <int LO, int HI>
+  __device__ __forceinline__ uint64_t exact_part(float M) {
+    const uint32_t eb = (d3s_f2u(T) >> 23) & 0xffu;
+    const bool quick = eb >= 127u - 20u && eb <= 127u + 20u && fabsf(M) >= 0x1p-15f;
+    uint64_t acc = 0;
+    if (quick) {
+      /* two terms at a time (few live registers) */
+#pragma unroll
+      for (int i = LO; i < HI; i++) {
+        const float L = c.val(i);
+        const float q = L * y;
+        acc += d3s_fix40_exp(__builtin_fmaf(__builtin_fmaf(-q, T, L), y, q) - M);
+        if ((i - LO) & 1) __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      using C1 = Chunks<1, BF16>;
+      const uint4 *s1 = src;
+      asm volatile("" : "+s"(s1)); /* a second read: not to be matched with the first */
+#pragma unroll 1
+      for (int j = LO / EPC; j < (HI + EPC - 1) / EPC; j++) {
+        const uint4 q = s1[min(j * WAVE + lane, nchunks - 1)];
+        C1 one;
+        one.w[0] = q.x;
+        one.w[1] = q.y;
+        one.w[2] = q.z;
+        one.w[3] = q.w;
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          const int i = j * EPC + e;
+          const int pe = C::pos(pos0, i);
+          const float L = pe == banned ? -__builtin_inff() : one.val(e);
+          const bool take = i >= LO && i < HI && (unsigned)pe < (unsigned)V;
+          acc += take ? d3s_fix40_exp(scale_logit(L, T, y, true) - M) : 0ull;
+        }
+      }
+    }
+    return wave_sum_u64(acc);
+  }
+
+  /* waves 2 and 3 of k_wave_row: the row's max as compute() takes it (the
+   * same M), then their share of the exact row sum, filed at out[0].  Rows
+   * that compute() ends at the max (refused, all -inf, T not finite: the same
+   * tests on the same values) file nothing; every other row files, whichever
+   * path wave 0 then takes. */
   __device__ __forceinline__ void helper_exact(uint64_t *out, int part) {
     if (!t_finite) return;
     const float ninf = -__builtin_inff();
@@ -441,61 +500,7 @@ struct WaveRow {
     const float M = scale_logit(Lmax, T, y, true);
     if (M == __builtin_inff() || M == ninf) return;
     if (BF16) c.launder();
-    /* x = L / T.  d3s_div_rn is q = L y and two fmas wherever T lies in
-     * [2^-20, 2^21) and |L| in [2^-60, 2^100].  Smaller |L| give |x| < 2^-43,
-     * below half an ulp of M when |M| >= 2^-15, so x - M rounds to -M from
-     * either quotient; -inf (masked) and L < -2^100 give the term 0 from
-     * either (-inf, a huge x or NaN all clamp to -43); L > 2^100 sends wave 0
-     * to the slow path, which does not read this sum.  Otherwise (rare) the
-     * half is read again, a chunk at a time, and every term takes
-     * d3s_div_rn. */
-    const uint32_t eb = (d3s_f2u(T) >> 23) & 0xffu;
-    const bool quick = eb >= 127u - 20u && eb <= 127u + 20u && fabsf(M) >= 0x1p-15f;
-    constexpr int H = CPT / 2 * EPC; /* part 0: elements below H */
-    uint64_t acc = 0;
-    if (quick) {
-      auto term = [&](float L) {
-        const float q = L * y;
-        return d3s_fix40_exp(__builtin_fmaf(__builtin_fmaf(-q, T, L), y, q) - M);
-      };
-      /* two terms at a time (few live registers; wave 0 needs the sum only
-       * after its filing and ranking) */
-      if (part == 0) {
-#pragma unroll
-        for (int i = 0; i < H; i++) {
-          acc += term(c.val(i));
-          if (i & 1) __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-#pragma unroll
-        for (int i = H; i < NV; i++) {
-          acc += term(c.val(i));
-          if (i & 1) __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    } else {
-      /* one chunk at a time, read again (L2) */
-      using C1 = Chunks<1, BF16>;
-      const uint4 *s1 = src;
-      asm volatile("" : "+s"(s1)); /* a second read: not to be matched with the first */
-      const int jlo = part == 0 ? 0 : CPT / 2, jhi = part == 0 ? CPT / 2 : CPT;
-#pragma unroll 1
-      for (int j = jlo; j < jhi; j++) {
-        const uint4 q = s1[min(j * WAVE + lane, nchunks - 1)];
-        C1 one;
-        one.w[0] = q.x;
-        one.w[1] = q.y;
-        one.w[2] = q.z;
-        one.w[3] = q.w;
-#pragma unroll
-        for (int e = 0; e < EPC; e++) {
-          const int pe = C::pos(pos0, j * EPC + e);
-          const float L = pe == banned ? -__builtin_inff() : one.val(e);
-          acc += (unsigned)pe < (unsigned)V ? d3s_fix40_exp(scale_logit(L, T, y, true) - M) : 0ull;
-        }
-      }
-    }
-    const uint64_t w = wave_sum_u64(acc);
+    const uint64_t w = part == 0 ? exact_part<EX1, EX2>(M) : exact_part<EX2, NV>(M);
     if (lane == 0) out[0] = w;
   }
 
@@ -1074,21 +1079,21 @@ void k_ras(RasArgs ra, int helpers) {
 
 /* k_wave for small launches: one row per 4-wave workgroup.  Wave 0 samples
  * the row as k_wave's waves do, except for the row sums: wave 1 loads the row
- * too (its loads meet wave 0's in L2) and takes the max and the fast sum, and
- * waves 2 and 3 take the exact row sum's two halves (the 2^-40 fixed-point
- * sum of d3s_expf(x - M)), while wave 0 runs the threshold, the candidates
- * and their filing.  Wave 0 reads lse' after the workgroup's one barrier,
- * just before its tail (or passes it here, on rows that end earlier); a cut
- * within the fast lse's margin takes the exact lse from the helpers' halves
- * and the tail goes on in the exact order, with no second pass over the
- * row. */
+ * too (its loads meet wave 0's in L2) and takes the max, the fast sum and a
+ * fifth of the exact row sum (the 2^-40 fixed-point sum of d3s_expf(x - M)),
+ * waves 2 and 3 the rest of the exact sum, while wave 0 runs the threshold,
+ * the candidates and their filing.  Wave 0 reads lse' after the workgroup's
+ * one barrier, just before its tail (or passes it here, on rows that end
+ * earlier); a cut within the fast lse's margin takes the exact lse from the
+ * helpers' shares and the tail goes on in the exact order, with no second
+ * pass over the row. */
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(row_occupancy<CPT, BF16>())))
 void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   D3S_HOT_APPLY(a);
   __shared__ WaveLds lds;
   __shared__ float lse_sh[2];
-  __shared__ uint64_t ex_sh[2];
+  __shared__ uint64_t ex_sh[3];
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id();
   const int row = (int)blockIdx.x;
@@ -1110,9 +1115,9 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
     if (!r.synced) __syncthreads();
   } else {
     if (wid == 1)
-      r.helper_lse(lse_sh);
+      r.helper_lse(lse_sh, &ex_sh[0]);
     else
-      r.helper_exact(&ex_sh[wid - 2], wid - 2);
+      r.helper_exact(&ex_sh[wid - 1], wid - 2);
     __syncthreads();
   }
 }
