@@ -200,6 +200,27 @@ __device__ __forceinline__ float slow_max(const RowRef &R) {
   return __ballot(bad) ? __builtin_nanf("") : wave_max_f(xm);
 }
 
+/* The candidates as a bit per element, no branches: element i of word i / 32
+ * at bit 31 - i % 32, set when v(i) >= t.  For t finite or +inf and v(i)
+ * finite or -inf, v - t is negative exactly when v < t (a difference is zero
+ * only between equal values, +0 then; a flushed one keeps its sign; -inf
+ * gives -inf), so its sign bit is the element's bit inverted: each word
+ * takes (w << 1) | sign(v - t) (one v_alignbit after the subtraction; the
+ * words' chains are independent), then is inverted; the last word's padding
+ * shifts out. */
+template <int NV, class F>
+__device__ __forceinline__ void cand_bits(uint32_t (&bits)[(NV + 31) / 32], F &&v, float t) {
+  constexpr int NWORD = (NV + 31) / 32;
+  uint32_t below[NWORD];
+#pragma unroll
+  for (int w = 0; w < NWORD; w++) below[w] = 0u;
+#pragma unroll
+  for (int i = 0; i < NV; i++) below[i / 32] = (below[i / 32] << 1) | (d3s_f2u(v(i) - t) >> 31);
+#pragma unroll
+  for (int w = 0; w < NWORD; w++) bits[w] = ~below[w];
+  if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
+}
+
 template <int CPT, bool BF16>
 struct WaveRow {
   /* candidates per lane read again while the row is still in L2 */
@@ -552,18 +573,7 @@ struct WaveRow {
      * at bit 31 - i % 32), no branches */
     constexpr int NWORD = (NV + 31) / 32;
     uint32_t bits[NWORD];
-#pragma unroll
-    for (int w = 0; w < NWORD; w++) bits[w] = 0u;
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-      /* bits = 2 bits + (v >= tau_lo): the compare's lane mask as the carry in
-       * (two wait states between a VALU write of vcc and its use as a mask) */
-      asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-          : "+v"(bits[i / 32])
-          : "v"(c.val(i)), "v"(tau_lo)
-          : "vcc");
-    }
-    if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
+    cand_bits<NV>(bits, [&](int i) { return c.val(i); }, tau_lo);
     int cnt = 0;
 #pragma unroll
     for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
@@ -909,16 +919,7 @@ void k_wide(SampleArgs a) {
   if (BF16) c.launder();
   constexpr int NWORD = (NV + 31) / 32;
   uint32_t bits[NWORD];
-#pragma unroll
-  for (int w = 0; w < NWORD; w++) bits[w] = 0u;
-#pragma unroll
-  for (int i = 0; i < NV; i++) {
-    asm("v_cmp_ge_f32 vcc, %1, %2\n\ts_nop 1\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-        : "+v"(bits[i / 32])
-        : "v"(c.val(i)), "v"(tau_lo)
-        : "vcc");
-  }
-  if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
+  cand_bits<NV>(bits, [&](int i) { return c.val(i); }, tau_lo);
   int cnt = 0;
 #pragma unroll
   for (int w = 0; w < NWORD; w++) cnt += __popc(bits[w]);
