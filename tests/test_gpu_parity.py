@@ -335,6 +335,33 @@ def test_exact_row_sum_edges(gpu, oracle, bf16, op_graph):
     assert got["counters"][gpu.COUNTER_EXACT_LSE] == N
 
 
+@pytest.mark.parametrize("bf16,V", [(False, 200), (False, 1500), (False, 3000), (False, 4097),
+                                    (False, 6000), (True, 1000), (True, 3000), (True, 5000),
+                                    (True, 8000)])
+def test_exact_row_sum_shares_every_width(gpu, oracle, bf16, V):
+    """Every row width the one-row kernel is built for (fp32 4, 8, 16, 17, 24
+    and bf16 4, 8, 10, 16 chunks a lane), every row taking the exact row sum
+    (D3S_FLAG_EXACT_LSE): the helper waves' three shares of it must add to
+    the oracle's sum at each width's split of the lanes' elements.  Rows
+    with T past 2^21 take the shares' re-read with the exact quotient; every
+    row has a banned index."""
+    rng = np.random.default_rng(300 + V)
+    N = 12
+    x = (rng.standard_normal((N, V)) * 2.5).astype(np.float32)
+    x[np.arange(N), rng.integers(0, V, N)] += 7.0
+    T = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    T[3] = 3e6
+    T[7] = 4194304.0
+    top_p = rng.uniform(0.5, 0.99, N).astype(np.float32)
+    ban = rng.integers(0, V, N).astype(np.int32)
+    u = oracle.uniform(300 + V, 0, N, 30)
+    if bf16:
+        x = W.f32_to_bf16_bits(x)
+    got, _ = compare(oracle, gpu, x, u, T, top_p, banned=ban, flags=gpu.FLAG_EXACT_LSE,
+                     label=f"exact row sum shares V={V} bf16={bf16}")
+    assert got["counters"][gpu.COUNTER_EXACT_LSE] == N
+
+
 @pytest.mark.parametrize("T,top_p", [(0.0, 0.7), (np.inf, 0.9), (np.nan, 0.9), (1e-5, 0.5),
                                      (1e4, 0.8), (0.7, np.nan), (0.7, -1.0), (0.7, 1.0)])
 def test_parameter_edges(gpu, oracle, T, top_p):
