@@ -237,8 +237,9 @@ struct WaveRow {
   const char *rowp;
   float T, y, uval, top_p;
   bool t_finite;
-  /* a cut that needs the exact lse returns NEED_EXACT (helper waves of the
-   * workgroup compute it) instead of the wave computing it alone */
+  /* a cut that needs the exact lse returns NEED_EXACT instead of the wave
+   * computing it alone (k_wave_row sets it beside ex_in, whose shares answer
+   * first: it keeps the one-wave exact pass out of that kernel's code) */
   bool defer_exact = false;
   float fin_M = 0.0f, fin_noise = 0.0f; /* the tail's max x and noise */
   /* the candidates from the registers (staged in LDS) instead of read again
@@ -1111,7 +1112,7 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   if (wid == 0) {
     r.lse_in = lse_sh;
     r.ex_in = ex_sh;
-    r.defer_exact = true; /* (never asked: the helpers' halves are there) */
+    r.defer_exact = true; /* (never reached: ex_in answers first) */
     (void)r.compute();
     if (!r.synced) __syncthreads();
   } else {
