@@ -665,8 +665,11 @@ def frame_latency(reps):
 def c_caller_latency(calls):
     """C1 one-row calls timed by drama3-mlx_amd/d3s_latency, a C program
     linked to the library (what a C caller such as tower.c sees, without
-    Python's call overhead): host call-to-synchronize p50 and event p50.  Run
-    in a child process before this process touches the GPU."""
+    Python's call overhead): host call-to-synchronize p50, call-to-done p50
+    when the caller polls the stream, and event p50; then the same under
+    spin-wait scheduling (hipDeviceScheduleSpin, set by the child before any
+    other HIP call).  Run in child processes before this process touches the
+    GPU."""
     import subprocess
     import tempfile
     import d3s_workloads as W
@@ -679,13 +682,21 @@ def c_caller_latency(calls):
         with open(path, "wb") as f:
             f.write(np.ascontiguousarray(w["logits"], np.float32).tobytes())
             f.write(np.ascontiguousarray(w["u"], np.float32).tobytes())
-        r = subprocess.run([exe, path, "256", str(V), str(K), str(calls), "0.7", "0.7"], capture_output=True,
-                           text=True, timeout=300)
-    if r.returncode != 0:
-        log(f"d3s_latency failed: {r.stderr.strip()[-300:]}")
-        return None
-    res = json.loads(r.stdout.strip().splitlines()[-1])
-    log(f"C caller, C1 one row: host p50 {res['host_p50_us']:.2f} us, event p50 {res['event_p50_us']:.2f} us")
+        runs = {}
+        for mode in ("default", "spin"):
+            extra = ["spin"] if mode == "spin" else []
+            r = subprocess.run([exe, path, "256", str(V), str(K), str(calls), "0.7", "0.7"] + extra,
+                               capture_output=True, text=True, timeout=300)
+            if r.returncode != 0:
+                log(f"d3s_latency ({mode}) failed: {r.stderr.strip()[-300:]}")
+                return None
+            runs[mode] = json.loads(r.stdout.strip().splitlines()[-1])
+    res = runs["default"]
+    res["spin_wait"] = {key: runs["spin"][key] for key in ("host_p50_us", "host_p90_us", "host_poll_p50_us",
+                                                           "host_poll_p90_us")}
+    log(f"C caller, C1 one row: host p50 {res['host_p50_us']:.2f} us (blocking synchronize), "
+        f"{res['host_poll_p50_us']:.2f} us (polling the stream), {res['spin_wait']['host_p50_us']:.2f} us "
+        f"(synchronize under spin-wait scheduling); event p50 {res['event_p50_us']:.2f} us")
     return res
 
 

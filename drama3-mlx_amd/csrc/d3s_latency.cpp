@@ -1,18 +1,24 @@
 /* Host-side latency of one-row d3s_sample calls as a C caller of the library
  * sees them (tower_decode_step samples one row at a time, src/tower.c:420-446):
- * per call, the wall time from the call to the return of hipStreamSynchronize,
- * and, in a second pass, HIP events around the launch.
+ * per call, the wall time from the call to its return (the enqueue) and to the
+ * return of hipStreamSynchronize;
+ * in a second pass, from the call until hipStreamQuery reports the stream
+ * done (the caller polls instead of blocking); in a third, HIP events around
+ * the launch.  With "spin" as the last argument the process asks for
+ * spin-wait scheduling (hipDeviceScheduleSpin) before any other HIP call, so
+ * hipStreamSynchronize polls too.
  *
  * Input: a raw file holding fp32 logits [n_rows, V] then fp32 uniforms
  * [n_rows, k] (bench.py writes it).  Calls cycle over the rows.  Output: one
  * JSON line on stdout.
- *   usage: d3s_latency <file> <n_rows> <V> <k> <calls> <temperature> <top_p> */
+ *   usage: d3s_latency <file> <n_rows> <V> <k> <calls> <temperature> <top_p> [spin] */
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <time.h>
 
 #include <algorithm>
+#include <string>
 #include <vector>
 
 #include "../../include/d3s_sampler.h"
@@ -42,7 +48,10 @@ double pct(std::vector<double> v, double q) {
 }  // namespace
 
 int main(int argc, char **argv) {
-  if (argc != 8) fail("usage: d3s_latency <file> <n_rows> <V> <k> <calls> <temperature> <top_p>", argc);
+  if (argc != 8 && argc != 9) fail("usage: d3s_latency <file> <n_rows> <V> <k> <calls> <temperature> <top_p> [spin]", argc);
+  const bool spin = argc == 9 && std::string(argv[8]) == "spin";
+  if (argc == 9 && !spin) fail("the last argument, when given, is spin", 0);
+  if (spin) check(hipSetDeviceFlags(hipDeviceScheduleSpin), "hipSetDeviceFlags");
   const int n_rows = atoi(argv[2]), V = atoi(argv[3]), k = atoi(argv[4]), calls = atoi(argv[5]);
   const float T = (float)atof(argv[6]), top_p = (float)atof(argv[7]);
   if (n_rows < 1 || V < 1 || k < 1 || calls < 1) fail("bad sizes", 0);
@@ -66,16 +75,34 @@ int main(int argc, char **argv) {
   check(hipEventCreate(&a), "hipEventCreate");
   check(hipEventCreate(&b), "hipEventCreate");
   const int warm = 100;
-  std::vector<double> host_us, event_us;
+  std::vector<double> host_us, call_us, event_us;
   for (int i = 0; i < warm + calls; i++) {
     const int r = i % n_rows;
     const double t0 = now_us();
     const int rc = d3s_sample(logits + (size_t)r * V, D3S_DTYPE_F32, 1, V, V, u + (size_t)r * k, k, nullptr,
                               nullptr, T, top_p, nullptr, ids, nullptr, nullptr, nullptr, 0u, s);
+    const double tc = now_us();
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     const double t1 = now_us();
     if (rc != D3S_OK) fail("d3s_sample", rc);
-    if (i >= warm) host_us.push_back(t1 - t0);
+    if (i >= warm) {
+      host_us.push_back(t1 - t0);
+      call_us.push_back(tc - t0);
+    }
+  }
+  std::vector<double> poll_us;
+  for (int i = 0; i < warm + calls; i++) {
+    const int r = i % n_rows;
+    const double t0 = now_us();
+    const int rc = d3s_sample(logits + (size_t)r * V, D3S_DTYPE_F32, 1, V, V, u + (size_t)r * k, k, nullptr,
+                              nullptr, T, top_p, nullptr, ids, nullptr, nullptr, nullptr, 0u, s);
+    hipError_t q;
+    while ((q = hipStreamQuery(s)) == hipErrorNotReady) {
+    }
+    check(q, "hipStreamQuery");
+    const double t1 = now_us();
+    if (rc != D3S_OK) fail("d3s_sample", rc);
+    if (i >= warm) poll_us.push_back(t1 - t0);
   }
   for (int i = 0; i < warm + calls; i++) {
     const int r = i % n_rows;
@@ -89,9 +116,11 @@ int main(int argc, char **argv) {
     check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
     if (i >= warm) event_us.push_back(ms * 1e3);
   }
-  printf("{\"calls\": %d, \"rows\": %d, \"host_p50_us\": %.3f, \"host_p90_us\": %.3f, "
+  printf("{\"calls\": %d, \"rows\": %d, \"spin\": %s, \"call_p50_us\": %.3f, \"host_p50_us\": %.3f, \"host_p90_us\": %.3f, "
+         "\"host_poll_p50_us\": %.3f, \"host_poll_p90_us\": %.3f, "
          "\"event_p50_us\": %.3f, \"event_p90_us\": %.3f}\n",
-         calls, n_rows, pct(host_us, 0.5), pct(host_us, 0.9), pct(event_us, 0.5), pct(event_us, 0.9));
+         calls, n_rows, spin ? "true" : "false", pct(call_us, 0.5), pct(host_us, 0.5), pct(host_us, 0.9), pct(poll_us, 0.5),
+         pct(poll_us, 0.9), pct(event_us, 0.5), pct(event_us, 0.9));
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   (void)hipStreamDestroy(s);
