@@ -597,8 +597,10 @@ def frame_latency(reps):
     it, the reference's own sampler micro-benchmark (tools/bench.c:287-328,
     "samplers (11)"): eleven sample_top_k_top_p calls on fp32 [1, 4097]
     uniform(0, 1) logits with T 1.0, top_k 30, top_p 0.9 (bench.c:313), here
-    eleven pairs of d3s_uniform_fill and d3s_sample.  p50 / p90 of events
-    around each frame over `reps` frames, and the host wall time per frame."""
+    eleven d3s_sample_seeded calls (sample_top_k_top_p's draw and kernel in
+    one launch, as the shim runs it), and beside them eleven pairs of
+    d3s_uniform_fill and d3s_sample.  p50 / p90 of events around each frame
+    over `reps` frames, and the host wall time per frame."""
     import d3s
     import d3s_workloads as W
     import hiprt
@@ -631,12 +633,17 @@ def frame_latency(reps):
 
     def samplers11(i):
         for j in range(11):
+            assert d3s.sample_seeded_raw(lg.ptr, d3s.DTYPE_F32, 1, V, V, 42, 11 * i + j, K, 1.0, 0.9, None,
+                                         ids11.ptr + 4 * j, stream=s.ptr) == 0
+
+    def samplers11_pairs(i):
+        for j in range(11):
             assert L.d3s_uniform_fill(u11.ptr + j * K * 4, K, 42, 11 * i + j, s.ptr) == 0
             assert d3s.sample_raw(lg.ptr, d3s.DTYPE_F32, 1, V, V, u11.ptr + j * K * 4, K, 1.0, 0.9, None,
                                   ids11.ptr + 4 * j, stream=s.ptr) == 0
 
     out = {}
-    for name, fn in (("frame", one_frame), ("samplers_11", samplers11)):
+    for name, fn in (("frame", one_frame), ("samplers_11", samplers11), ("samplers_11_pairs", samplers11_pairs)):
         ev, wall = [], []
         for i in range(reps + 20):
             t0 = time.perf_counter()
@@ -653,12 +660,15 @@ def frame_latency(reps):
     out["frame"]["launches"] = 10
     out["frame"]["what"] = ("d3s_sample_ras on bf16 [1,4097] (both draws) + 9 d3s_sample on bf16 [1,4096], "
                             "one stream (src/tower.c:420-446)")
-    out["samplers_11"]["launches"] = 22
-    out["samplers_11"]["what"] = ("11 x (d3s_uniform_fill + d3s_sample) on fp32 [1,4097] uniform(0,1) logits, "
-                                  "T 1.0, top_k 30, top_p 0.9 (tools/bench.c:313)")
+    out["samplers_11"]["launches"] = 11
+    out["samplers_11"]["what"] = ("11 x d3s_sample_seeded (the uniform draw and the sample in one launch) on fp32 "
+                                  "[1,4097] uniform(0,1) logits, T 1.0, top_k 30, top_p 0.9 (tools/bench.c:313)")
+    out["samplers_11_pairs"]["launches"] = 22
+    out["samplers_11_pairs"]["what"] = ("the same as 11 x (d3s_uniform_fill + d3s_sample)")
     s.destroy()
     log(f"frame (RAS + 9 codebooks, 10 launches): p50 {out['frame']['p50_us']:.2f} us; "
-        f"samplers (11) as tools/bench.c: p50 {out['samplers_11']['p50_us']:.2f} us")
+        f"samplers (11) as tools/bench.c: p50 {out['samplers_11']['p50_us']:.2f} us in 11 launches, "
+        f"{out['samplers_11_pairs']['p50_us']:.2f} us as 22")
     return out
 
 

@@ -216,28 +216,28 @@ int check_caller_ws(const void *ws, int64_t bytes, size_t need) {
 
 enum class WsMode { Stream, Scratch, Caller };
 
-/* d3s_sample's checks and routing, with the workspace from the stream's
- * block, the static scratch or the caller */
-int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
-                const float *u, int k, const float *temperature, const float *top_p, float temperature_scalar,
-                float top_p_scalar, const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
-                uint32_t *counters, unsigned flags, void *stream, WsMode mode, void *ws = nullptr,
-                int64_t ws_bytes = 0) {
+/* the checks every d3s_sample form shares and its arguments, all but the
+ * uniforms; D3S_OK (and n_rows 0: nothing to launch) or the status */
+int sample_args(d3s::SampleArgs &a, const void *logits, int dtype, int64_t n_rows, int64_t vocab,
+                int64_t row_stride, int k, const float *temperature, const float *top_p,
+                float temperature_scalar, float top_p_scalar, const int32_t *banned, int32_t *ids, float *probs,
+                int32_t *cand, uint32_t *counters, unsigned flags) {
   if (dtype != D3S_DTYPE_F32 && dtype != D3S_DTYPE_BF16) return D3S_ERR_DTYPE;
   const int shape = check_shape(n_rows, vocab, row_stride, k);
   if (shape != D3S_OK) return shape;
   if ((flags & ~SAMPLE_FLAGS) != 0u) return D3S_ERR_ARG;
   if (n_rows == 0) return D3S_OK;
-  if (!logits || !u || !ids) return D3S_ERR_ARG;
+  if (!logits || !ids) return D3S_ERR_ARG;
   /* rows are addressed in whole elements */
   if ((uintptr_t)logits % (dtype == D3S_DTYPE_F32 ? 4u : 2u) != 0u) return D3S_ERR_ARG;
-  d3s::SampleArgs a;
   a.logits = logits;
   a.row_stride = row_stride;
   a.vocab = (int)vocab;
   a.k = k;
   a.n_rows = (int)n_rows;
-  a.u = u;
+  a.u = nullptr;
+  a.u_seed = 0;
+  a.u_stream = 0;
   a.temperature = temperature;
   a.top_p = top_p;
   a.temperature_scalar = temperature_scalar;
@@ -249,6 +249,22 @@ int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, in
   a.counters = counters;
   a.flags = flags;
   a.opgraph = d3s::op_graph_order(a.vocab, k, (flags & D3S_FLAG_OP_GRAPH) || env_no_fused());
+  return D3S_OK;
+}
+
+/* d3s_sample's checks and routing, with the workspace from the stream's
+ * block, the static scratch or the caller */
+int sample_call(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                const float *u, int k, const float *temperature, const float *top_p, float temperature_scalar,
+                float top_p_scalar, const int32_t *banned, int32_t *ids, float *probs, int32_t *cand,
+                uint32_t *counters, unsigned flags, void *stream, WsMode mode, void *ws = nullptr,
+                int64_t ws_bytes = 0) {
+  d3s::SampleArgs a;
+  const int arc = sample_args(a, logits, dtype, n_rows, vocab, row_stride, k, temperature, top_p,
+                              temperature_scalar, top_p_scalar, banned, ids, probs, cand, counters, flags);
+  if (arc != D3S_OK || n_rows == 0) return arc;
+  if (!u) return D3S_ERR_ARG;
+  a.u = u;
   const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
   hipStream_t s = (hipStream_t)stream;
   const size_t need = routed_workspace_bytes(a, dt);
@@ -507,6 +523,23 @@ int d3s_sample_ws(const void *logits, int dtype, int64_t n_rows, int64_t vocab, 
   return sample_call(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, temperature_scalar,
                      top_p_scalar, banned, ids, probs, cand, counters, flags, stream, WsMode::Caller, workspace,
                      workspace_bytes);
+}
+
+int d3s_sample_seeded(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                      uint64_t seed, uint64_t stream_id, int k, const float *temperature, const float *top_p,
+                      float temperature_scalar, float top_p_scalar, const int32_t *banned, int32_t *ids,
+                      float *probs, int32_t *cand, uint32_t *counters, unsigned flags, void *stream) {
+  d3s::SampleArgs a;
+  const int arc = sample_args(a, logits, dtype, n_rows, vocab, row_stride, k, temperature, top_p,
+                              temperature_scalar, top_p_scalar, banned, ids, probs, cand, counters, flags);
+  if (arc != D3S_OK || n_rows == 0) return arc;
+  a.u_seed = seed;
+  a.u_stream = stream_id;
+  /* the one-wave kernels draw the uniforms themselves; no other route does */
+  if ((flags & D3S_FLAG_GENERIC) != 0u) return D3S_ERR_UNSUPPORTED;
+  const d3s::Dtype dt = dtype == D3S_DTYPE_F32 ? d3s::DT_F32 : d3s::DT_BF16;
+  if (!d3s::launch_wave(a, dt, (hipStream_t)stream)) return D3S_ERR_UNSUPPORTED;
+  return launched();
 }
 
 int64_t d3s_sample_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab, int k, unsigned flags) {

@@ -16,7 +16,9 @@ struct SampleArgs {
   int vocab;                /* V */
   int k;                    /* uniform columns per row, 1 <= k <= V */
   int n_rows;
-  const float *u;           /* [n_rows, k] */
+  const float *u;           /* [n_rows, k]; null: the one-wave kernels draw u[r, j] =
+                               d3s_uniform(u_seed, u_stream, r k + j) themselves */
+  uint64_t u_seed, u_stream;
   const float *temperature; /* [n_rows] or null -> temperature_scalar */
   const float *top_p;       /* [n_rows] or null -> top_p_scalar */
   float temperature_scalar;

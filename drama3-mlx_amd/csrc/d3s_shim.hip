@@ -119,6 +119,22 @@ d3s_array sample_top_k_top_p(d3s_array logits, float temperature, int top_k, flo
   const int V = logits->cols, N = logits->rows;
   const int k = top_k < V ? top_k : V; /* src/sampling.c:207 */
   if (k < 1) die("sample_top_k_top_p: top_k must be at least 1");
+  if (logits->dtype != D3S_ARRAY_F32 && logits->dtype != D3S_ARRAY_BF16)
+    die("sample_top_k_top_p: logits must be fp32 or bf16");
+  /* the draw and the kernel in one launch where the one-wave kernel holds
+   * the rows (it draws the uniforms itself: the same bits), else the draw
+   * into u and the kernel on it */
+  d3s_array ids = new_device(D3S_ARRAY_I32, N, 1);
+  ids->ndim = 1; /* int32 [N] */
+  ids->sampled = true;
+  const int rc = d3s_sample_seeded(logits->data, logits->dtype == D3S_ARRAY_F32 ? D3S_DTYPE_F32 : D3S_DTYPE_BF16,
+                                   N, V, logits->row_stride, g_seed, g_draw, k, nullptr, nullptr, temperature,
+                                   top_p, nullptr, (int32_t *)ids->data, nullptr, nullptr, nullptr, 0u, nullptr);
+  if (rc == D3S_OK) {
+    g_draw++;
+    return ids;
+  }
+  if (rc != D3S_ERR_UNSUPPORTED) die("sampling kernel failed (status %d)", rc); /* src/sampling.c:169-170 */
   d3s_array u = new_device(D3S_ARRAY_F32, N, k);
   if (d3s_uniform_fill((float *)u->data, (int64_t)N * k, g_seed, g_draw++, nullptr) != D3S_OK)
     die("uniform draw failed");

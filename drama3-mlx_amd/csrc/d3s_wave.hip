@@ -221,7 +221,9 @@ __device__ __forceinline__ void cand_bits(uint32_t (&bits)[(NV + 31) / 32], F &&
   if (NV % 32) bits[NWORD - 1] <<= 32 - NV % 32;
 }
 
-template <int CPT, bool BF16>
+/* DRAW: the call gives no u; the row's uniforms are drawn here (only the
+ * one-row kernel is built so: the other forms keep no trace of it) */
+template <int CPT, bool BF16, bool DRAW = false>
 struct WaveRow {
   /* candidates per lane read again while the row is still in L2 */
   static constexpr int EARLY = 3;
@@ -288,14 +290,19 @@ struct WaveRow {
 
   /* the row's temperature, banned index and uniform (top_p, which only the
    * tail needs, later), loaded before the row so that waiting for them does
-   * not wait for it; params_done() takes them once the row's loads are out */
+   * not wait for it; params_done() takes them once the row's loads are out
+   * (and draws the uniform when the call gives none) */
   uint32_t t_word, b_word;
   __device__ __forceinline__ void params() {
     t_word = a.temperature ? row_word(a.temperature) : d3s_f2u(a.temperature_scalar);
     b_word = a.banned ? row_word(a.banned) : 0xffffffffu;
-    uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
+    if constexpr (!DRAW) uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
   }
   __device__ __forceinline__ void params_done() {
+    /* DRAW: this lane's uniform drawn here, while the row's loads are in
+     * flight (the same bits as d3s_uniform_fill's element r k + lane) */
+    if constexpr (DRAW)
+      uval = lane < k ? d3s_uniform(a.u_seed, a.u_stream, (uint64_t)row * (uint64_t)k + (uint64_t)lane) : 0.0f;
     const float t = d3s_u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)t_word));
     T = t < 1e-5f ? 1e-5f : t; /* src/sampling.c:16,195 */
     banned = __builtin_amdgcn_readfirstlane((int)b_word);
@@ -1089,7 +1096,7 @@ void k_ras(RasArgs ra, int helpers) {
  * earlier); a cut within the fast lse's margin takes the exact lse from the
  * helpers' shares and the tail goes on in the exact order, with no second
  * pass over the row. */
-template <int CPT, bool BF16>
+template <int CPT, bool BF16, bool DRAW = false>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(row_occupancy<CPT, BF16>())))
 void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   D3S_HOT_APPLY(a);
@@ -1099,7 +1106,7 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id();
   const int row = (int)blockIdx.x;
-  WaveRow<CPT, BF16> r(a, lds, row);
+  WaveRow<CPT, BF16, DRAW> r(a, lds, row);
   r.V = a.vocab;
   r.k = a.k;
   r.lane = lane;
@@ -1174,7 +1181,11 @@ bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
   /* a launch too small to fill the chip spreads its rows one per workgroup
    * over more CUs, with three helper waves for the exact lse; larger ones
    * pack WR rows, which keeps the CUs fuller */
-  if (a.n_rows <= WR_SPREAD_ROWS)
+  if (!a.u) { /* the call's draw in the kernel: one-row launches only */
+    if (a.n_rows > WR_SPREAD_ROWS) return false;
+    hipLaunchKernelGGL((k_wave_row<CPT, BF16, true>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s,
+                       D3S_HOT_ARGS(a), a);
+  } else if (a.n_rows <= WR_SPREAD_ROWS)
     hipLaunchKernelGGL((k_wave_row<CPT, BF16>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s, D3S_HOT_ARGS(a), a);
   else
     hipLaunchKernelGGL((k_wave<CPT, BF16>), dim3((unsigned)((a.n_rows + WR - 1) / WR)), dim3(WAVE * WR), 0, s,

@@ -67,6 +67,9 @@ def lib():
         L.d3s_sample_ws.argtypes = [vp, i32, i64, i64, i64, vp, i32, vp, vp, f32, f32, vp, vp, vp, vp,
                                     vp, u32, vp, i64, vp]
         L.d3s_sample_ws.restype = i32
+        L.d3s_sample_seeded.argtypes = [vp, i32, i64, i64, i64, ctypes.c_uint64, ctypes.c_uint64, i32, vp, vp,
+                                        f32, f32, vp, vp, vp, vp, vp, u32, vp]
+        L.d3s_sample_seeded.restype = i32
         L.d3s_sample_workspace_bytes.argtypes = [i32, i64, i64, i32, u32]
         L.d3s_sample_workspace_bytes.restype = i64
         L.d3s_workspace_init.argtypes = [vp, i64, vp]
@@ -128,6 +131,17 @@ def sample_raw(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_
               banned, ids, probs, cand, counters, flags, stream)
 
 
+def sample_seeded_raw(logits, dtype, n_rows, vocab, row_stride, seed, draw, k, temperature, top_p, banned, ids,
+                      probs=None, cand=None, counters=None, flags=0, stream=None):
+    """d3s_sample_seeded on device pointers (ints): the uniforms drawn in the
+    kernel from (seed, draw), as d3s_uniform_fill would write them.
+    temperature / top_p as in sample_raw."""
+    t_ptr, t_s = (temperature[1], 0.0) if isinstance(temperature, tuple) else (None, float(temperature))
+    p_ptr, p_s = (top_p[1], 0.0) if isinstance(top_p, tuple) else (None, float(top_p))
+    return lib().d3s_sample_seeded(logits, dtype, n_rows, vocab, row_stride, seed, draw, k, t_ptr, p_ptr, t_s,
+                                   p_s, banned, ids, probs, cand, counters, flags, stream)
+
+
 def workspace_bytes(dtype, n_rows, vocab, k, flags=0):
     """d3s_sample_workspace_bytes: the workspace d3s_sample_ws needs (or a
     negative status)."""
@@ -154,11 +168,12 @@ class Workspace:
 
 
 def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True, row_stride=None,
-           vocab=None, stream=None, noalloc=False, workspace=None):
+           vocab=None, stream=None, noalloc=False, workspace=None, seed_draw=None):
     """Host arrays in, host arrays out (copies through device memory).
     logits: float32 or uint16 (bf16 bits) [N, row_stride]; u: float32 [N, k];
-    temperature / top_p: scalars or float32 [N].  Returns dict(ids, probs, cand,
-    counters, rc)."""
+    temperature / top_p: scalars or float32 [N].  seed_draw = (seed, draw):
+    d3s_sample_seeded instead, u then an int, k.  Returns dict(ids, probs,
+    cand, counters, rc)."""
     import hiprt
     logits = np.ascontiguousarray(logits)
     dtype = DTYPE_F32 if logits.dtype == np.float32 else DTYPE_BF16
@@ -167,10 +182,14 @@ def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True,
     N = logits.shape[0]
     stride = logits.shape[1] if row_stride is None else row_stride
     V = stride if vocab is None else vocab
-    u = np.ascontiguousarray(u, np.float32)
-    k = u.shape[1]
-    bufs = dict(logits=hiprt.to_device(logits), u=hiprt.to_device(u),
-                ids=hiprt.DeviceBuffer(4 * N), counters=hiprt.DeviceBuffer(4 * NUM_COUNTERS).zero())
+    bufs = dict(logits=hiprt.to_device(logits), ids=hiprt.DeviceBuffer(4 * N),
+                counters=hiprt.DeviceBuffer(4 * NUM_COUNTERS).zero())
+    if seed_draw is None:
+        u = np.ascontiguousarray(u, np.float32)
+        k = u.shape[1]
+        bufs["u"] = hiprt.to_device(u)
+    else:
+        k = int(u)
     if want_probs:
         bufs["probs"] = hiprt.DeviceBuffer(4 * N * k)
         bufs["cand"] = hiprt.DeviceBuffer(4 * N * k)
@@ -186,11 +205,17 @@ def sample(logits, u, temperature, top_p, banned=None, flags=0, want_probs=True,
     if banned is not None:
         bufs["ban"] = hiprt.to_device(np.asarray(banned, np.int32))
         ban = bufs["ban"].ptr
-    rc = sample_raw(bufs["logits"].ptr, dtype, N, V, stride, bufs["u"].ptr, k, T, P, ban,
-                    bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
-                    bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
-                    stream.ptr if stream else None, noalloc=noalloc,
-                    workspace=workspace.arg() if isinstance(workspace, Workspace) else workspace)
+    if seed_draw is not None:
+        rc = sample_seeded_raw(bufs["logits"].ptr, dtype, N, V, stride, seed_draw[0], seed_draw[1], k, T, P,
+                               ban, bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
+                               bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
+                               stream.ptr if stream else None)
+    else:
+        rc = sample_raw(bufs["logits"].ptr, dtype, N, V, stride, bufs["u"].ptr, k, T, P, ban,
+                        bufs["ids"].ptr, bufs["probs"].ptr if want_probs else None,
+                        bufs["cand"].ptr if want_probs else None, bufs["counters"].ptr, flags,
+                        stream.ptr if stream else None, noalloc=noalloc,
+                        workspace=workspace.arg() if isinstance(workspace, Workspace) else workspace)
     out = dict(rc=rc)
     if rc != OK:
         return out

@@ -42,7 +42,7 @@ extern "C" {
 /* status codes */
 #define D3S_OK 0
 #define D3S_ERR_ARG -1         /* shape, pointer or parameter out of range */
-#define D3S_ERR_UNSUPPORTED -2 /* vocab (and so k) beyond D3S_MAX_VOCAB */
+#define D3S_ERR_UNSUPPORTED -2 /* vocab (and so k) beyond D3S_MAX_VOCAB; d3s_sample_seeded: rows the one-wave kernel does not hold */
 #define D3S_ERR_LAUNCH -3      /* the HIP launch failed */
 #define D3S_ERR_DTYPE -4       /* unknown logits dtype */
 #define D3S_ERR_NOMEM -5       /* the library's workspace could not be allocated */
@@ -274,6 +274,23 @@ int d3s_linear_sample_bf16_ws(const uint16_t *x, const uint16_t *w, int64_t n_ro
  * Replaces: m_uniform (src/mlxu.c:771-774) as used by sample_top_k_top_p
  * (src/sampling.c:208); the MLX generator itself is not reproduced. */
 int d3s_uniform_fill(float *u, int64_t n, uint64_t seed, uint64_t draw, void *stream);
+
+/* d3s_uniform_fill(u, n_rows * k, seed, draw) then d3s_sample with that u,
+ * in one launch: the one-wave kernel draws each rank's uniform itself (the
+ * same bits), so no u is written or read.  Same arguments, checks and
+ * results as that pair, with (seed, draw) in u's place.  Only the one-wave
+ * kernel's one-row-a-workgroup form draws them: launches of more than 1024
+ * rows, rows it does not hold (k above 64; rows longer than 6144 fp32 / 8192
+ * bf16 elements, or 6141 / 8185 where the base or the stride leaves a row
+ * start off 16 bytes) and D3S_FLAG_GENERIC return D3S_ERR_UNSUPPORTED with
+ * nothing launched; take the pair there.  Never allocates.
+ * Replaces: sample_top_k_top_p's draw and kernel call together
+ * (src/sampling.c:205-209: m_uniform at :208, the call at :209); no single
+ * reference function does both. */
+int d3s_sample_seeded(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                      uint64_t seed, uint64_t draw, int k, const float *temperature, const float *top_p,
+                      float temperature_scalar, float top_p_scalar, const int32_t *banned, int32_t *ids,
+                      float *probs, int32_t *cand, uint32_t *counters, unsigned flags, void *stream);
 
 /* The largest k d3s_sample accepts (D3S_MAX_VOCAB: any k up to the row's
  * vocab), and the largest vocab the fused kernel takes for a dtype (wider

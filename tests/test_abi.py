@@ -80,6 +80,27 @@ def test_argument_validation_without_device(lib):
     assert d3s.sample_raw(**{**base, "n_rows": 0}) == 0  # nothing to do, nothing launched
 
 
+def test_seeded_validation_without_device(lib):
+    """d3s_sample_seeded: d3s_sample's checks, and the routes whose kernels
+    read u from memory refused before anything is launched."""
+    import d3s
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below returns before a launch
+    base = dict(logits=p.value, dtype=0, n_rows=4, vocab=100, row_stride=100, seed=1, draw=2, k=10,
+                temperature=1.0, top_p=0.9, banned=None, ids=p.value)
+    assert d3s.sample_seeded_raw(**{**base, "dtype": 5}) == -4
+    assert d3s.sample_seeded_raw(**{**base, "k": 0}) == -1
+    assert d3s.sample_seeded_raw(**{**base, "k": 101}) == -1
+    assert d3s.sample_seeded_raw(**{**base, "ids": None}) == -1
+    assert d3s.sample_seeded_raw(**{**base, "flags": 64}) == -1
+    assert d3s.sample_seeded_raw(**{**base, "n_rows": 0}) == 0
+    assert d3s.sample_seeded_raw(**{**base, "flags": 1}) == -2  # D3S_FLAG_GENERIC
+    assert d3s.sample_seeded_raw(**{**base, "k": 65}) == -2
+    # rows longer than one wave's registers: 6141 fp32 / 8185 bf16 at a row start off 16 bytes
+    assert d3s.sample_seeded_raw(**{**base, "vocab": 6142, "row_stride": 6142}) == -2
+    assert d3s.sample_seeded_raw(**{**base, "dtype": 1, "vocab": 8186, "row_stride": 8186}) == -2
+    assert d3s.sample_seeded_raw(**{**base, "n_rows": 1025}) == -2  # more rows than one a workgroup
+
+
 def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
     """No CPU fallback: with the built library absent, the first call into the
     product raises instead of computing anything."""
