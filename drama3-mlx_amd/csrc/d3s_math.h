@@ -350,7 +350,11 @@ D3S_HD float d3s_uniform(uint64_t seed, uint64_t stream, uint64_t index) {
   c.v[2] = (uint32_t)stream;
   c.v[3] = (uint32_t)(stream >> 32);
   const d3s_u32x4 o = d3s_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
-  const uint32_t w = o.v[index & 3];
+  /* selects, not o.v[index & 3]: a run-time index into the array makes the
+   * device compiler move it to LDS, which needs the dispatch packet and so
+   * costs the kernel two preloaded argument registers */
+  const uint32_t j = (uint32_t)index & 3u;
+  const uint32_t w = j == 0 ? o.v[0] : j == 1 ? o.v[1] : j == 2 ? o.v[2] : o.v[3];
   return (float)(w >> 8) * 0x1.0p-24f;
 }
 

@@ -257,6 +257,10 @@ struct WaveRow {
    * by the helper waves before that same barrier; a cut within the fast lse's
    * margin takes the exact lse from them */
   const uint64_t *ex_in = nullptr;
+  /* DRAW, k_wave_row: the race's noise per lane, filed by helper wave 2
+   * before that same barrier (its ten Philox rounds and the seed's kernarg
+   * read then stay off wave 0's path) */
+  const float *noise_in = nullptr;
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -291,7 +295,7 @@ struct WaveRow {
   /* the row's temperature, banned index and uniform (top_p, which only the
    * tail needs, later), loaded before the row so that waiting for them does
    * not wait for it; params_done() takes them once the row's loads are out
-   * (and draws the uniform when the call gives none) */
+   * (DRAW: no u; draw_noise() draws it) */
   uint32_t t_word, b_word;
   __device__ __forceinline__ void params() {
     t_word = a.temperature ? row_word(a.temperature) : d3s_f2u(a.temperature_scalar);
@@ -299,10 +303,6 @@ struct WaveRow {
     if constexpr (!DRAW) uval = lane < k ? a.u[(size_t)row * k + lane] : 0.0f;
   }
   __device__ __forceinline__ void params_done() {
-    /* DRAW: this lane's uniform drawn here, while the row's loads are in
-     * flight (the same bits as d3s_uniform_fill's element r k + lane) */
-    if constexpr (DRAW)
-      uval = lane < k ? d3s_uniform(a.u_seed, a.u_stream, (uint64_t)row * (uint64_t)k + (uint64_t)lane) : 0.0f;
     const float t = d3s_u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)t_word));
     T = t < 1e-5f ? 1e-5f : t; /* src/sampling.c:16,195 */
     banned = __builtin_amdgcn_readfirstlane((int)b_word);
@@ -394,7 +394,7 @@ struct WaveRow {
     const float M = slow_max<CPT, BF16>(R);
     if (d3s_isnan(M) || M == -__builtin_inff()) return wave_write_special(a, row, !d3s_isnan(M));
     const int n = exact_select<CPT, BF16>(R);
-    return finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, -d3s_logf(1.0f - uval), true);
+    return finish(n, M, exact_lse<CPT, BF16>(R, M), true, 0.0f, own_noise(), true);
   }
 
   /* The fast row sum S' = sum 2^(L c + b) over the row (b = -RN(Lmax c)),
@@ -533,10 +533,26 @@ struct WaveRow {
     if (lane == 0) out[0] = w;
   }
 
+  /* DRAW: the race's noise -log(1 - u) from this lane's uniform, drawn here
+   * (the same bits as d3s_uniform_fill's element r k + lane; u = 0 on lanes
+   * past k, as the regular kernels' uval) */
+  __device__ __forceinline__ float draw_noise() const {
+    const float u =
+        lane < k ? d3s_uniform(a.u_seed, a.u_stream, (uint64_t)row * (uint64_t)k + (uint64_t)lane) : 0.0f;
+    return -d3s_logf(1.0f - u);
+  }
+  __device__ __forceinline__ float own_noise() const {
+    if constexpr (DRAW)
+      return draw_noise();
+    else
+      return -d3s_logf(1.0f - uval);
+  }
+
   /* the row, once loaded (and masked), to its id */
   __device__ __forceinline__ int compute() {
     const float ninf = -__builtin_inff();
-    const float noise = -d3s_logf(1.0f - uval); /* the race's noise needs only u */
+    /* the race's noise needs only u (DRAW: taken after the barrier below) */
+    float noise = DRAW ? 0.0f : own_noise();
     bool slow = !t_finite;
     const float cf = slow ? 0.0f : LOG2E_F / T; /* needs only T: off the max's path */
     float M = 0.0f, b = 0.0f, delta = 0.0f, lm = ninf;
@@ -694,6 +710,7 @@ struct WaveRow {
       lse = lse_in[0];
       eps_s = lse_in[1];
     }
+    if constexpr (DRAW) noise = (noise_in && synced) ? noise_in[lane] : draw_noise();
     return finish(n, M, lse, false, eps_s, noise, need_sel);
   }
 
@@ -1103,6 +1120,7 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
   __shared__ WaveLds lds;
   __shared__ float lse_sh[2];
   __shared__ uint64_t ex_sh[3];
+  __shared__ float noise_sh[DRAW ? WAVE : 1];
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id();
   const int row = (int)blockIdx.x;
@@ -1120,9 +1138,13 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
     r.lse_in = lse_sh;
     r.ex_in = ex_sh;
     r.defer_exact = true; /* (never reached: ex_in answers first) */
+    if constexpr (DRAW) r.noise_in = noise_sh;
     (void)r.compute();
     if (!r.synced) __syncthreads();
   } else {
+    /* DRAW: wave 2 draws while its share's loads are in flight */
+    if constexpr (DRAW)
+      if (wid == 2) noise_sh[lane] = r.draw_noise();
     if (wid == 1)
       r.helper_lse(lse_sh, &ex_sh[0]);
     else
