@@ -8,6 +8,8 @@
 #include "d3s_internal.h"
 #include "d3s_math.h"
 
+#include <type_traits>
+
 namespace d3s {
 namespace {
 
@@ -165,6 +167,37 @@ __device__ __forceinline__ int key_idx(uint64_t key) { return (int)(~(uint32_t)k
     (a).vocab = hot_vocab;                                                                                \
     (a).k = hot_k;                                                                                        \
     (a).flags = hot_flags;                                                                                \
+  } while (0)
+
+/* The same for kernels that draw their uniforms (u null), in the same slots
+ * with other types: the seed in u's, the width, k and the flags in one word
+ * (vocab | k << 16 | flags << 24: vocab < 2^16, k and flags < 2^8, checked
+ * before launch) and the draw's stream in the room of k and the flags, so
+ * that the draw needs no kernarg read either.  D3S_HOT_PARAMS_T(DRAW) names
+ * the one list or the other for a kernel templated on DRAW. */
+#define D3S_HOT_PARAMS_T(DRAW)                                                                            \
+  const void *hot_logits, int64_t hot_stride, const int32_t *hot_banned, const float *hot_temperature,    \
+      std::conditional_t<DRAW, uint64_t, const float *> hot_u, float hot_T,                               \
+      std::conditional_t<DRAW, uint32_t, int> hot_vocab, std::conditional_t<DRAW, uint32_t, int> hot_k,   \
+      unsigned hot_flags
+#define D3S_DRAW_ARGS(a)                                                                                  \
+  (a).logits, (a).row_stride, (a).banned, (a).temperature, (a).u_seed, (a).temperature_scalar,           \
+      (uint32_t)(a).vocab | (uint32_t)(a).k << 16 | (a).flags << 24, (uint32_t)(a).u_stream,              \
+      (unsigned)((a).u_stream >> 32)
+#define D3S_DRAW_FITS(a) ((a).vocab < 0x10000 && (a).k < 0x100 && (a).flags < 0x100u)
+#define D3S_DRAW_APPLY(a)                                                                                 \
+  do {                                                                                                    \
+    (a).logits = hot_logits;                                                                              \
+    (a).row_stride = hot_stride;                                                                          \
+    (a).banned = hot_banned;                                                                              \
+    (a).temperature = hot_temperature;                                                                    \
+    (a).u = nullptr;                                                                                      \
+    (a).u_seed = (uint64_t)hot_u;                                                                         \
+    (a).temperature_scalar = hot_T;                                                                       \
+    (a).vocab = (int)(hot_vocab & 0xffffu);                                                               \
+    (a).k = (int)((hot_vocab >> 16) & 0xffu);                                                             \
+    (a).flags = hot_vocab >> 24;                                                                          \
+    (a).u_stream = (uint64_t)hot_k | (uint64_t)hot_flags << 32;                                           \
   } while (0)
 
 struct RowP {

@@ -261,6 +261,7 @@ struct WaveRow {
    * before that same barrier (its ten Philox rounds and the seed's kernarg
    * read then stay off wave 0's path) */
   const float *noise_in = nullptr;
+  float *noise_out = nullptr; /* set on the helper that files it */
   C c; /* -inf outside the row and at the banned index */
 
   __device__ WaveRow(const SampleArgs &a_, WaveLds &S_, int row_) : a(a_), S(S_), row(row_) {}
@@ -321,6 +322,10 @@ struct WaveRow {
     else
       c.load(src, nchunks, lane);
     params_done();
+    /* DRAW: the helper that files the race's noise draws it here, while the
+     * row's loads are in flight (the masking below waits for them) */
+    if constexpr (DRAW)
+      if (noise_out) noise_out[lane] = draw_noise();
     /* the partial chunk at the row start and every chunk row from the one
      * holding the row end on */
     const int jlast = (nchunks - 1) / WAVE;
@@ -1115,8 +1120,11 @@ void k_ras(RasArgs ra, int helpers) {
  * pass over the row. */
 template <int CPT, bool BF16, bool DRAW = false>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(row_occupancy<CPT, BF16>())))
-void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
-  D3S_HOT_APPLY(a);
+void k_wave_row(D3S_HOT_PARAMS_T(DRAW), SampleArgs a) {
+  if constexpr (DRAW)
+    D3S_DRAW_APPLY(a);
+  else
+    D3S_HOT_APPLY(a);
   __shared__ WaveLds lds;
   __shared__ float lse_sh[2];
   __shared__ uint64_t ex_sh[3];
@@ -1133,6 +1141,8 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
    * later they read L2 after wave 0's row is in, and still finish before
    * wave 0 reaches its tail (2048 cycles: too late) */
   if (wid >= 2) __builtin_amdgcn_s_sleep(8);
+  if constexpr (DRAW)
+    if (wid == 2) r.noise_out = noise_sh;
   r.load();
   if (wid == 0) {
     r.lse_in = lse_sh;
@@ -1142,9 +1152,6 @@ void k_wave_row(D3S_HOT_PARAMS, SampleArgs a) {
     (void)r.compute();
     if (!r.synced) __syncthreads();
   } else {
-    /* DRAW: wave 2 draws while its share's loads are in flight */
-    if constexpr (DRAW)
-      if (wid == 2) noise_sh[lane] = r.draw_noise();
     if (wid == 1)
       r.helper_lse(lse_sh, &ex_sh[0]);
     else
@@ -1204,9 +1211,9 @@ bool try_wave(const SampleArgs &a, int max_off, hipStream_t s) {
    * over more CUs, with three helper waves for the exact lse; larger ones
    * pack WR rows, which keeps the CUs fuller */
   if (!a.u) { /* the call's draw in the kernel: one-row launches only */
-    if (a.n_rows > WR_SPREAD_ROWS) return false;
+    if (a.n_rows > WR_SPREAD_ROWS || !D3S_DRAW_FITS(a)) return false;
     hipLaunchKernelGGL((k_wave_row<CPT, BF16, true>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s,
-                       D3S_HOT_ARGS(a), a);
+                       D3S_DRAW_ARGS(a), a);
   } else if (a.n_rows <= WR_SPREAD_ROWS)
     hipLaunchKernelGGL((k_wave_row<CPT, BF16>), dim3((unsigned)a.n_rows), dim3(WAVE * WR), 0, s, D3S_HOT_ARGS(a), a);
   else
