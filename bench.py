@@ -211,6 +211,31 @@ def head_probe(one_launch, n=20):
         hiprt.synchronize()
 
 
+def samplers_probe(n=50):
+    """The reference's samplers(11) loop (tools/bench.c:287-328): eleven
+    samples on fp32 [1, 4097] uniform(0, 1) logits, T 1.0, top_k 30, top_p 0.9,
+    n times as eleven d3s_sample_seeded launches and then as eleven pairs of
+    d3s_uniform_fill and d3s_sample (the same uniforms), each group followed by
+    a synchronisation."""
+    import d3s
+    import hiprt
+    Vs, k = 4097, 30
+    rng = np.random.default_rng(31)
+    lg = hiprt.to_device(rng.random((1, Vs)).astype(np.float32))
+    u = hiprt.DeviceBuffer(4 * 11 * k)
+    ids = hiprt.DeviceBuffer(4 * 11)
+    for i in range(n):
+        for j in range(11):
+            assert d3s.sample_seeded_raw(lg.ptr, d3s.DTYPE_F32, 1, Vs, Vs, 42, 11 * i + j, k, 1.0, 0.9, None,
+                                         ids.ptr + 4 * j) == 0
+        hiprt.synchronize()
+        for j in range(11):
+            assert d3s.lib().d3s_uniform_fill(u.ptr + j * k * 4, k, 42, 11 * i + j, None) == 0
+            assert d3s.sample_raw(lg.ptr, d3s.DTYPE_F32, 1, Vs, Vs, u.ptr + j * k * 4, k, 1.0, 0.9, None,
+                                  ids.ptr + 4 * j) == 0
+        hiprt.synchronize()
+
+
 def counter_probe(name, pool, g_head):
     """For rocprofv3 --pmc runs: the calibration copy, then launches of one
     workload only, each followed by a synchronisation, so every other dispatch
@@ -219,13 +244,18 @@ def counter_probe(name, pool, g_head):
     1025 (four rows per workgroup, k_wave); c2: 50 C2
     launches (nine rows); c3one: 50 one-batch C3 launches; c3: 20 headline
     launches (g_head batches each); c4 / c5: 20 launches of C4 / C5 (ids only);
-    head / head1: 20 backbone-head gemv + sample calls, two launches / one."""
+    head / head1: 20 backbone-head gemv + sample calls, two launches / one;
+    samplers: the samplers(11) loop 50 times, seeded and as pairs."""
     import d3s
     import d3s_workloads as W
     import hiprt
     calibration_copy()
     if name in ("head", "head1"):
         head_probe(name == "head1")
+        log(f"counter probe {name}: done")
+        return
+    if name == "samplers":
+        samplers_probe()
         log(f"counter probe {name}: done")
         return
     if name in ("c3", "c3one"):
@@ -807,7 +837,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the C2 / C4 / C5 figures")
     ap.add_argument("--counter-probe", choices=["c1", "c1rows", "c1long", "c2", "c3one", "c3", "c4", "c5", "head",
-                                                "head1"], default=None,
+                                                "head1", "samplers"], default=None,
                     help="only run one workload's launches (for --pmc runs)")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="N",
                     help="only run the copy calibration and N headline launches (for --pmc runs)")
