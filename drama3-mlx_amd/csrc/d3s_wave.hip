@@ -466,7 +466,10 @@ struct WaveRow {
    * [EX2, NV) (about a fifth and two halves of the rest: each files before
    * wave 0 reaches its tail) */
   static constexpr int EX1 = (NV / 5) & ~1;
-  static constexpr int EX2 = EX1 + (NV - EX1) / 2;
+  /* (DRAW: wave 2 also draws the race's noise, ten Philox rounds and a log:
+   * it takes 3/8 of the rest, wave 3 the other 5/8, so the two file about
+   * together) */
+  static constexpr int EX2 = EX1 + (DRAW ? ((NV - EX1) * 3 / 8) & ~1 : (NV - EX1) / 2);
 
   /* the terms fix40(d3s_expf(x - M)) of elements [LO, HI) of every lane,
    * summed over the wave (masked elements hold -inf, whose term is 0).  An
