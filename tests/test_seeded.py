@@ -27,14 +27,17 @@ def flat_uniforms(oracle, seed, draw, n, k):
     return oracle.uniform(seed, draw, 1, n * k).reshape(n, k)
 
 
-def check(oracle, gpu, x, k, T, top_p, seed, draw, banned=None, flags=0, label=""):
+def check(oracle, gpu, x, k, T, top_p, seed, draw, banned=None, flags=0, label="", vocab=None):
+    """vocab: rows of that many elements read at x's row stride (the oracle
+    gets the rows alone)"""
     print(f"[seeded] {label} shape={x.shape} k={k} flags={flags}", flush=True)
     u = flat_uniforms(oracle, seed, draw, x.shape[0], k)
-    got = gpu.sample(x, k, T, top_p, banned=banned, flags=flags, seed_draw=(seed, draw))
+    sub = dict(row_stride=x.shape[1], vocab=vocab) if vocab else {}
+    got = gpu.sample(x, k, T, top_p, banned=banned, flags=flags, seed_draw=(seed, draw), **sub)
     assert got["rc"] == 0, got["rc"]
-    exp = oracle.sample(x, u, T, top_p, banned=banned, n_threads=8,
-                        op_graph=bool(flags & gpu.FLAG_OP_GRAPH))
-    pair = gpu.sample(x, u, T, top_p, banned=banned, flags=flags)
+    exp = oracle.sample(np.ascontiguousarray(x[:, :vocab]) if vocab else x, u, T, top_p, banned=banned,
+                        n_threads=8, op_graph=bool(flags & gpu.FLAG_OP_GRAPH))
+    pair = gpu.sample(x, u, T, top_p, banned=banned, flags=flags, **sub)
     assert pair["rc"] == 0
     bad = np.nonzero(got["ids"] != exp["ids"])[0]
     parity_report.record(f"seeded {label}", len(exp["ids"]), len(bad), 0)
@@ -67,6 +70,21 @@ def test_seeded_widths(gpu, oracle, bf16, V, k):
     if bf16:
         x = W.f32_to_bf16_bits(x)
     check(oracle, gpu, x, k, T, top_p, 7, 1234567890123, banned=ban, label=f"V={V} k={k} bf16={bf16}")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_seeded_high_words_and_row_stride(gpu, oracle, bf16):
+    """Seeds and draws with their high 32 bits set (the kernel takes both as
+    leading arguments, the draw split into two words), on rows read at a
+    stride wider than the row."""
+    rng = np.random.default_rng(91 + bf16)
+    V, stride = 3001, 3072
+    x = (rng.standard_normal((24, stride)) * 2.5).astype(np.float32)
+    if bf16:
+        x = W.f32_to_bf16_bits(x)
+    for seed, draw in ((0xFEDCBA9876543210, 0x8000000000000007), (0x100000000, 0xFFFFFFFF)):
+        check(oracle, gpu, x, 30, 0.9, 0.85, seed, draw, vocab=V,
+              label=f"seed={seed:#x} draw={draw:#x} V={V} stride={stride} bf16={bf16}")
 
 
 def test_seeded_largest_launch_and_flags(gpu, oracle):
