@@ -258,8 +258,8 @@ struct WaveRow {
    * margin takes the exact lse from them */
   const uint64_t *ex_in = nullptr;
   /* DRAW, k_wave_row: the race's noise per lane, filed by helper wave 2
-   * before that same barrier (its ten Philox rounds and the seed's kernarg
-   * read then stay off wave 0's path) */
+   * before that same barrier (its ten Philox rounds and the logarithm then
+   * stay off wave 0's path) */
   const float *noise_in = nullptr;
   float *noise_out = nullptr; /* set on the helper that files it */
   C c; /* -inf outside the row and at the banned index */
