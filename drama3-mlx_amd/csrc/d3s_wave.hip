@@ -1080,17 +1080,45 @@ __device__ __forceinline__ void ras_pick(const RasArgs &ra, int row, int id1, in
  * draws' temperatures differ), as k_wave_row's wave 1 does; every wave then
  * passes one barrier before the draws' tails.  Otherwise a workgroup of four
  * waves takes two rows. */
+/* k_ras's leading arguments, preloaded into SGPRs as D3S_HOT_PARAMS are for
+ * the other one-wave kernels: what both draws' waves need before their row
+ * loads (the shared logits, stride, width and row count, each draw's
+ * uniforms and temperature, and kk = k | retry k << 8 | helpers << 16).  The
+ * draws' per-row temperature and banned arrays are never set on this route
+ * and their flags are 0 (checked before launch): the waves take them so.
+ * 52 bytes, no padding. */
+#define D3S_RAS_HOT_PARAMS                                                                                \
+  const void *hot_logits, int64_t hot_stride, const float *hot_u, const float *hot_u_retry, float hot_T,  \
+      float hot_T_retry, int hot_vocab, int hot_rows, uint32_t hot_kk
+#define D3S_RAS_HOT_ARGS(r, helpers)                                                                      \
+  (r).first.logits, (r).first.row_stride, (r).first.u, (r).retry.u, (r).first.temperature_scalar,        \
+      (r).retry.temperature_scalar, (r).first.vocab, (r).first.n_rows,                                    \
+      (uint32_t)(r).first.k | (uint32_t)(r).retry.k << 8 | (uint32_t)(helpers) << 16
+
 template <int CPT, bool BF16>
 __global__ __launch_bounds__(WAVE *WR) __attribute__((amdgpu_waves_per_eu(wave_occupancy<CPT, BF16>())))
-void k_ras(RasArgs ra, int helpers) {
+void k_ras(D3S_RAS_HOT_PARAMS, RasArgs ra) {
   __shared__ WaveLds lds_all[WR];
   __shared__ int drawn[WR];
   __shared__ float lse_sh[2][2];
+  const int helpers = (int)(hot_kk >> 16);
+  const int n_rows = hot_rows;
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
-  const int row = helpers ? (int)blockIdx.x : (int)(blockIdx.x * (blockDim.x / WAVE / 2)) + wid / 2;
+  /* (blocks of WAVE * WR threads, as launched) */
+  const int row = helpers ? (int)blockIdx.x : (int)(blockIdx.x * (WR / 2)) + wid / 2;
   const bool retry = (wid & 1) != 0;
   const int lane = lane_id();
-  const SampleArgs &a = retry ? ra.retry : ra.first;
+  SampleArgs a = retry ? ra.retry : ra.first; /* the fields the tail needs, later */
+  a.logits = hot_logits;
+  a.row_stride = hot_stride;
+  a.vocab = hot_vocab;
+  a.n_rows = n_rows;
+  a.u = retry ? hot_u_retry : hot_u;
+  a.temperature = nullptr;
+  a.temperature_scalar = retry ? hot_T_retry : hot_T;
+  a.banned = nullptr;
+  a.k = (int)((hot_kk >> (retry ? 8 : 0)) & 0xffu);
+  a.flags = 0u;
   WaveRow<CPT, BF16> r(a, lds_all[wid], row);
   r.V = a.vocab;
   r.k = a.k;
@@ -1099,7 +1127,7 @@ void k_ras(RasArgs ra, int helpers) {
     r.load();
     r.helper_lse(lse_sh[wid & 1]);
     __syncthreads();
-  } else if (row < ra.first.n_rows) {
+  } else if (row < n_rows) {
     if (helpers) r.lse_in = lse_sh[wid & 1];
     r.load();
     const int id = r.compute();
@@ -1107,7 +1135,7 @@ void k_ras(RasArgs ra, int helpers) {
     if (helpers && !r.synced) __syncthreads();
   }
   __syncthreads();
-  if (retry || (helpers && wid >= 2) || row >= ra.first.n_rows) return;
+  if (retry || (helpers && wid >= 2) || row >= n_rows) return;
   ras_pick(ra, row, drawn[wid], drawn[wid + 1]);
 }
 
@@ -1259,13 +1287,18 @@ bool try_ras(const RasArgs &r, int max_off, hipStream_t s) {
    * helper waves, otherwise two rows per workgroup */
   const int n = r.first.n_rows;
   const int rpw = n <= WR_SPREAD_ROWS ? 1 : WR / 2;
-  hipLaunchKernelGGL((k_ras<CPT, BF16>), dim3((unsigned)((n + rpw - 1) / rpw)), dim3(WAVE * WR), 0, s, r,
-                     rpw == 1 ? 1 : 0);
+  hipLaunchKernelGGL((k_ras<CPT, BF16>), dim3((unsigned)((n + rpw - 1) / rpw)), dim3(WAVE * WR), 0, s,
+                     D3S_RAS_HOT_ARGS(r, rpw == 1 ? 1 : 0), r);
   return true;
 }
 
 bool launch_ras(const RasArgs &r, Dtype dt, hipStream_t s) {
   if (r.first.k > KF || r.retry.k > KF) return false;
+  /* what k_ras takes as given (its leading arguments carry the rest) */
+  if (r.first.temperature || r.retry.temperature || r.first.banned || r.retry.banned || r.first.flags ||
+      r.retry.flags || r.first.logits != r.retry.logits || r.first.row_stride != r.retry.row_stride ||
+      r.first.vocab != r.retry.vocab || r.first.n_rows != r.retry.n_rows)
+    return false;
   const SampleArgs &a = r.first;
   const int es = dt == DT_F32 ? 4 : 2;
   const bool aligned = ((uintptr_t)a.logits % 16u) == 0u && (a.row_stride * es) % 16 == 0;
