@@ -1319,7 +1319,8 @@ __device__ __forceinline__ bool topp_ids_row(const SampleArgs &a, const int row,
  * or the full path) filed for k_topp_redo */
 template <int EPT, bool BF16, int TBLOCK>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids_waves(EPT, TBLOCK)))) void k_topp_ids(
-    SampleArgs a, ToppRedo rd) {
+    D3S_HOT_PARAMS, SampleArgs a, ToppRedo rd) {
+  D3S_HOT_APPLY(a);
   D3S_TOPP_SHARED
   __shared__ uint64_t gsum_s[TBLOCK + 2]; /* the group sums (entry TBLOCK: the -inf bucket's group) */
   const int row = (int)blockIdx.x;
@@ -1338,9 +1339,12 @@ __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(topp_ids
  * the two paths' arrays. */
 template <int EPT, bool BF16, int TBLOCK>
 __global__ __launch_bounds__(TBLOCK) __attribute__((amdgpu_waves_per_eu(2))) void k_topp_redo(
-    SampleArgs a, ToppRedo rd) {
+    uint32_t *hot_count, SampleArgs a, ToppRedo rd) {
   D3S_TOPP_SHARED
   __shared__ uint64_t gsum_s[TBLOCK + 2]; /* the group sums (entry TBLOCK: the -inf bucket's group) */
+  /* rd.count again as a leading (preloaded) argument: the count's load
+   * issues without waiting for the kernarg segment */
+  rd.count = hot_count;
   const uint32_t n = __hip_atomic_load(rd.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   /* every workgroup reads the same count (nothing changes it before the
    * last arrival below); none filed: the counts are zero already, and no
@@ -1388,11 +1392,12 @@ bool try_topp(const SampleArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
       rd.count = (uint32_t *)ws;
       rd.done = (uint32_t *)((char *)ws + 128);
       rd.rows = (int32_t *)((char *)ws + split_counter_bytes());
-      hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), arrays, s, a, rd);
+      hipLaunchKernelGGL((k_topp_ids<EPT, BF16, TBLOCK>), dim3(a.n_rows), dim3(TBLOCK), arrays, s,
+                         D3S_HOT_ARGS(a), a, rd);
       /* (every row filed under FLAG_EXACT_LSE: a workgroup each) */
       const int grid = a.n_rows < TOPP_REDO_WG || (a.flags & FLAG_EXACT_LSE) ? a.n_rows : TOPP_REDO_WG;
       hipLaunchKernelGGL((k_topp_redo<EPT, BF16, TBLOCK>), dim3(grid), dim3(TBLOCK), ranked > arrays ? ranked : arrays,
-                         s, a, rd);
+                         s, rd.count, a, rd);
       return true;
     }
   }
