@@ -749,7 +749,11 @@ constexpr int row_occupancy() {
 constexpr int LIN_WAVES = 4;
 constexpr int LIN_PER_WG = 2 * LIN_WAVES; /* logits per workgroup */
 
-__global__ __launch_bounds__(WAVE *LIN_WAVES) void k_linear(LinearArgs la) {
+/* LinearArgs's fields as scalar arguments, so all of them are preloaded into
+ * SGPRs (9) and the gemv's first loads wait on no kernarg read */
+__global__ __launch_bounds__(WAVE *LIN_WAVES) void k_linear(const uint16_t *x, const uint16_t *w, int K, int V,
+                                                           int n_rows, uint16_t *y) {
+  const LinearArgs la{x, w, K, V, n_rows, y};
   const int n = (int)blockIdx.y;
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
   const int lane = lane_id(), hl = lane & 31;
@@ -1317,7 +1321,8 @@ void launch_ras_select(const RasArgs &r, const int32_t *first, const int32_t *re
 
 void launch_linear(const LinearArgs &la, hipStream_t s) {
   const unsigned groups = (unsigned)((la.V + LIN_PER_WG - 1) / LIN_PER_WG);
-  hipLaunchKernelGGL(k_linear, dim3(groups, (unsigned)la.n_rows), dim3(WAVE * LIN_WAVES), 0, s, la);
+  hipLaunchKernelGGL(k_linear, dim3(groups, (unsigned)la.n_rows), dim3(WAVE * LIN_WAVES), 0, s, la.x, la.w, la.K,
+                     la.V, la.n_rows, la.y);
 }
 
 int wide_max_vocab(Dtype dt) { return dt == DT_F32 ? wide_vmax<19, false>() : wide_vmax<19, true>(); }
