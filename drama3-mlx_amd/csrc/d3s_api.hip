@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <map>
+#include <memory>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -40,7 +41,27 @@ std::map<Key, Block> g_ws;
  * before it grew and still be enqueueing on it, so they are kept until the
  * stream's block is released */
 std::map<Key, std::vector<void *>> g_retired;
+/* one lock per key, never freed (a stream handle reused later takes it again) */
+std::map<Key, std::unique_ptr<std::recursive_mutex>> g_call_locks;
 }  // namespace
+
+/* Held by a call that uses the stream's workspace block while it enqueues:
+ * a call is several launches that keep their state in the block (the
+ * sorting kernels' keys, the segmented kernel's records), so the launches
+ * of two calls on one stream from different host threads must not
+ * interleave.  (Recursive: a call may make another through the C-ABI.) */
+std::unique_lock<std::recursive_mutex> stream_call_lock(hipStream_t s) {
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  std::recursive_mutex *m = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    std::unique_ptr<std::recursive_mutex> &p = g_call_locks[Key{dev, (uintptr_t)s}];
+    if (!p) p = std::make_unique<std::recursive_mutex>();
+    m = p.get();
+  }
+  return std::unique_lock<std::recursive_mutex>(*m);
+}
 
 void *stream_workspace(hipStream_t s, size_t bytes) {
   int dev = 0;
@@ -511,6 +532,7 @@ int d3s_sample(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int
                float temperature_scalar, float top_p_scalar, const int32_t *banned,
                int32_t *ids, float *probs, int32_t *cand, uint32_t *counters, unsigned flags,
                void *stream) {
+  const auto lock = d3s::stream_call_lock((hipStream_t)stream);
   return sample_call(logits, dtype, n_rows, vocab, row_stride, u, k, temperature, top_p, temperature_scalar,
                      top_p_scalar, banned, ids, probs, cand, counters, flags, stream, WsMode::Stream);
 }
@@ -566,7 +588,10 @@ int d3s_workspace_init(void *workspace, int64_t bytes, void *stream) {
   return launched();
 }
 
-int d3s_stream_workspace_release(void *stream) { return d3s::release_stream_workspace((hipStream_t)stream); }
+int d3s_stream_workspace_release(void *stream) {
+  const auto lock = d3s::stream_call_lock((hipStream_t)stream); /* no call mid-enqueue on the block */
+  return d3s::release_stream_workspace((hipStream_t)stream);
+}
 
 int d3s_sample_noalloc(const void *logits, int dtype, int64_t n_rows, int64_t vocab, int64_t row_stride,
                        const float *u, int k, const float *temperature, const float *top_p,
@@ -581,6 +606,7 @@ int d3s_sample_ras(const void *logits, int dtype, int64_t n_rows, int64_t vocab,
                    const float *u, const float *u_retry, const int32_t *history, int history_len,
                    const d3s_ras_params *params, int32_t *main_tok, int32_t *code0,
                    int32_t *first_idx, int32_t *retry_idx, uint32_t *counters, void *stream) {
+  const auto lock = d3s::stream_call_lock((hipStream_t)stream);
   return ras_call(logits, dtype, n_rows, vocab, row_stride, u, u_retry, history, history_len, params, main_tok,
                   code0, first_idx, retry_idx, counters, stream, WsMode::Stream);
 }
@@ -628,6 +654,7 @@ int d3s_linear_sample_bf16(const uint16_t *x, const uint16_t *w, int64_t n_rows,
                            uint16_t *y, const float *u, int k, const float *temperature, const float *top_p,
                            float temperature_scalar, float top_p_scalar, int32_t *ids, float *probs,
                            int32_t *cand, uint32_t *counters, unsigned flags, void *stream) {
+  const auto lock = d3s::stream_call_lock((hipStream_t)stream);
   return linear_sample_call(x, w, n_rows, K, V, y, u, k, temperature, top_p, temperature_scalar, top_p_scalar, ids,
                             probs, cand, counters, flags, stream, WsMode::Stream);
 }

@@ -23,7 +23,10 @@
  * d3s_linear_sample_bf16) are a convenience that takes the workspace from a
  * block the library keeps per (device, stream), allocated on the stream's
  * first call that needs one (the NULL stream is one such stream for every
- * thread); d3s_stream_workspace_release frees a stream's block.
+ * thread); d3s_stream_workspace_release frees a stream's block.  Such calls
+ * on one stream from several host threads each enqueue all their launches
+ * before the next one starts (a lock per (device, stream)): their launches
+ * never interleave on the block.
  * d3s_sample_noalloc never allocates either: its workspace is one fixed block
  * of static device memory per GPU.
  */
